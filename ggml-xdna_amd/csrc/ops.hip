@@ -1,0 +1,270 @@
+// The small fp32 ops between the matmuls (piece::run_rows,
+// src/xdna-exec.cpp:253-346), as HBM-bound row kernels. RMS_NORM (+ the scale
+// row MUL after it) and the GLUs can also write the next matmul's packed bfp16
+// input directly, so a normalised or gated row goes HBM -> registers ->
+// packed operand without a round trip through an fp32 tensor.
+#include "zest_common.h"
+#include "zest_device.h"
+
+namespace {
+
+using zest::encode8;
+
+// Writes 16 values of packed row r, columns [col, col+16) (col % 16 == 0).
+__device__ inline void pack16(uint8_t * packed, int64_t R_pad, int64_t r, int64_t col, const float v[16]) {
+    uint4 m;
+    const uint32_t e0 = encode8(v, m.x, m.y);
+    const uint32_t e1 = encode8(v + 8, m.z, m.w);
+    uint8_t * tile = packed + zest_tile_offset(r / ZEST_TILE_ROWS, col / ZEST_TILE_K, R_pad);
+    const int64_t rr = r % ZEST_TILE_ROWS, q = (col % ZEST_TILE_K) / 16;
+    *reinterpret_cast<uint4 *>(tile + rr * ZEST_TILE_K + q * 16) = m;
+    *reinterpret_cast<uint16_t *>(tile + ZEST_TILE_MANT + rr * 8 + q * 2) = (uint16_t) (e0 | (e1 << 8));
+}
+
+__device__ inline void load16(const float * p, float v[16], int64_t valid) {
+    if (valid >= 16 && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 q = reinterpret_cast<const float4 *>(p)[i];
+            v[4 * i] = q.x;
+            v[4 * i + 1] = q.y;
+            v[4 * i + 2] = q.z;
+            v[4 * i + 3] = q.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[i] = i < valid ? p[i] : 0.0f;
+    }
+}
+
+__device__ inline void store16(float * p, const float v[16], int64_t valid) {
+    if (valid >= 16 && (reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            reinterpret_cast<float4 *>(p)[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            if (i < valid) p[i] = v[i];
+    }
+}
+
+constexpr int NORM_THREADS = 256;
+constexpr int NORM_UNITS = 4;  // 16-column units per thread: rows up to 16384 wide
+
+// One workgroup per row: sum of squares (fp32), sc = 1/sqrt(ss/d + eps),
+// y = x * sc (* w). Units of 16 columns stay in registers between the two
+// passes. Writes y and/or the packed row, including the zero blocks of the
+// K padding when d % 64 != 0.
+__global__ __launch_bounds__(NORM_THREADS) void rms_norm_kernel(const float * __restrict__ x, int64_t d, float eps,
+                                                                const float * __restrict__ w, float * __restrict__ y,
+                                                                uint8_t * __restrict__ packed, int64_t R_pad) {
+    const int64_t r = blockIdx.x;
+    const float * xr = x + r * d;
+    const int64_t units = (d + 15) / 16, d_pad = zest_k_padded(d);
+    float v[NORM_UNITS][16];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NORM_UNITS; k++) {
+        const int64_t u = threadIdx.x + (int64_t) k * NORM_THREADS;
+        if (u < units) {
+            load16(xr + u * 16, v[k], d - u * 16);
+#pragma unroll
+            for (int i = 0; i < 16; i++) ss += v[k][i] * v[k][i];
+        }
+    }
+    __shared__ float part[NORM_THREADS / 64];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NORM_THREADS / 64; i++) tot += part[i];
+    const float sc = 1.0f / sqrtf(tot / (float) d + eps);
+#pragma unroll
+    for (int k = 0; k < NORM_UNITS; k++) {
+        const int64_t u = threadIdx.x + (int64_t) k * NORM_THREADS;
+        if (u < units) {
+            float o[16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int64_t j = u * 16 + i;
+                o[i] = j < d ? v[k][i] * sc : 0.0f;
+                if (w && j < d) o[i] *= w[j];
+            }
+            if (y) store16(y + r * d + u * 16, o, d - u * 16);
+            if (packed) pack16(packed, R_pad, r, u * 16, o);
+        } else if (packed && u * 16 < d_pad) {
+            float z[16] = {};
+            pack16(packed, R_pad, r, u * 16, z);
+        }
+    }
+}
+
+__device__ inline float act(int kind, float g) {
+    switch (kind) {
+        case ZEST_GLU_SWIGLU: return g / (1.0f + expf(-g));
+        case ZEST_GLU_GEGLU: return 0.5f * g * (1.0f + tanhf(0.7978845608f * g * (1.0f + 0.044715f * g * g)));
+        case ZEST_GLU_GEGLU_ERF: return 0.5f * g * (1.0f + erff(g * 0.7071067812f));
+        case ZEST_GLU_GEGLU_QUICK: return g / (1.0f + expf(-1.702f * g));
+        default: return g > 0.0f ? g : 0.0f;
+    }
+}
+
+// One thread per 16 outputs of one row: y = act(g) * u (REGLU as g > 0 ? g*u : 0).
+template <int KIND>
+__global__ __launch_bounds__(256) void glu_kernel(const float * __restrict__ g, int64_t sg, const float * __restrict__ u,
+                                                  int64_t su, int64_t rows, int64_t f, float * __restrict__ y,
+                                                  uint8_t * __restrict__ packed, int64_t R_pad) {
+    const int64_t units = zest_k_padded(f) / 16;
+    const int64_t idx = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= rows * units) return;
+    const int64_t r = idx / units, c = (idx % units) * 16;
+    float o[16];
+    if (c < f) {
+        float gv[16], uv[16];
+        load16(g + r * sg + c, gv, f - c);
+        load16(u + r * su + c, uv, f - c);
+#pragma unroll
+        for (int i = 0; i < 16; i++) o[i] = (KIND == ZEST_GLU_REGLU) ? (gv[i] > 0.0f ? gv[i] * uv[i] : 0.0f)
+                                                                     : act(KIND, gv[i]) * uv[i];
+        if (y) store16(y + r * f + c, o, f - c);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) o[i] = 0.0f;
+    }
+    if (packed) {
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            if (c + i >= f) o[i] = 0.0f;
+        pack16(packed, R_pad, r, c, o);
+    }
+}
+
+__global__ __launch_bounds__(256) void add_kernel(const float * __restrict__ a, const float * __restrict__ b,
+                                                  int64_t n, int64_t d, int b_row, float * __restrict__ y) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    y[i] = a[i] + (b_row ? b[i % d] : b[i]);
+}
+
+__global__ __launch_bounds__(256) void mul_row_kernel(const float * __restrict__ x, const float * __restrict__ w,
+                                                      int64_t n, int64_t d, float * __restrict__ y) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    y[i] = x[i] * w[i % d];
+}
+
+__global__ __launch_bounds__(256) void scale_kernel(const float * __restrict__ x, int64_t n, float s, float b,
+                                                    float * __restrict__ y) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    y[i] = x[i] * s + b;
+}
+
+// ROPE: one workgroup per (token, head); thread p < n_dims/2 owns pair p.
+// theta for pair p is pos * theta_scale^p built by p float multiplications,
+// as the reference's table loop does (src/xdna-exec.cpp:225-233); the
+// rotation of :326-339; dimensions past n_dims copied.
+__global__ __launch_bounds__(256) void rope_kernel(const float * __restrict__ x, int64_t heads, int64_t d,
+                                                   const int32_t * __restrict__ pos, const float * __restrict__ ff,
+                                                   int n_dims, int neox, float theta_scale, float freq_scale,
+                                                   float ext_factor, float attn_factor, float corr0, float corr1,
+                                                   float * __restrict__ y) {
+    const int64_t t = blockIdx.x / heads, h = blockIdx.x % heads;
+    const float * src = x + (t * heads + h) * d;
+    float * dst = y + (t * heads + h) * d;
+    for (int p = threadIdx.x; p < n_dims / 2; p += blockDim.x) {
+        float theta = (float) pos[t];
+        for (int i = 0; i < p; i++) theta *= theta_scale;
+        const float theta_extrap = ff ? theta / ff[p] : theta;
+        float th = freq_scale * theta_extrap, mscale = attn_factor;
+        if (ext_factor != 0.0f) {
+            const float yv = ((float) p - corr0) / fmaxf(0.001f, corr1 - corr0);
+            const float ramp_mix = (1.0f - fminf(1.0f, fmaxf(0.0f, yv))) * ext_factor;
+            th = th * (1.0f - ramp_mix) + theta_extrap * ramp_mix;
+            mscale *= 1.0f + 0.1f * logf(1.0f / freq_scale);
+        }
+        const float c = cosf(th) * mscale, sn = sinf(th) * mscale;
+        const int64_t ic = neox ? p : 2 * p, off = neox ? n_dims / 2 : 1;
+        const float x0 = src[ic], x1 = src[ic + off];
+        dst[ic] = x0 * c - x1 * sn;
+        dst[ic + off] = x0 * sn + x1 * c;
+    }
+    for (int64_t i = n_dims + threadIdx.x; i < d; i += blockDim.x) dst[i] = src[i];
+}
+
+unsigned blocks_for(int64_t n, int per) { return (unsigned) ((n + per - 1) / per); }
+
+} // namespace
+
+extern "C" {
+
+int zest_rms_norm(const float * x, int64_t rows, int64_t d, float eps, const float * w, float * y, void * packed,
+                  void * stream) {
+    ZEST_REQUIRE(x && (y || packed), "zest_rms_norm: null pointer");
+    ZEST_REQUIRE(rows > 0 && d > 0, "zest_rms_norm: rows=%lld d=%lld", (long long) rows, (long long) d);
+    ZEST_REQUIRE((d + 15) / 16 <= (int64_t) NORM_UNITS * NORM_THREADS, "zest_rms_norm: rows of %lld are too wide",
+                 (long long) d);
+    ZEST_REQUIRE(!packed || d % 8 == 0, "zest_rms_norm: packing needs d %% 8 == 0");
+    hipLaunchKernelGGL(rms_norm_kernel, dim3((unsigned) rows), dim3(NORM_THREADS), 0, zest::as_stream(stream), x, d,
+                       eps, w, y, (uint8_t *) packed, zest_rows_padded(rows));
+    return zest::check_launch("zest_rms_norm");
+}
+
+int zest_glu(int kind, const float * g, int64_t sg, const float * u, int64_t su, int64_t rows, int64_t f, float * y,
+             void * packed, void * stream) {
+    ZEST_REQUIRE(g && u && (y || packed), "zest_glu: null pointer");
+    ZEST_REQUIRE(rows > 0 && f > 0 && sg >= f && su >= f, "zest_glu: bad shape");
+    ZEST_REQUIRE(!packed || f % 8 == 0, "zest_glu: packing needs f %% 8 == 0");
+    const int64_t n = rows * (zest_k_padded(f) / 16);
+    const dim3 grid(blocks_for(n, 256));
+    hipStream_t s = zest::as_stream(stream);
+    const int64_t R_pad = zest_rows_padded(rows);
+    uint8_t * p = (uint8_t *) packed;
+    switch (kind) {
+        case ZEST_GLU_SWIGLU: hipLaunchKernelGGL(glu_kernel<ZEST_GLU_SWIGLU>, grid, dim3(256), 0, s, g, sg, u, su, rows, f, y, p, R_pad); break;
+        case ZEST_GLU_GEGLU: hipLaunchKernelGGL(glu_kernel<ZEST_GLU_GEGLU>, grid, dim3(256), 0, s, g, sg, u, su, rows, f, y, p, R_pad); break;
+        case ZEST_GLU_GEGLU_ERF: hipLaunchKernelGGL(glu_kernel<ZEST_GLU_GEGLU_ERF>, grid, dim3(256), 0, s, g, sg, u, su, rows, f, y, p, R_pad); break;
+        case ZEST_GLU_GEGLU_QUICK: hipLaunchKernelGGL(glu_kernel<ZEST_GLU_GEGLU_QUICK>, grid, dim3(256), 0, s, g, sg, u, su, rows, f, y, p, R_pad); break;
+        case ZEST_GLU_REGLU: hipLaunchKernelGGL(glu_kernel<ZEST_GLU_REGLU>, grid, dim3(256), 0, s, g, sg, u, su, rows, f, y, p, R_pad); break;
+        default: return zest::fail(ZEST_E_UNSUPPORTED, "zest_glu: GLU kind %d", kind);
+    }
+    return zest::check_launch("zest_glu");
+}
+
+int zest_add(const float * a, const float * b, int64_t rows, int64_t d, int b_is_row, float * y, void * stream) {
+    ZEST_REQUIRE(a && b && y && rows > 0 && d > 0, "zest_add: bad arguments");
+    const int64_t n = rows * d;
+    hipLaunchKernelGGL(add_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, zest::as_stream(stream), a, b, n, d, b_is_row,
+                       y);
+    return zest::check_launch("zest_add");
+}
+
+int zest_mul_row(const float * x, const float * w, int64_t rows, int64_t d, float * y, void * stream) {
+    ZEST_REQUIRE(x && w && y && rows > 0 && d > 0, "zest_mul_row: bad arguments");
+    const int64_t n = rows * d;
+    hipLaunchKernelGGL(mul_row_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, zest::as_stream(stream), x, w, n, d, y);
+    return zest::check_launch("zest_mul_row");
+}
+
+int zest_scale(const float * x, int64_t n, float s, float b, float * y, void * stream) {
+    ZEST_REQUIRE(x && y && n > 0, "zest_scale: bad arguments");
+    hipLaunchKernelGGL(scale_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, zest::as_stream(stream), x, n, s, b, y);
+    return zest::check_launch("zest_scale");
+}
+
+int zest_rope(const float * x, int64_t T, int64_t heads, int64_t d, const int32_t * pos, const float * ff, int n_dims,
+              int mode, float freq_base, float freq_scale, float ext_factor, float attn_factor, float corr0, float corr1,
+              float * y, void * stream) {
+    ZEST_REQUIRE(x && pos && y && T > 0 && heads > 0 && d > 0, "zest_rope: bad arguments");
+    ZEST_REQUIRE(n_dims > 0 && n_dims % 2 == 0 && n_dims <= d, "zest_rope: n_dims=%d d=%lld", n_dims, (long long) d);
+    ZEST_REQUIRE(mode == 0 || mode == 2, "zest_rope: mode %d (normal 0 or neox 2)", mode);
+    const float theta_scale = powf(freq_base, -2.0f / (float) n_dims);
+    hipLaunchKernelGGL(rope_kernel, dim3((unsigned) (T * heads)), dim3(64), 0, zest::as_stream(stream), x, heads, d, pos,
+                       ff, n_dims, mode == 2, theta_scale, freq_scale, ext_factor, attn_factor, corr0, corr1, y);
+    return zest::check_launch("zest_rope");
+}
+
+} // extern "C"

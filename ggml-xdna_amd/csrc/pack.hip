@@ -1,0 +1,209 @@
+// The two HBM-bound converters of the path:
+//   zest_pack_act        fp32 activations -> packed bfp16 (per chunk)
+//   zest_convert_weight  GGUF F32 / Q8_0 / Q4_K weights -> packed bfp16 (once,
+//                        into the resident weight cache)
+// Both write the tile layout of zest_layout.h with 16-byte mantissa stores.
+#include "zest_common.h"
+#include "zest_device.h"
+
+namespace {
+
+using zest::encode8;
+
+// One thread encodes two blocks (16 values) of one row: 64 bytes of fp32 in,
+// a 16-byte mantissa store and a 2-byte exponent store out. A workgroup is one
+// 16-row tile row by 256 columns (4 tiles): thread t takes row t/16 and the
+// 16-column quarter t%16. Rows past M and columns past K become zero blocks.
+__global__ __launch_bounds__(256) void pack_act_kernel(const float * __restrict__ x, int64_t M, int64_t K, int64_t ldx,
+                                                       uint8_t * __restrict__ dst, int64_t R_pad, int64_t K_pad) {
+    const int t = threadIdx.x;
+    const int64_t rt = blockIdx.y;
+    const int64_t r = rt * ZEST_TILE_ROWS + (t >> 4);
+    const int64_t col = (int64_t) blockIdx.x * 256 + (t & 15) * 16;
+    if (col >= K_pad) return;
+    float v[16];
+    const bool row_ok = r < M;
+    if (row_ok && col + 16 <= K && (ldx & 3) == 0) {
+        typedef float f32x4 __attribute__((ext_vector_type(4)));
+        const f32x4 * p = reinterpret_cast<const f32x4 *>(x + r * ldx + col);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const f32x4 q = __builtin_nontemporal_load(p + i);
+            v[4 * i] = q.x;
+            v[4 * i + 1] = q.y;
+            v[4 * i + 2] = q.z;
+            v[4 * i + 3] = q.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[i] = (row_ok && col + i < K) ? x[r * ldx + col + i] : 0.0f;
+    }
+    uint4 m;
+    const uint32_t e0 = encode8(v, m.x, m.y);
+    const uint32_t e1 = encode8(v + 8, m.z, m.w);
+    uint8_t * tile = dst + zest_tile_offset(rt, col / ZEST_TILE_K, R_pad);
+    const int rr = t >> 4, q = (t & 15) & 3;
+    *reinterpret_cast<uint4 *>(tile + rr * ZEST_TILE_K + q * 16) = m;
+    *reinterpret_cast<uint16_t *>(tile + ZEST_TILE_MANT + rr * 8 + q * 2) = (uint16_t) (e0 | (e1 << 8));
+}
+
+__device__ inline float half_to_float(uint16_t h) { return (float) __builtin_bit_cast(_Float16, h); }
+
+// Q8_0: 34-byte blocks of fp16 d + 32 int8; y = d * q, exact in fp32. One
+// thread takes one GGUF block = half a tile row: 32 mantissa bytes (two
+// 16-byte stores) and four exponent bytes. Workgroup: 8 rows x 32 blocks.
+__global__ __launch_bounds__(256) void convert_q8_0_kernel(const uint8_t * __restrict__ raw, int64_t N, int64_t K,
+                                                           uint8_t * __restrict__ dst, int64_t R_pad, int64_t K_pad) {
+    const int t = threadIdx.x;
+    const int64_t r = (int64_t) blockIdx.y * 8 + (t >> 5);
+    const int64_t jb = (int64_t) blockIdx.x * 32 + (t & 31);  // 32-column block
+    const int64_t col = jb * 32;
+    if (col >= K_pad || r >= R_pad) return;
+    uint4 m0 = make_uint4(0, 0, 0, 0), m1 = make_uint4(0, 0, 0, 0);
+    uint32_t ex = 0;
+    if (r < N && col < K) {
+        const uint8_t * b = raw + r * (K / 32 * 34) + jb * 34;
+        const uint16_t * h = reinterpret_cast<const uint16_t *>(b);  // 2-byte aligned
+        const float d = half_to_float(h[0]);
+        float v[32];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const uint16_t pair = h[1 + i];
+            v[2 * i] = (float) (int8_t) (pair & 0xff) * d;
+            v[2 * i + 1] = (float) (int8_t) (pair >> 8) * d;
+        }
+        uint32_t e[4];
+        e[0] = encode8(v, m0.x, m0.y);
+        e[1] = encode8(v + 8, m0.z, m0.w);
+        e[2] = encode8(v + 16, m1.x, m1.y);
+        e[3] = encode8(v + 24, m1.z, m1.w);
+        ex = e[0] | (e[1] << 8) | (e[2] << 16) | (e[3] << 24);
+    }
+    uint8_t * tile = dst + zest_tile_offset(r / ZEST_TILE_ROWS, col / ZEST_TILE_K, R_pad);
+    const int64_t rr = r % ZEST_TILE_ROWS, half = (col % ZEST_TILE_K) / 32;
+    uint4 * mp = reinterpret_cast<uint4 *>(tile + rr * ZEST_TILE_K + half * 32);
+    mp[0] = m0;
+    mp[1] = m1;
+    *reinterpret_cast<uint32_t *>(tile + ZEST_TILE_MANT + rr * 8 + half * 4) = ex;
+}
+
+// Q4_K: 144-byte super-blocks of 256: fp16 d, fp16 dmin, 12 bytes of 6-bit
+// (scale, min) pairs, 128 bytes of nibbles. Sub-block s (0..7) is 32 values:
+// the low (s even) or high (s odd) nibbles of qs[32*(s/2) ..+32), with pair s:
+// y = (d*sc)*q - dmin*m. The products are exact in fp32, so the one rounding
+// is the subtraction's and fma gives the same float. One thread per
+// sub-block; workgroup 8 rows x 32 sub-blocks (4 super-blocks).
+__global__ __launch_bounds__(256) void convert_q4_k_kernel(const uint8_t * __restrict__ raw, int64_t N, int64_t K,
+                                                           uint8_t * __restrict__ dst, int64_t R_pad, int64_t K_pad) {
+    const int t = threadIdx.x;
+    const int64_t r = (int64_t) blockIdx.y * 8 + (t >> 5);
+    const int64_t sb = (int64_t) blockIdx.x * 32 + (t & 31);  // 32-column sub-block
+    const int64_t col = sb * 32;
+    if (col >= K_pad || r >= R_pad) return;
+    uint4 m0 = make_uint4(0, 0, 0, 0), m1 = make_uint4(0, 0, 0, 0);
+    uint32_t ex = 0;
+    if (r < N && col < K) {
+        const uint8_t * blk = raw + r * (K / 256 * 144) + (sb / 8) * 144;
+        const int s = (int) (sb & 7);
+        const uint32_t dd = *reinterpret_cast<const uint32_t *>(blk);
+        const float d = half_to_float((uint16_t) (dd & 0xffff)), dmin = half_to_float((uint16_t) (dd >> 16));
+        const uint8_t * sc = blk + 4;
+        uint32_t scv, mv;
+        if (s < 4) {
+            scv = sc[s] & 63;
+            mv = sc[s + 4] & 63;
+        } else {
+            scv = (sc[s + 4] & 0xF) | ((sc[s - 4] >> 6) << 4);
+            mv = (sc[s + 4] >> 4) | ((sc[s] >> 6) << 4);
+        }
+        const float d1 = d * (float) scv, m1f = dmin * (float) mv;
+        const uint4 * qp = reinterpret_cast<const uint4 *>(blk + 16 + 32 * (s >> 1));
+        const uint4 qa = qp[0], qb = qp[1];
+        const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        const int shift = (s & 1) * 4;
+        float v[32];
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            const uint32_t nib = (w[i >> 2] >> ((i & 3) * 8 + shift)) & 0xF;
+            v[i] = fmaf(d1, (float) nib, -m1f);
+        }
+        uint32_t e[4];
+        e[0] = encode8(v, m0.x, m0.y);
+        e[1] = encode8(v + 8, m0.z, m0.w);
+        e[2] = encode8(v + 16, m1.x, m1.y);
+        e[3] = encode8(v + 24, m1.z, m1.w);
+        ex = e[0] | (e[1] << 8) | (e[2] << 16) | (e[3] << 24);
+    }
+    uint8_t * tile = dst + zest_tile_offset(r / ZEST_TILE_ROWS, col / ZEST_TILE_K, R_pad);
+    const int64_t rr = r % ZEST_TILE_ROWS, half = (col % ZEST_TILE_K) / 32;
+    uint4 * mp = reinterpret_cast<uint4 *>(tile + rr * ZEST_TILE_K + half * 32);
+    mp[0] = m0;
+    mp[1] = m1;
+    *reinterpret_cast<uint32_t *>(tile + ZEST_TILE_MANT + rr * 8 + half * 4) = ex;
+}
+
+bool aligned(const void * p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+} // namespace
+
+extern "C" {
+
+int64_t zest_rows_pad(int64_t rows) { return zest_rows_padded(rows); }
+int64_t zest_k_pad(int64_t K) { return zest_k_padded(K); }
+size_t zest_bfp16_bytes(int64_t rows, int64_t K) {
+    return (size_t) (zest_rows_padded(rows) * zest_k_padded(K) / 8 * 9);
+}
+
+size_t zest_raw_row_bytes(int type, int64_t K) {
+    switch (type) {
+        case ZEST_TYPE_F32: return (size_t) K * 4;
+        case ZEST_TYPE_Q8_0: return K % 32 ? 0 : (size_t) (K / 32) * 34;
+        case ZEST_TYPE_Q4_K: return K % 256 ? 0 : (size_t) (K / 256) * 144;
+        default: return 0;
+    }
+}
+
+int zest_pack_act(const float * x, int64_t M, int64_t K, int64_t ldx, void * dst, void * stream) {
+    ZEST_REQUIRE(x && dst, "zest_pack_act: null pointer");
+    ZEST_REQUIRE(M > 0 && K > 0 && K % 8 == 0, "zest_pack_act: M=%lld K=%lld (K must be a positive multiple of 8)",
+                 (long long) M, (long long) K);
+    ZEST_REQUIRE(ldx >= K, "zest_pack_act: row stride %lld < K %lld", (long long) ldx, (long long) K);
+    ZEST_REQUIRE(aligned(x, 16) && aligned(dst, 16), "zest_pack_act: pointers must be 16-byte aligned");
+    const int64_t R_pad = zest_rows_padded(M), K_pad = zest_k_padded(K);
+    const dim3 grid((unsigned) ((K_pad + 255) / 256), (unsigned) (R_pad / ZEST_TILE_ROWS));
+    hipLaunchKernelGGL(pack_act_kernel, grid, dim3(256), 0, zest::as_stream(stream), x, M, K, ldx, (uint8_t *) dst,
+                       R_pad, K_pad);
+    return zest::check_launch("zest_pack_act");
+}
+
+int zest_convert_weight(int type, const void * raw, int64_t N, int64_t K, void * dst, void * stream) {
+    ZEST_REQUIRE(raw && dst, "zest_convert_weight: null pointer");
+    ZEST_REQUIRE(N > 0 && K > 0 && K % 8 == 0, "zest_convert_weight: N=%lld K=%lld", (long long) N, (long long) K);
+    ZEST_REQUIRE(aligned(dst, 16), "zest_convert_weight: dst must be 16-byte aligned");
+    const int64_t R_pad = zest_rows_padded(N), K_pad = zest_k_padded(K);
+    hipStream_t s = zest::as_stream(stream);
+    switch (type) {
+        case ZEST_TYPE_F32:
+            return zest_pack_act((const float *) raw, N, K, K, dst, stream);
+        case ZEST_TYPE_Q8_0: {
+            ZEST_REQUIRE(K % 32 == 0, "zest_convert_weight: Q8_0 needs K %% 32 == 0 (K=%lld)", (long long) K);
+            ZEST_REQUIRE(aligned(raw, 2), "zest_convert_weight: Q8_0 rows must be 2-byte aligned");
+            const dim3 grid((unsigned) ((K_pad / 32 + 31) / 32), (unsigned) (R_pad / 8));
+            hipLaunchKernelGGL(convert_q8_0_kernel, grid, dim3(256), 0, s, (const uint8_t *) raw, N, K, (uint8_t *) dst,
+                               R_pad, K_pad);
+            return zest::check_launch("zest_convert_weight(Q8_0)");
+        }
+        case ZEST_TYPE_Q4_K: {
+            ZEST_REQUIRE(K % 256 == 0, "zest_convert_weight: Q4_K needs K %% 256 == 0 (K=%lld)", (long long) K);
+            ZEST_REQUIRE(aligned(raw, 16), "zest_convert_weight: Q4_K rows must be 16-byte aligned");
+            const dim3 grid((unsigned) ((K_pad / 32 + 31) / 32), (unsigned) (R_pad / 8));
+            hipLaunchKernelGGL(convert_q4_k_kernel, grid, dim3(256), 0, s, (const uint8_t *) raw, N, K, (uint8_t *) dst,
+                               R_pad, K_pad);
+            return zest::check_launch("zest_convert_weight(Q4_K)");
+        }
+        default:
+            return zest::fail(ZEST_E_UNSUPPORTED, "zest_convert_weight: weight type %d has no converter", type);
+    }
+}
+
+} // extern "C"

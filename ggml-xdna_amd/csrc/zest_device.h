@@ -1,0 +1,77 @@
+// Device helpers shared by the kernels: the bfp16 block encoder and the
+// lossless bfp16 -> bf16 expansion.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "zest_layout.h"
+
+namespace zest {
+
+// One block of eight floats -> exponent byte (returned) and eight mantissa
+// bytes (m0 = bytes 0..3, m1 = bytes 4..7). The reference's arithmetic
+// (src/npu/bfp16_pack.cpp:85-127): e = the largest biased exponent field;
+// q = RNE(x * 2^(133 - e)) saturated to [-128, 127]. ldexp is exact here
+// (|x * 2^(133-e)| < 128, and anything it would round in underflow is below
+// one half), rint rounds to nearest even, and med3 saturates.
+__device__ inline uint32_t encode8(const float v[8], uint32_t & m0, uint32_t & m1) {
+    uint32_t e = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) e = max(e, (__float_as_uint(v[i]) >> 23) & 0xffu);
+    const int sh = 133 - (int) e;
+    uint32_t b[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float q = __builtin_amdgcn_fmed3f(__builtin_rintf(__builtin_ldexpf(v[i], sh)), -128.0f, 127.0f);
+        b[i] = (uint32_t) (int32_t) q & 0xffu;
+    }
+    m0 = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+    m1 = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+    return e;
+}
+
+// 2^(e - 133) as a float: normal for e >= 7, subnormal below.
+__device__ inline float block_scale(uint32_t e) {
+    return e >= 7u ? __uint_as_float((e - 6u) << 23) : __uint_as_float(1u << (e + 16u));
+}
+
+// Eight mantissas (two dwords) with one exponent -> eight bf16 (four dwords),
+// each exactly the decoded value q * 2^(e-133) (bfp16_decode_block,
+// src/npu/bfp16_pack.cpp:129-144). A signed 8-bit mantissa times a power of
+// two has at most 8 significant bits, so it is exact in bf16; the bf16 is the
+// top half of the exact float (whose low half is zero).
+//
+// For exponent bytes 7..253 (every block of realistic data) 2^(e-133) and
+// 128 * 2^(e-133) are normal floats: each byte is read unsigned after
+// flipping its sign bit (u = q + 128) and fma(u, s, -128 s) = q * s exactly,
+// two VALU ops per value. The other bytes (zero and tiny blocks, 0..6; the
+// top of the float range, 254..255) take the plain q * s, where fp32
+// rounding of the product gives what the reference's decode gives.
+__device__ inline void expand8(uint32_t w0, uint32_t w1, uint32_t e, uint32_t out[4]) {
+    const float s = block_scale(e);
+    float f[8];
+    if (__builtin_expect(e - 7u < 247u, 1)) {
+        const float off = -128.0f * s;
+        const uint32_t u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;
+        f[0] = fmaf((float) (u0 & 0xffu), s, off);
+        f[1] = fmaf((float) ((u0 >> 8) & 0xffu), s, off);
+        f[2] = fmaf((float) ((u0 >> 16) & 0xffu), s, off);
+        f[3] = fmaf((float) (u0 >> 24), s, off);
+        f[4] = fmaf((float) (u1 & 0xffu), s, off);
+        f[5] = fmaf((float) ((u1 >> 8) & 0xffu), s, off);
+        f[6] = fmaf((float) ((u1 >> 16) & 0xffu), s, off);
+        f[7] = fmaf((float) (u1 >> 24), s, off);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            f[i] = (float) (int8_t) (w0 >> (8 * i)) * s;
+            f[4 + i] = (float) (int8_t) (w1 >> (8 * i)) * s;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        out[i] = __builtin_amdgcn_perm(__float_as_uint(f[2 * i + 1]), __float_as_uint(f[2 * i]), 0x07060302u);
+}
+
+} // namespace zest

@@ -1,0 +1,171 @@
+"""Synthetic decoder-stack workloads of the prefill MUL_MAT path (the
+BASELINE configurations), run through the C ABI on one GPU.
+
+A layer, for one chunk of M tokens with residual stream h [M][H] (fp32):
+    RMS_NORM(h) * w_attn   -> packed (fused)        xdna-exec's norm -> q/k/v piece
+    Q, K, V = GEMM(packed, Wq / Wk / Wv)
+    (attention is excluded; the O projection's input is a stand-in: Q's output)
+    pack(Q) ; O = GEMM(., Wo) ; h = h + O
+    RMS_NORM(h) * w_ffn    -> packed (fused)
+    G, U = GEMM(packed, Wgate / Wup)
+    SiLU(G) * U            -> packed (fused)        the down projection's input
+    D = GEMM(., Wdown) ; h = h + D
+Weights are random-init N(0, 0.02), quantised to GGUF on the GPU, converted
+once into the resident bfp16 cache (timed separately, as the reference
+reports warm prefill with its one-time copy build apart).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import ggml_xdna_amd as z
+from ggml_xdna_amd import quant
+
+BF16_PEAK_TFLOPS = 2516.6  # MI355X dense bf16 MFMA: 256 CU x 2.4 GHz x 4096 FLOP/clk
+HBM_PEAK_GBS = 8000.0
+
+
+@dataclass
+class StackConfig:
+    name: str
+    layers: int
+    hidden: int
+    q: int
+    kv: int
+    ffn: int
+    qkv_type: int     # GGUF type of Q/K/V (and gate/up)
+    o_type: int
+    ffn_type: int     # gate/up
+    down_type: int
+    tokens: int       # prompt length
+    chunk: int        # tokens per chunk
+    outlier_frac: float = 0.0
+    outlier_scale: float = 1.0
+
+    def matmuls(self):
+        """(name, N, K, type) of one layer's weights."""
+        return [("attn_q", self.q, self.hidden, self.qkv_type), ("attn_k", self.kv, self.hidden, self.qkv_type),
+                ("attn_v", self.kv, self.hidden, self.qkv_type), ("attn_output", self.hidden, self.q, self.o_type),
+                ("ffn_gate", self.ffn, self.hidden, self.ffn_type), ("ffn_up", self.ffn, self.hidden, self.ffn_type),
+                ("ffn_down", self.hidden, self.ffn, self.down_type)]
+
+    def flops_per_token(self) -> float:
+        return 2.0 * sum(n * k for _, n, k, _ in self.matmuls()) * self.layers
+
+
+CONFIGS = {
+    # Qwen3-4B-shaped, 36 layers, 8192 tokens in 2048-token chunks
+    "qwen3-4b": StackConfig("qwen3-4b", 36, 2560, 4096, 1024, 9728, z.TYPE_Q4_K, z.TYPE_Q8_0, z.TYPE_Q4_K,
+                            z.TYPE_Q8_0, 8192, 2048),
+    # hidden 1024, 16 layers, Q8_0, chunk swept by the caller
+    "small-1024": StackConfig("small-1024", 16, 1024, 1024, 1024, 4096, z.TYPE_Q8_0, z.TYPE_Q8_0, z.TYPE_Q8_0,
+                              z.TYPE_Q8_0, 4096, 4096),
+    # 27B-class, 64 layers, all Q4_K, one 4096-token chunk, 0.5% outliers x30
+    "dense-27b": StackConfig("dense-27b", 64, 5120, 6144, 1024, 17408, z.TYPE_Q4_K, z.TYPE_Q4_K, z.TYPE_Q4_K,
+                             z.TYPE_Q4_K, 4096, 4096, 0.005, 30.0),
+}
+
+
+@dataclass
+class Layer:
+    w: dict = field(default_factory=dict)      # name -> packed bfp16 cache entry
+    attn_norm: object = None
+    ffn_norm: object = None
+
+
+class Stack:
+    """Weights resident in HBM plus per-chunk work buffers."""
+
+    def __init__(self, cfg: StackConfig, seed: int = 0, device: str = "cuda"):
+        import torch
+        self.cfg, self.device = cfg, device
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        self.layers: list[Layer] = []
+        self.convert_bytes = 0.0   # algorithmic bytes of the one-time conversion
+        self.convert_ms = 0.0
+        raw_by_shape = {}
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for li in range(cfg.layers):
+            L = Layer()
+            for name, n, k, t in cfg.matmuls():
+                key = (name, n, k, t)
+                # distinct random weights per shape; layers share the GGUF source bytes
+                # (values do not change the work) but each gets its own cache entry
+                if key not in raw_by_shape:
+                    w = torch.randn((n, k), generator=g, device=device) * 0.02
+                    raw_by_shape[key] = quant.quantize(t, w)
+                    del w
+                raw = raw_by_shape[key]
+                ev0.record()
+                L.w[name] = z.convert_weight(t, raw, n, k)
+                ev1.record()
+                ev1.synchronize()
+                self.convert_ms += ev0.elapsed_time(ev1)
+                self.convert_bytes += raw.numel() + n * k * 9 / 8
+            L.attn_norm = 1.0 + 0.1 * torch.randn(cfg.hidden, generator=g, device=device)
+            L.ffn_norm = 1.0 + 0.1 * torch.randn(cfg.hidden, generator=g, device=device)
+            self.layers.append(L)
+        del raw_by_shape
+        self.chunk = cfg.chunk
+        self._alloc(cfg.chunk)
+        x = torch.randn((cfg.tokens, cfg.hidden), generator=g, device=device)
+        if cfg.outlier_frac > 0:
+            nout = max(1, int(cfg.hidden * cfg.outlier_frac))
+            ch = torch.randperm(cfg.hidden, generator=g, device=device)[:nout]
+            x[:, ch] *= cfg.outlier_scale
+        self.x = x
+
+    def _alloc(self, m: int):
+        import torch
+        c, dev = self.cfg, self.device
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.h = torch.empty((m, c.hidden), **f32)
+        self.qo = torch.empty((m, c.q), **f32)
+        self.ko = torch.empty((m, c.kv), **f32)
+        self.vo = torch.empty((m, c.kv), **f32)
+        self.oo = torch.empty((m, c.hidden), **f32)
+        self.go = torch.empty((m, c.ffn), **f32)
+        self.uo = torch.empty((m, c.ffn), **f32)
+        self.do = torch.empty((m, c.hidden), **f32)
+        self.pa = z.empty_packed(m, c.hidden, dev)
+        self.po = z.empty_packed(m, c.q, dev)
+        self.pd = z.empty_packed(m, c.ffn, dev)
+
+    def run_chunk(self, x_chunk, gemm_events=None):
+        """One chunk through every layer. gemm_events: a list to which
+        (start, end, flops) event pairs around each GEMM are appended."""
+        import torch
+        c, m = self.cfg, x_chunk.shape[0]
+        eps = 1e-6
+        self.h.copy_(x_chunk)
+
+        def gemm(a, wname, L, n, k, out):
+            if gemm_events is not None:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                z.gemm(a, m, L.w[wname], n, k, out=out)
+                e1.record()
+                gemm_events.append((e0, e1, 2.0 * m * n * k))
+            else:
+                z.gemm(a, m, L.w[wname], n, k, out=out)
+
+        for L in self.layers:
+            z.rms_norm(self.h, eps, L.attn_norm, y=None, packed=self.pa)
+            gemm(self.pa, "attn_q", L, c.q, c.hidden, self.qo)
+            gemm(self.pa, "attn_k", L, c.kv, c.hidden, self.ko)
+            gemm(self.pa, "attn_v", L, c.kv, c.hidden, self.vo)
+            z.pack_act(self.qo, out=self.po)
+            gemm(self.po, "attn_output", L, c.hidden, c.q, self.oo)
+            z.add(self.h, self.oo, y=self.h)
+            z.rms_norm(self.h, eps, L.ffn_norm, y=None, packed=self.pa)
+            gemm(self.pa, "ffn_gate", L, c.ffn, c.hidden, self.go)
+            gemm(self.pa, "ffn_up", L, c.ffn, c.hidden, self.uo)
+            z.glu(z.GLU_SWIGLU, self.go, self.uo, c.ffn, y=None, packed=self.pd)
+            gemm(self.pd, "ffn_down", L, c.hidden, c.ffn, self.do)
+            z.add(self.h, self.do, y=self.h)
+        return self.h
+
+    def run_prompt(self, gemm_events=None):
+        for t0 in range(0, self.cfg.tokens, self.chunk):
+            self.run_chunk(self.x[t0:t0 + self.chunk], gemm_events)

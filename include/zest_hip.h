@@ -1,0 +1,122 @@
+/*
+ * zest_hip.h — the thin C ABI between the C++ host side (the ggml backend in
+ * ggml-xdna_amd/csrc/backend) and the hand-written CDNA4 kernels of the bfp16
+ * prefill MUL_MAT path. Plain pointers, sizes and int status codes; no C++ or
+ * torch types. Device pointers are HIP device memory; `stream` is a
+ * hipStream_t passed as void* (NULL = the default stream). Every call only
+ * enqueues work on `stream` and returns; results are ready when the stream is.
+ *
+ * Errors: a negative status, with zest_last_error() (thread-local) saying why.
+ *
+ * Each entry point names the reference interface it replaces (paths in the
+ * Cyronius/ggml-xdna tree).
+ */
+#ifndef ZEST_HIP_H
+#define ZEST_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ZEST_API __attribute__((visibility("default")))
+
+enum zest_status {
+    ZEST_OK = 0,
+    ZEST_E_ARG = -1,         /* a bad size, pointer or type */
+    ZEST_E_HIP = -2,         /* the HIP runtime failed */
+    ZEST_E_UNSUPPORTED = -3, /* no kernel for this case */
+    ZEST_E_SELF_TEST = -4,   /* the known-answer multiply came out wrong */
+};
+
+/* Weight types, numbered as ggml's enum ggml_type. */
+enum zest_type { ZEST_TYPE_F32 = 0, ZEST_TYPE_Q8_0 = 8, ZEST_TYPE_Q4_K = 12 };
+
+/* GLU kinds, numbered as ggml's enum ggml_glu_op. */
+enum zest_glu_kind {
+    ZEST_GLU_REGLU = 0,
+    ZEST_GLU_GEGLU = 1,
+    ZEST_GLU_SWIGLU = 2,
+    ZEST_GLU_GEGLU_ERF = 3,
+    ZEST_GLU_GEGLU_QUICK = 4,
+};
+
+/* Makes `device` current for the calling thread and checks it is a gfx950
+ * (MI355X-class) GPU. Replaces the device-open half of xdna_npu_usable
+ * (src/xdna-npu.cpp:255-291). */
+ZEST_API int zest_init(int device);
+
+/* The registration known-answer test: npu_self_test's integer multiply
+ * (src/xdna-npu.cpp:142-184) run through the pack and GEMM kernels on the
+ * current device; every output must equal the exact integer. 0 when it
+ * passes. Synchronous. */
+ZEST_API int zest_self_test(void);
+
+/* What the last failing call on this thread said. */
+ZEST_API const char *zest_last_error(void);
+
+/* ---- the tile layout (ggml-xdna_amd/csrc/zest_layout.h) ----------------- */
+ZEST_API int64_t zest_rows_pad(int64_t rows);          /* rows rounded up to 256 */
+ZEST_API int64_t zest_k_pad(int64_t K);                /* K rounded up to 64 */
+ZEST_API size_t zest_bfp16_bytes(int64_t rows, int64_t K); /* bytes of a packed operand */
+ZEST_API size_t zest_raw_row_bytes(int type, int64_t K);  /* bytes of one GGUF row */
+
+/* fp32 activations x[M][K] (row stride ldx floats) -> packed bfp16, bit-exact
+ * with the reference encoder; rows M..rows_pad(M)-1 and columns K..k_pad(K)-1
+ * become zero blocks. K % 8 == 0. Replaces bfp16_pack_a_into
+ * (src/npu/bfp16_pack.h:58) / xdna_npu::encode_row (src/xdna-npu.h:96). */
+ZEST_API int zest_pack_act(const float *x, int64_t M, int64_t K, int64_t ldx, void *dst, void *stream);
+
+/* A GGUF weight raw[N][K] of `type` (F32, Q8_0 or Q4_K rows, as ggml stores
+ * them) -> packed bfp16 weight cache entry (zest_bfp16_bytes(N, K) bytes).
+ * Dequantisation as ggml's to_float, then the same encoder. Replaces
+ * xdna_npu::add_weight's unpack + bfp16_pack_b (src/xdna-npu.cpp:339-378). */
+ZEST_API int zest_convert_weight(int type, const void *raw, int64_t N, int64_t K, void *dst, void *stream);
+
+/* c[M][N] (row stride ldc floats) = A . W^T over packed operands a (M rows)
+ * and w (N rows), K columns each: bfp16 expanded to bf16 in LDS, bf16 MFMA,
+ * fp32 accumulation, fp32 store. If `nonfinite` (a device word) is non-NULL,
+ * it is OR-ed with 1 when any stored value is NaN or infinite. Replaces
+ * xdna_npu::mul_mat (src/xdna-npu.cpp:392-444) and the NPU kernel's
+ * mm_f32_first/mid + output mode 0 (kernels/bfp16_gemm/aie_kernels/aie2p/
+ * mm_bfp_acc.cc:44-116, 258-278). */
+ZEST_API int zest_gemm(const void *a, int64_t M, const void *w, int64_t N, int64_t K, float *c, int64_t ldc,
+                       uint32_t *nonfinite, void *stream);
+
+/* ---- the fused host ops (piece::run_rows, src/xdna-exec.cpp:253-346) ---- */
+
+/* y = RMS_NORM(x) (eps), optionally times a scale row w[d] (the MUL that
+ * follows a norm, :258-277). y (fp32 rows, may be NULL) and/or packed (the
+ * next matmul's packed input, rows_pad(rows) x d, may be NULL). */
+ZEST_API int zest_rms_norm(const float *x, int64_t rows, int64_t d, float eps, const float *w, float *y, void *packed,
+                           void *stream);
+
+/* y[r][j] = act(g[r][j]) * u[r][j] for the GLU kinds (:296-320); g and u rows
+ * have strides sg/su floats (one tensor's halves, or two tensors). y and/or
+ * packed as for zest_rms_norm. */
+ZEST_API int zest_glu(int kind, const float *g, int64_t sg, const float *u, int64_t su, int64_t rows, int64_t f,
+                      float *y, void *packed, void *stream);
+
+/* y = a + b, b either the same shape or one row of d broadcast (:278-289). */
+ZEST_API int zest_add(const float *a, const float *b, int64_t rows, int64_t d, int b_is_row, float *y, void *stream);
+
+/* y = x * w, w one row of d broadcast over rows (:271-277). */
+ZEST_API int zest_mul_row(const float *x, const float *w, int64_t rows, int64_t d, float *y, void *stream);
+
+/* y = x * s + b over n floats (:290-295). */
+ZEST_API int zest_scale(const float *x, int64_t n, float s, float b, float *y, void *stream);
+
+/* ROPE over x[T][heads][d] with positions pos[T] (device int32), normal
+ * (mode 0) or NeoX (mode 2), rotating the first n_dims of each head, with
+ * YaRN and optional per-frequency factors ff[n_dims/2] (:203-239, :321-342).
+ * corr_dims are ggml_rope_yarn_corr_dims' two values, computed by the host. */
+ZEST_API int zest_rope(const float *x, int64_t T, int64_t heads, int64_t d, const int32_t *pos, const float *ff,
+                       int n_dims, int mode, float freq_base, float freq_scale, float ext_factor, float attn_factor,
+                       float corr0, float corr1, float *y, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

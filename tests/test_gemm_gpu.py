@@ -1,0 +1,144 @@
+"""The HIP bfp16 GEMM against the oracle. Products of two bfp16 values are
+exact in bf16 x bf16 -> fp32, so the only allowed difference from the
+reference loop over the same decoded operands is fp32 summation order:
+every output must sit inside |g - r64| <= 1e-3 |r64| + 2 K 2^-24 sum|a b|,
+and the integer / exponent-shift known-answer tests must hold exactly."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+from gen import Rng, make_data
+from helpers import gemm_check, load_quant
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def run_gemm(z, x: np.ndarray, wtype: int, raw: np.ndarray, n: int):
+    import torch
+    m, k = x.shape
+    a = z.pack_act(_dev(x))
+    w = z.convert_weight(wtype, _dev(raw), n, k)
+    nf = torch.zeros(1, dtype=torch.int32, device="cuda")
+    c = z.gemm(a, m, w, n, k, nonfinite=nf)
+    torch.cuda.synchronize()
+    return c.cpu().numpy(), int(nf.item()), a, w
+
+
+def decoded(z, oracle, packed, rows, k):
+    return oracle.decode_rows(z.tiles_to_blocks(packed.cpu().numpy(), rows, k))
+
+
+def test_self_test_entry_point(zest_gpu):
+    zest_gpu.self_test()
+
+
+def test_integer_kat_exact(zest_gpu, oracle):
+    # npu_self_test (src/xdna-npu.cpp:142-184) at several sizes
+    for m, k, n in [(512, 128, 512), (1024, 2560, 768), (37, 64, 300)]:
+        a, w = oracle.self_test_inputs(m, k, n)
+        c, nf, _, _ = run_gemm(zest_gpu, a, 0, w.view(np.uint8), n)
+        want = a.astype(np.int64) @ w.astype(np.int64).T
+        assert np.array_equal(c, want.astype(np.float32)), (m, k, n)
+        assert nf == 0
+
+
+def test_exponent_shift_kat(zest_gpu, oracle):
+    # raising every weight exponent byte by d scales every output by exactly
+    # 2^d (tools/npu-ceiling-repro.cpp:14-23)
+    import torch
+    m, k, n = 256, 512, 512
+    x = Rng(3).normal(m * k).reshape(m, k)
+    w = Rng(4).normal(n * k, 0, 0.02).reshape(n, k)
+    c0, _, a, wp = run_gemm(zest_gpu, x, 0, w.view(np.uint8), n)
+    tiles = wp.view(-1, 1152)
+    for d in (3, -5):
+        shifted = wp.clone().view(-1, 1152)
+        e = shifted[:, 1024:].to(torch.int32)
+        shifted[:, 1024:] = torch.where(e > 0, e + d, e).to(torch.uint8)
+        c = zest_gpu.gemm(a, m, shifted.view(-1), n, k)
+        torch.cuda.synchronize()
+        assert np.array_equal(c.cpu().numpy(), np.ldexp(c0, d))
+    assert tiles.shape[0] > 0
+
+
+@pytest.mark.parametrize("wtype,M,N,K", [
+    (8, 1024, 2560, 2560),   # BASELINE config 1 (test-mul-mat shape), Q8_0
+    (12, 600, 896, 1536),    # padded widths and a ragged batch (test-mul-mat.cpp:153-156)
+    (12, 520, 8960, 1536),
+    (0, 300, 200, 200),      # K not a multiple of 64
+    (8, 1, 256, 512),
+    (12, 2048, 1024, 2560),  # K/V projection of config 3
+])
+def test_gemm_against_oracle(zest_gpu, oracle, wtype, M, N, K):
+    import torch
+    quant = load_quant()
+    x = Rng(M + N).normal(M * K).reshape(M, K)
+    w = Rng(M + K).normal(N * K, 0, 0.02).reshape(N, K)
+    raw = quant.quantize(wtype, torch.from_numpy(w)).numpy() if wtype else w.view(np.uint8)
+    c, nf, a, wp = run_gemm(zest_gpu, x, wtype, raw, N)
+    assert nf == 0
+    ad = decoded(zest_gpu, oracle, a, M, K)
+    wd = decoded(zest_gpu, oracle, wp, N, K)
+    rows = np.arange(M) if M * N * K <= 4e9 else np.linspace(0, M - 1, 96).astype(int)
+    r64, ab = oracle.mul_mat_f64(wd, ad[rows])
+    worst, maxrel = gemm_check(c[rows], r64, ab, K)
+    assert worst <= 1.0, worst
+    assert maxrel <= 1e-3, maxrel
+    # and against the reference loop itself (xdna-ref's fp32 sequential dot)
+    ref32 = oracle.mul_mat_f32(wd, ad[rows[:32]])
+    _, maxrel32 = gemm_check(c[rows[:32]], ref32.astype(np.float64), ab[:32], K)
+    assert maxrel32 <= 1e-3
+
+
+def test_gemm_full_size_ffn_properties(zest_gpu, oracle):
+    # BASELINE config 2 sizes: gate 2048 x 9728 x 2560 with 1% outlier
+    # channels; checked on sampled rows, plus linearity in the activations
+    import torch
+    quant = load_quant()
+    M, N, K = 2048, 9728, 2560
+    rng = Rng(21)
+    x = rng.normal(M * K).reshape(M, K)
+    x[:, rng.ints(K // 100, 0, K - 1)] *= 20.0
+    w = Rng(22).normal(N * K, 0, 0.02).reshape(N, K)
+    raw = quant.quantize(12, torch.from_numpy(w).cuda()).cpu().numpy()
+    c, nf, a, wp = run_gemm(zest_gpu, x, 12, raw, N)
+    assert nf == 0
+    rows = np.array([0, 1, 2, 511, 1024, 1500, 2046, 2047])
+    ad = decoded(zest_gpu, oracle, a, M, K)[rows]
+    wd = decoded(zest_gpu, oracle, wp, N, K)
+    r64, ab = oracle.mul_mat_f64(wd, ad)
+    worst, maxrel = gemm_check(c[rows], r64, ab, K)
+    assert worst <= 1.0 and maxrel <= 1e-3
+    # scaling the activations by 2^j shifts every exponent byte: outputs scale exactly
+    c2, _, _, _ = run_gemm(zest_gpu, x * 4.0, 12, raw, N)
+    assert np.array_equal(c2, c * 4.0)
+
+
+def test_nonfinite_flag(zest_gpu):
+    import torch
+    m, k, n = 64, 128, 256
+    x = Rng(1).normal(m * k).reshape(m, k)
+    w = Rng(2).normal(n * k).reshape(n, k)
+    _, nf, a, wp = run_gemm(zest_gpu, x, 0, w.view(np.uint8), n)
+    assert nf == 0
+    x[5, 17] = np.inf
+    c, nf, _, _ = run_gemm(zest_gpu, x, 0, w.view(np.uint8), n)
+    assert nf == 1
+
+
+def test_gemm_wide_exponent_data(zest_gpu, oracle):
+    # make_data's wide exponents 2^-24..2^12 in both operands
+    m, k, n = 256, 1024, 512
+    x = make_data(m * k, 77).reshape(m, k)
+    w = make_data(n * k, 78).reshape(n, k)
+    c, nf, a, wp = run_gemm(zest_gpu, x, 0, w.view(np.uint8), n)
+    ad = decoded(zest_gpu, oracle, a, m, k)
+    wd = decoded(zest_gpu, oracle, wp, n, k)
+    r64, ab = oracle.mul_mat_f64(wd, ad)
+    worst, _ = gemm_check(c, r64, ab, k)
+    assert worst <= 1.0

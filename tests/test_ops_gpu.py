@@ -1,0 +1,98 @@
+"""The host-op kernels against the oracle, at the bar of tests/test-host-ops.cpp
+(nrmse <= 1e-5 against the CPU's result; inputs N(0, 1.5), rope factors
+U(1, 4), positions 5000 + 300 i). The fused packs must be bit-exact with the
+reference encoder applied to the kernel's own fp32 result."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+from gen import Rng
+from helpers import nrmse
+
+pytestmark = pytest.mark.gpu
+
+EXACT = 1e-5
+
+
+def _dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+@pytest.mark.parametrize("rows,d", [(8, 256), (2048, 2560), (5, 200), (3, 5120)])
+def test_rms_norm_mul_and_fused_pack(zest_gpu, oracle, rows, d):
+    import torch
+    x = Rng(rows + d).normal(rows * d, 0, 1.5).reshape(rows, d)
+    w = Rng(d).normal(d, 1.0, 0.1)
+    want = oracle.mul_row(oracle.rms_norm(x, 1e-6), w)
+    packed = zest_gpu.empty_packed(rows, d)
+    y = zest_gpu.rms_norm(_dev(x), 1e-6, _dev(w), packed=packed)
+    got = _host(y)
+    assert nrmse(got, want) <= EXACT
+    pk = zest_gpu.tiles_to_blocks(_host(packed), rows, d) if d % 8 == 0 else None
+    if pk is not None:
+        assert np.array_equal(pk, oracle.encode_rows(got))
+    # without the scale row: plain RMS_NORM
+    y2 = zest_gpu.rms_norm(_dev(x), 1e-6)
+    assert nrmse(_host(y2), oracle.rms_norm(x, 1e-6)) <= EXACT
+    del torch
+
+
+@pytest.mark.parametrize("kind", [0, 1, 2, 3, 4])
+def test_glu_split(zest_gpu, oracle, kind):
+    rows, f = 8, 256
+    g = Rng(50 + kind).normal(rows * f, 0, 1.5).reshape(rows, f)
+    u = Rng(60 + kind).normal(rows * f, 0, 1.5).reshape(rows, f)
+    got = _host(zest_gpu.glu(kind, _dev(g), _dev(u), f))
+    assert nrmse(got, oracle.glu(kind, g, u)) <= EXACT
+
+
+@pytest.mark.parametrize("swapped", [False, True])
+def test_swiglu_one_tensor_and_fused_pack(zest_gpu, oracle, swapped):
+    # one tensor [rows][2f]: gate and up are its halves (swapped: up first)
+    rows, f = 2048, 9728
+    x = Rng(70).normal(rows * 2 * f, 0, 1.5).reshape(rows, 2 * f)
+    xt = _dev(x)
+    g, u = (xt[:, f:], xt[:, :f]) if swapped else (xt[:, :f], xt[:, f:])
+    packed = zest_gpu.empty_packed(rows, f)
+    got = _host(zest_gpu.glu(2, g, u, f, packed=packed))
+    gh, uh = (x[:, f:], x[:, :f]) if swapped else (x[:, :f], x[:, f:])
+    assert nrmse(got, oracle.glu(2, gh, uh)) <= EXACT
+    assert np.array_equal(zest_gpu.tiles_to_blocks(_host(packed), rows, f), oracle.encode_rows(got))
+
+
+def test_add_mul_scale(zest_gpu, oracle):
+    rows, d = 8, 256
+    a = Rng(80).normal(rows * d, 0, 1.5).reshape(rows, d)
+    b = Rng(81).normal(rows * d, 0, 1.5).reshape(rows, d)
+    r = Rng(82).normal(d, 0, 1.5)
+    assert nrmse(_host(zest_gpu.add(_dev(a), _dev(b))), oracle.add(a, b)) <= EXACT
+    assert nrmse(_host(zest_gpu.add(_dev(a), _dev(r), b_is_row=True)), oracle.add_row(a, r)) <= EXACT
+    assert nrmse(_host(zest_gpu.mul_row(_dev(a), _dev(r))), oracle.mul_row(a, r)) <= EXACT
+    assert nrmse(_host(zest_gpu.scale(_dev(a), 0.37, 0.25)), oracle.scale(a, np.float32(0.37), np.float32(0.25))) <= EXACT
+
+
+ROPE_CASES = [  # (n_dims, mode, n_ctx_orig, freq_scale, ext_factor, factors): tests/test-host-ops.cpp:146-152
+    (64, 0, 0, 1.0, 0.0, False), (64, 2, 0, 1.0, 0.0, False), (32, 0, 0, 1.0, 0.0, False),
+    (48, 2, 0, 1.0, 0.0, False), (64, 2, 4096, 0.25, 1.0, False), (64, 2, 4096, 1.0, 0.0, True),
+    (64, 0, 4096, 0.25, 1.0, True),
+]
+
+
+@pytest.mark.parametrize("n_dims,mode,n_ctx,fs,ext,factors", ROPE_CASES)
+def test_rope(zest_gpu, oracle, n_dims, mode, n_ctx, fs, ext, factors):
+    T, H, HD = 8, 4, 64
+    x = Rng(90).normal(T * H * HD, 0, 1.5).reshape(T, H, HD)
+    pos = (5000 + 300 * np.arange(T)).astype(np.int32)
+    ff = (1.0 + 3.0 * Rng(91).uniform(n_dims // 2)).astype(np.float32) if factors else None
+    want = oracle.rope(x, pos, ff, n_dims, mode, n_ctx, 10000.0, fs, ext, 1.0, 32.0, 1.0)
+    corr = oracle.corr_dims(n_dims, n_ctx, 10000.0, 32.0, 1.0)
+    got = zest_gpu.rope(_dev(x), _dev(pos), None if ff is None else _dev(ff), n_dims, mode, 10000.0, fs, ext, 1.0,
+                        corr)
+    assert nrmse(_host(got), want) <= EXACT

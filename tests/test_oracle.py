@@ -1,0 +1,263 @@
+"""The CPU oracle pinned against the reference's golden vectors, its known
+answer tests, closed forms and brute force (no GPU). Mirrors
+tests/test-bfp16-pack.cpp and the accuracy contract of tests/test-mul-mat.cpp."""
+from __future__ import annotations
+
+import hashlib
+
+import numpy as np
+import pytest
+from gen import Rng, make_data
+from helpers import GOLDEN, RefPacker, gemm_check, load_quant, nrmse
+
+GOLD = np.load(GOLDEN / "bfp16_golden.npz")
+
+A_SHAPES = [(512, 256, 128, 64), (256, 384, 64, 128), (1024, 6144, 128, 64)]
+B_SHAPES = [(1024, 256, 64, 64, 8), (4096, 2048, 64, 64, 8), (2048, 6144, 64, 128, 8), (512, 128, 32, 64, 4)]
+
+
+def test_encode_matches_reference_golden_blocks(oracle):
+    got = oracle.encode_rows(GOLD["blocks_x"]).reshape(-1, 9)
+    assert np.array_equal(got, GOLD["blocks_enc"])
+
+
+def test_saturation_kat(oracle):
+    # tests/test-bfp16-pack.cpp:168-175
+    blk = np.ldexp(np.array([127.75, 1.0, -3.5, 0.0, 64.0, -127.5, 0.25, 100.5], dtype=np.float32), -6)
+    enc = oracle.encode_rows(blk[None, :])[0, 0]
+    m = enc[1:].view(np.int8)
+    assert enc[0] == 127 and m[0] == 127 and m[5] == -128 and m[7] == 100
+
+
+def test_zero_block_is_all_zero_bytes(oracle):
+    z = np.array([[0.0, -0.0, 0.0, 0.0, -0.0, 0.0, 0.0, 0.0]], dtype=np.float32)
+    assert not oracle.encode_rows(z).any()
+
+
+def test_decode_every_exponent_byte(oracle):
+    # tests/test-bfp16-pack.cpp:180-191: every exponent byte, mantissas -128..127
+    e = np.repeat(np.arange(256, dtype=np.uint8), 32)
+    m = np.tile(np.arange(-128, 128, dtype=np.int8), 256).reshape(-1, 8)
+    blocks = np.concatenate([e[:, None], m.view(np.uint8)], axis=1)
+    got = oracle.decode_rows(blocks[:, None, :]).reshape(-1, 8)
+    with np.errstate(over="ignore"):  # 128 * 2^122 overflows to -inf in float, as in the reference
+        want = np.ldexp(m.astype(np.float64), e[:, None].astype(np.int32) - 133).astype(np.float32)
+    assert np.array_equal(got, want)
+
+
+def test_encode_decode_round_trip_is_exact_for_representable_blocks(oracle):
+    # a block whose largest mantissa magnitude is in 64..127 re-encodes to
+    # itself: the exponent byte is recovered and every value is exact
+    # (-128 is left out: its float exponent is one above the block's)
+    rng = Rng(5)
+    n = 4096
+    e = rng.ints(n, 8, 250).astype(np.uint8)
+    m = rng.ints(n * 8, -127, 127).astype(np.int8).reshape(n, 8)
+    m[:, 0] = np.array([127, -127, 64, -64], dtype=np.int8)[rng.ints(n, 0, 3)]
+    blocks = np.concatenate([e[:, None], m.view(np.uint8)], axis=1)
+    x = oracle.decode_rows(blocks[:, None, :])
+    assert np.array_equal(oracle.encode_rows(x).reshape(n, 9), blocks)
+
+
+def test_encoder_matches_independent_float64_statement(oracle):
+    # the test's own reference encoder (tests/test-bfp16-pack.cpp:21-38) works
+    # in double; restate it with numpy float64 and compare on wide data
+    x = make_data(64 * 1024, 99).reshape(-1, 8)
+    bits = x.view(np.uint32)
+    e = ((bits >> 23) & 0xFF).max(axis=1)
+    q = np.rint(np.ldexp(x.astype(np.float64), (133 - e.astype(np.int32))[:, None]))
+    q = np.clip(q, -128, 127).astype(np.int8)
+    want = np.concatenate([e.astype(np.uint8)[:, None], q.view(np.uint8)], axis=1)
+    assert np.array_equal(oracle.encode_rows(x).reshape(-1, 9), want)
+
+
+@pytest.mark.parametrize("M,K,m,k", A_SHAPES)
+def test_pack_a_order_matches_reference(oracle, M, K, m, k):
+    x = make_data(M * K, 1 + M + K).reshape(M, K)
+    got = oracle.pack_a(x, m, k)
+    key = f"a_{M}x{K}_m{m}k{k}"
+    if key in GOLD:
+        assert np.array_equal(got, GOLD[key])
+    assert hashlib.sha256(got.tobytes()).digest() == GOLD[key + "_sha256"].tobytes()
+
+
+@pytest.mark.parametrize("N,K,n,k,cols", B_SHAPES)
+def test_pack_b_order_matches_reference(oracle, N, K, n, k, cols):
+    w = make_data(N * K, 7 + N + K).reshape(N, K)
+    got = oracle.pack_b(w, n, k, cols)
+    key = f"b_{N}x{K}_n{n}k{k}c{cols}"
+    if key in GOLD:
+        assert np.array_equal(got, GOLD[key])
+    assert hashlib.sha256(got.tobytes()).digest() == GOLD[key + "_sha256"].tobytes()
+
+
+def test_oracle_against_reference_packer_built_here(oracle):
+    try:
+        ref = RefPacker("avx2")
+    except FileNotFoundError:
+        pytest.skip("oracle/_ref not built (reference tree absent)")
+    for seed in (3, 4):
+        x = make_data(256 * 512, seed).reshape(256, 512)
+        assert np.array_equal(oracle.pack_a(x, 128, 64), ref.pack_a(x, 128, 64))
+        assert np.array_equal(oracle.pack_b(x, 64, 64, 4), ref.pack_b(x, 64, 64, 4))
+
+
+# ---- GGUF dequant --------------------------------------------------------------
+
+def _fp16(v):
+    return np.array([v], dtype=np.float16).view(np.uint8)
+
+
+def test_q8_0_dequant_closed_form(oracle):
+    q = np.arange(-128, 128, dtype=np.int8).reshape(8, 32)
+    raw = np.concatenate([np.concatenate([_fp16(0.5 * (i + 1)), q[i].view(np.uint8)]) for i in range(8)])
+    y = oracle.dequant(8, raw, 1, 256)
+    want = (q.astype(np.float64) * (0.5 * (np.arange(8) + 1))[:, None]).reshape(-1)
+    assert np.array_equal(y.reshape(-1), want.astype(np.float32))
+
+
+def _q4k_block(d, dmin, sc, mn, q):
+    """A Q4_K block from 8 (scale, min) pairs and 256 nibbles, packed by the
+    inverse of the 6-bit layout (scales[0..3] = sc|hi2(sc4..7), [4..7] =
+    m|hi2(m4..7), [8..11] = lo4(sc4..7)|lo4(m4..7)<<4)."""
+    sc = np.asarray(sc, dtype=np.uint8)
+    mn = np.asarray(mn, dtype=np.uint8)
+    s = np.zeros(12, dtype=np.uint8)
+    s[0:4] = sc[0:4] | ((sc[4:8] >> 4) << 6)
+    s[4:8] = mn[0:4] | ((mn[4:8] >> 4) << 6)
+    s[8:12] = (sc[4:8] & 0xF) | ((mn[4:8] & 0xF) << 4)
+    q = np.asarray(q, dtype=np.uint8).reshape(8, 32)
+    qs = (q[0::2] | (q[1::2] << 4)).reshape(-1)
+    return np.concatenate([_fp16(d), _fp16(dmin), s, qs])
+
+
+def test_q4_k_dequant_hand_built_blocks(oracle):
+    # every sub-block gets its own scale and min, including the split 6-bit
+    # fields of sub-blocks 4..7; constant nibbles per sub-block reveal the
+    # order (low nibbles of a 32-byte run first, then the high nibbles)
+    sc = [1, 2, 3, 63, 17, 33, 48, 62]
+    mn = [0, 5, 63, 9, 21, 40, 63, 1]
+    q = np.repeat(np.arange(8) + 3, 32)
+    for d, dmin in ((0.25, 0.125), (1.5, 0.0078125)):
+        raw = _q4k_block(d, dmin, sc, mn, q)
+        y = oracle.dequant(12, raw, 1, 256).reshape(8, 32)
+        want = np.array([d * sc[j] * (j + 3) - dmin * mn[j] for j in range(8)], dtype=np.float64)
+        assert np.array_equal(y, np.repeat(want.astype(np.float32)[:, None], 32, axis=1))
+    # varying nibbles inside one sub-block keep their positions
+    qv = np.arange(256) % 16
+    raw = _q4k_block(1.0, 0.0, [1] * 8, [0] * 8, qv)
+    assert np.array_equal(oracle.dequant(12, raw, 1, 256).reshape(-1), qv.astype(np.float32))
+
+
+@pytest.mark.parametrize("wtype", [8, 12])
+def test_quantize_dequantize_round_trip_bound(oracle, wtype):
+    import torch
+    quant = load_quant()
+    n, k = 64, 512
+    w = Rng(17).normal(n * k, 0.0, 0.02).reshape(n, k)
+    raw = quant.quantize(wtype, torch.from_numpy(w)).numpy()
+    y = oracle.dequant(wtype, raw, n, k)
+    if wtype == 8:
+        step = np.abs(w.reshape(n, k // 32, 32)).max(axis=2) / 127.0
+        err = np.abs(y - w).reshape(n, k // 32, 32).max(axis=2)
+        # half a step, plus the fp16 rounding of d over |q| <= 127 steps
+        assert (err <= (0.5 + 127 * 2.0 ** -11) * step + 1e-7).all()
+    else:
+        assert nrmse(y, w) < 0.08  # 4-bit: ~ (range/15)/sqrt(12) / std
+        assert np.abs(y - w).max() < 0.02
+
+
+# ---- the reference matmul --------------------------------------------------------
+
+def test_ref_mul_mat_integer_kat(oracle):
+    # npu_self_test's operands (src/xdna-npu.cpp:142-156): exact under any order
+    a, w = oracle.self_test_inputs(512, 128, 512)
+    want = a.astype(np.int64) @ w.astype(np.int64).T
+    got = oracle.mul_mat_f32(w, a)
+    assert np.array_equal(got, want.astype(np.float32))
+
+
+@pytest.mark.parametrize("wtype", [8, 12])
+def test_ref_mul_mat_dequantises_then_dots(oracle, wtype):
+    import torch
+    quant = load_quant()
+    n, k, m = 48, 512, 40
+    w = Rng(23).normal(n * k, 0.0, 0.02).reshape(n, k)
+    raw = quant.quantize(wtype, torch.from_numpy(w)).numpy()
+    x = Rng(24).normal(m * k).reshape(m, k)
+    y = oracle.ref_mul_mat(wtype, raw, n, k, x, threads=3)
+    assert np.array_equal(y, oracle.mul_mat_f32(oracle.dequant(wtype, raw, n, k), x, threads=5))
+    r64, ab = oracle.mul_mat_f64(oracle.dequant(wtype, raw, n, k), x)
+    worst, _ = gemm_check(y, r64, ab, k)
+    assert worst <= 1.0
+
+
+def test_fp64_reference_against_numpy(oracle):
+    w = Rng(31).normal(33 * 200).reshape(33, 200)
+    x = Rng(32).normal(21 * 200).reshape(21, 200)
+    r64, ab = oracle.mul_mat_f64(w, x, threads=4)
+    assert np.allclose(r64, x.astype(np.float64) @ w.astype(np.float64).T, rtol=1e-12, atol=1e-12)
+    assert np.allclose(ab, np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T, rtol=1e-12)
+
+
+# ---- host ops ------------------------------------------------------------------
+
+def test_rms_norm_closed_form_and_fp64(oracle):
+    x = np.full((3, 256), 2.0, dtype=np.float32)
+    y = oracle.rms_norm(x, 0.0)
+    assert np.allclose(y, 1.0, rtol=0, atol=1e-6)
+    x = Rng(41).normal(8 * 256, 0, 1.5).reshape(8, 256)
+    x64 = x.astype(np.float64)
+    want = x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + 1e-6)
+    assert nrmse(oracle.rms_norm(x, 1e-6), want) < 1e-6
+
+
+def test_glu_kinds_against_library_functions(oracle):
+    from scipy.special import erf, expit
+    g = Rng(43).normal(8 * 256, 0, 1.5).reshape(8, 256).astype(np.float32)
+    u = Rng(44).normal(8 * 256, 0, 1.5).reshape(8, 256).astype(np.float32)
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    assert nrmse(oracle.glu(2, g, u), g64 * expit(g64) * u64) < 1e-6                       # SwiGLU
+    assert nrmse(oracle.glu(3, g, u), 0.5 * g64 * (1 + erf(g64 / np.sqrt(2))) * u64) < 1e-6  # GeGLU (erf)
+    assert nrmse(oracle.glu(1, g, u), 0.5 * g64 * (1 + erf(g64 / np.sqrt(2))) * u64) < 2e-3  # tanh approximation
+    assert nrmse(oracle.glu(4, g, u), g64 * expit(1.702 * g64) * u64) < 1e-6                 # quick GELU
+    assert nrmse(oracle.glu(0, g, u), np.maximum(g64, 0) * u64) < 1e-7                       # ReGLU
+
+
+def test_elementwise_ops(oracle):
+    x = Rng(45).normal(4 * 64).reshape(4, 64)
+    w = Rng(46).normal(64)
+    assert np.array_equal(oracle.mul_row(x, w), x * w[None, :])
+    assert np.array_equal(oracle.add_row(x, w), x + w[None, :])
+    assert np.array_equal(oracle.add(x, x[::-1].copy()), x + x[::-1])
+    assert np.array_equal(oracle.scale(x, np.float32(0.37), np.float32(0.25)),
+                          x * np.float32(0.37) + np.float32(0.25))
+
+
+@pytest.mark.parametrize("mode", [0, 2])
+def test_rope_is_a_rotation_by_pos_times_theta(oracle, mode):
+    # no YaRN, no factors, attn_factor 1: each pair turns by pos*base^(-2p/n)
+    T, H, D = 4, 3, 64
+    x = Rng(47).normal(T * H * D).reshape(T, H, D)
+    pos = np.array([0, 1, 17, 5000], dtype=np.int32)
+    for n_dims in (D, D // 2):
+        y = oracle.rope(x, pos, None, n_dims, mode, 0, 10000.0, 1.0, 0.0, 1.0, 32.0, 1.0)
+        half = n_dims // 2
+        p = np.arange(half)
+        theta = pos[:, None].astype(np.float64) * 10000.0 ** (-2.0 * p / n_dims)[None, :]
+        i0 = p if mode == 2 else 2 * p
+        i1 = i0 + (half if mode == 2 else 1)
+        z = (x[:, :, i0] + 1j * x[:, :, i1]) * np.exp(1j * theta)[:, None, :]
+        assert np.allclose(y[:, :, i0], z.real, atol=2e-3)
+        assert np.allclose(y[:, :, i1], z.imag, atol=2e-3)
+        assert np.array_equal(y[:, :, n_dims:], x[:, :, n_dims:])
+        assert np.array_equal(y[0], x[0])  # position 0 turns nothing
+
+
+def test_rope_yarn_corr_dims_closed_form(oracle):
+    # parity unpinned against ggml (absent): checked against the YaRN formula
+    # dim(r) = n_dims*ln(n_ctx/(2*pi*r)) / (2 ln base), floor/ceil and clamped
+    n, ctx, base = 64, 4096, 10000.0
+    dim = lambda r: n * np.log(ctx / (2 * np.pi * r)) / (2 * np.log(base))
+    lo, hi = oracle.corr_dims(n, ctx, base, 32.0, 1.0)
+    assert lo == max(0.0, np.floor(dim(32.0))) and hi == min(n - 1.0, np.ceil(dim(1.0)))

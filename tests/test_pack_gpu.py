@@ -1,0 +1,117 @@
+"""The HIP activation packer and weight converters against the reference's
+golden bytes and the CPU oracle: bit-exact (tests/test-bfp16-pack.cpp's bar),
+through the tile layout's bijection to row-major blocks."""
+from __future__ import annotations
+
+import hashlib
+
+import numpy as np
+import pytest
+from gen import Rng, edge_blocks, make_data
+from helpers import GOLDEN, load_quant
+from layout_ref import a_block_index, b_block_index, to_npu_order
+
+pytestmark = pytest.mark.gpu
+GOLD = np.load(GOLDEN / "bfp16_golden.npz")
+
+
+def gpu_pack(z, x: np.ndarray, ldx: int | None = None) -> np.ndarray:
+    import torch
+    m, k = x.shape
+    if ldx is None:
+        xt = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    else:
+        full = torch.zeros((m, ldx), dtype=torch.float32)
+        full[:, :k] = torch.from_numpy(x)
+        xt = full.cuda()[:, :k]
+    out = z.pack_act(xt)
+    torch.cuda.synchronize()
+    return z.tiles_to_blocks(out.cpu().numpy(), m, k)
+
+
+@pytest.mark.parametrize("M,K,m,k", [(512, 256, 128, 64), (256, 384, 64, 128), (1024, 6144, 128, 64)])
+def test_pack_act_matches_reference_golden(zest_gpu, M, K, m, k):
+    x = make_data(M * K, 1 + M + K).reshape(M, K)
+    got = to_npu_order(gpu_pack(zest_gpu, x), a_block_index(M, K, m, k))
+    key = f"a_{M}x{K}_m{m}k{k}"
+    if key in GOLD:
+        assert np.array_equal(got, GOLD[key])
+    assert hashlib.sha256(got.tobytes()).digest() == GOLD[key + "_sha256"].tobytes()
+
+
+def test_pack_act_golden_blocks_and_edge_cases(zest_gpu):
+    x = GOLD["blocks_x"]  # make_data blocks + zero / subnormal / tiny / saturating / near-FLT_MAX blocks
+    n = x.shape[0] // 8 * 8
+    got = gpu_pack(zest_gpu, x[:n].reshape(-1, 64))
+    assert np.array_equal(got.reshape(-1, 9), GOLD["blocks_enc"][:n])
+    e = edge_blocks()
+    got = gpu_pack(zest_gpu, e.reshape(1, -1))
+    assert np.array_equal(got.reshape(-1, 9), GOLD["blocks_enc"][-e.shape[0]:])
+
+
+@pytest.mark.parametrize("M,K,ldx", [(1, 8, None), (17, 24, None), (600, 200, None), (300, 2560, 2600),
+                                     (2048, 2560, None)])
+def test_pack_act_ragged_shapes_against_oracle(zest_gpu, oracle, M, K, ldx):
+    x = make_data(M * K, M * 31 + K).reshape(M, K)
+    assert np.array_equal(gpu_pack(zest_gpu, x, ldx), oracle.encode_rows(x))
+
+
+def test_pack_act_padding_is_zero(zest_gpu):
+    import torch
+    M, K = 70, 72  # rows pad to 256, columns to 128
+    x = torch.from_numpy(make_data(M * K, 5).reshape(M, K)).cuda()
+    out = torch.full((zest_gpu.bfp16_bytes(M, K),), 0xAB, dtype=torch.uint8, device="cuda")
+    zest_gpu.pack_act(x, out)
+    torch.cuda.synchronize()
+    full = zest_gpu.tiles_to_blocks(out.cpu().numpy(), zest_gpu.rows_pad(M), zest_gpu.k_pad(K))
+    assert not full[M:].any() and not full[:, K // 8:].any()
+
+
+def test_pack_act_outlier_channels_full_size(zest_gpu, oracle):
+    # BASELINE config 2's activations: N(0,1) with 1% of channels x20
+    M, K = 2048, 2560
+    rng = Rng(2)
+    x = rng.normal(M * K).reshape(M, K)
+    ch = rng.ints(K // 100, 0, K - 1)
+    x[:, ch] *= 20.0
+    assert np.array_equal(gpu_pack(zest_gpu, x), oracle.encode_rows(x))
+
+
+def gpu_convert(z, wtype: int, raw: np.ndarray, n: int, k: int) -> np.ndarray:
+    import torch
+    rt = torch.from_numpy(np.ascontiguousarray(raw)).cuda()
+    out = z.convert_weight(wtype, rt, n, k)
+    torch.cuda.synchronize()
+    return z.tiles_to_blocks(out.cpu().numpy(), n, k)
+
+
+@pytest.mark.parametrize("wtype,N,K", [(8, 256, 512), (8, 300, 2560), (8, 100, 96), (12, 256, 512),
+                                       (12, 333, 2560), (12, 9728, 2560), (12, 2560, 9728), (8, 2560, 4096)])
+def test_convert_weight_matches_oracle(zest_gpu, oracle, wtype, N, K):
+    import torch
+    quant = load_quant()
+    w = Rng(N + K + wtype).normal(N * K, 0.0, 0.02).reshape(N, K)
+    raw = quant.quantize(wtype, torch.from_numpy(w)).numpy()
+    want = oracle.encode_rows(oracle.dequant(wtype, raw, N, K))
+    assert np.array_equal(gpu_convert(zest_gpu, wtype, raw, N, K), want)
+
+
+def test_convert_weight_npu_order_matches_reference_golden(zest_gpu):
+    # F32 weights through the converter land, via the bijection, exactly on
+    # the reference packer's bfp16_pack_b bytes
+    for N, K, n, k, cols in [(1024, 256, 64, 64, 8), (512, 128, 32, 64, 4)]:
+        w = make_data(N * K, 7 + N + K).reshape(N, K)
+        got = to_npu_order(gpu_convert(zest_gpu, 0, w.view(np.uint8), N, K), b_block_index(N, K, n, k, cols))
+        assert np.array_equal(got, GOLD[f"b_{N}x{K}_n{n}k{k}c{cols}"])
+
+
+def test_convert_extreme_quant_blocks(zest_gpu, oracle):
+    # Q8_0 blocks with d = 0, the largest fp16 d, subnormal d and +-128 quants
+    rng = Rng(9)
+    n, k = 16, 256
+    raw = rng.ints(n * k // 32 * 34, 0, 255).astype(np.uint8).reshape(n, k // 32, 34)
+    ds = np.array([0.0, 65504.0, 6e-8, -1.0, 2.0 ** -14, 1e-3, -3e-5, 1.0], dtype=np.float16)
+    raw[:, :, :2] = ds[rng.ints(n * k // 32, 0, 7)].view(np.uint8).reshape(n, k // 32, 2)
+    raw = raw.reshape(n, -1)
+    want = oracle.encode_rows(oracle.dequant(8, raw, n, k))
+    assert np.array_equal(gpu_convert(zest_gpu, 8, raw, n, k), want)
