@@ -74,4 +74,62 @@ __device__ inline void expand8(uint32_t w0, uint32_t w1, uint32_t e, uint32_t ou
         out[i] = __builtin_amdgcn_perm(__float_as_uint(f[2 * i + 1]), __float_as_uint(f[2 * i]), 0x07060302u);
 }
 
+typedef unsigned short zest_u16x2 __attribute__((ext_vector_type(2)));
+
+// Sixteen mantissas (one 16-byte unit: two blocks) with their two exponent
+// bytes -> sixteen bf16, the same values as expand8 with fewer VALU ops when
+// both exponent bytes are in 7..133 (blocks whose largest magnitude is below
+// 128 and above 2^-120: the activations and weights of real models):
+//   float(q) by a byte-select convert with sign extension (exact), its top
+//   half is bf16(q) (exact: |q| <= 128 has at most 8 significant bits), and
+//   q * 2^(e-133) is that bf16 with (133 - e) subtracted from its exponent
+//   field: a 16-bit saturating subtract on both halves of a dword. The
+//   exponent field of a nonzero bf16(q) is at least 127 and 133 - e is at
+//   most 126, so the sign bit never borrows, and q = 0 saturates to 0.
+// Two ops per value. Other exponent bytes go through expand8.
+//
+// expand16_fast is that fast path alone, branch-free so it can be scheduled
+// between MFMAs; it returns true when the unit needs expand8 instead (its
+// output is then not the decoded values and must be replaced).
+__device__ inline bool expand16_fast(const uint4 & m, uint32_t e2, uint32_t out[8]) {
+    // (133 - e) << 7 for each block
+    const int32_t d0 = 133 * 128 - (int32_t) ((e2 & 0xffu) << 7);
+    const int32_t d1 = 133 * 128 - (int32_t) ((e2 >> 8) << 7);
+    const zest_u16x2 dv0 = {(unsigned short) d0, (unsigned short) d0};
+    const zest_u16x2 dv1 = {(unsigned short) d1, (unsigned short) d1};
+    const uint32_t w[4] = {m.x, m.y, m.z, m.w};
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint32_t wd = w[i >> 1];
+        const int sh = (i & 1) * 16;
+        const float lo = (float) (int8_t) (wd >> sh), hi = (float) (int8_t) (wd >> (sh + 8));
+        const uint32_t b = __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+        const zest_u16x2 r = __builtin_elementwise_sub_sat(__builtin_bit_cast(zest_u16x2, b), i < 4 ? dv0 : dv1);
+        out[i] = __builtin_bit_cast(uint32_t, r);
+    }
+    // exponent bytes 7..133 <=> 0 <= (133 - e) * 128 <= 126 * 128
+    return max((uint32_t) d0, (uint32_t) d1) > 126u * 128u;
+}
+
+__device__ inline void expand16(const uint4 & m, uint32_t e2, uint32_t out[8]) {
+    const uint32_t e0 = e2 & 0xffu, e1 = e2 >> 8;
+    if (__builtin_expect((e0 - 7u <= 126u) & (e1 - 7u <= 126u), 1)) {
+        const uint32_t d0 = (133u - e0) * 0x00800080u, d1 = (133u - e1) * 0x00800080u;
+        const uint32_t w[4] = {m.x, m.y, m.z, m.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t wd = w[i >> 1];
+            const int sh = (i & 1) * 16;
+            const float lo = (float) (int8_t) (wd >> sh), hi = (float) (int8_t) (wd >> (sh + 8));
+            const uint32_t b = __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+            const zest_u16x2 r = __builtin_elementwise_sub_sat(__builtin_bit_cast(zest_u16x2, b),
+                                                               __builtin_bit_cast(zest_u16x2, i < 4 ? d0 : d1));
+            out[i] = __builtin_bit_cast(uint32_t, r);
+        }
+    } else {
+        expand8(m.x, m.y, e0, out);
+        expand8(m.z, m.w, e1, out + 4);
+    }
+}
+
 } // namespace zest
