@@ -33,9 +33,12 @@ struct unit_regs {
     uint32_t e;
 };
 
-template <int BM_, int BN_, int WGM_, int WGN_>
+// BM x BN tile over WGM x WGN waves; DEPTH 1 or 2 staging register sets (how
+// many K-steps ahead the global loads run); the next step's expansion starts
+// after sub-step EXP_START of the current one.
+template <int BM_, int BN_, int WGM_, int WGN_, int DEPTH_ = 2, int EXP_START_ = 0>
 struct gemm_cfg {
-    static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_;
+    static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, DEPTH = DEPTH_, EXP_START = EXP_START_;
     static constexpr int NT = 64 * WGM * WGN;
     static constexpr int WM = BM / WGM, WN = BN / WGN;
     static constexpr int TI = WM / 32, TJ = WN / 32;
@@ -178,16 +181,13 @@ __device__ inline void read_frags(bf16x8 (&af)[C::TI], bf16x8 (&bfr)[C::TJ], con
 // same time (one wave per SIMD, in-order issue). Units whose exponent bytes
 // need the general expansion are redone after the MFMAs, behind a
 // wave-uniform branch that real data almost never takes.
-#ifndef ZEST_GEMM_EXP_START
-#define ZEST_GEMM_EXP_START 1
-#endif
-template <class C, int CUR, bool LOAD>
+template <class C, int CUR, bool LOAD, bool EXPAND>
 __device__ inline void mma_step(f32x16 (&acc)[C::TI][C::TJ], uint8_t * smem, const lds_lanes & ll,
-                                unit_regs (&st)[C::U], const slab_reader & ra, int a_off, const slab_reader & rw,
-                                int w_off) {
-    constexpr int EXP_START = ZEST_GEMM_EXP_START;
+                                unit_regs (&sl)[C::U], unit_regs (&st)[C::U], const slab_reader & ra, int a_off,
+                                const slab_reader & rw, int w_off) {
+    constexpr int EXP_START = C::EXP_START;
     constexpr int EXP_STEPS = 4 - EXP_START;
-    if (LOAD) load_step<C>(st, ra, a_off, rw, w_off);
+    if (LOAD) load_step<C>(sl, ra, a_off, rw, w_off);
     bf16x8 af[2][C::TI], bfr[2][C::TJ];
     read_frags<C>(af[0], bfr[0], smem, ll, 0, CUR);
     bool slow[C::U];
@@ -199,7 +199,7 @@ __device__ inline void mma_step(f32x16 (&acc)[C::TI][C::TJ], uint8_t * smem, con
 #pragma unroll
             for (int j = 0; j < C::TJ; j++)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s & 1][i], bfr[s & 1][j], acc[i][j], 0, 0, 0);
-        if (LOAD && s >= EXP_START) {
+        if (EXPAND && s >= EXP_START) {
 #pragma unroll
             for (int u = (s - EXP_START) * C::U / EXP_STEPS; u < (s - EXP_START + 1) * C::U / EXP_STEPS; u++) {
                 uint32_t b[8];
@@ -215,13 +215,16 @@ __device__ inline void mma_step(f32x16 (&acc)[C::TI][C::TJ], uint8_t * smem, con
     constexpr int PER = C::TI * C::TJ;  // MFMAs per sub-step
     constexpr int MFMAS = 4 * PER;
     constexpr int EXP_MFMAS = EXP_STEPS * PER;
-    constexpr int VALU_PER = LOAD ? (C::U * 34 + EXP_MFMAS - 1) / EXP_MFMAS : 0;
-    constexpr int STORES = LOAD ? 2 * C::U : 0;
+    constexpr int VALU_PER = EXPAND ? (C::U * 34 + EXP_MFMAS - 1) / EXP_MFMAS : 0;
+    constexpr int STORES = EXPAND ? 2 * C::U : 0;
     constexpr int READS = 3 * (C::TI + C::TJ);
     constexpr int LOADS = LOAD ? 2 * C::U : 0;
-    __builtin_amdgcn_sched_group_barrier(0x100, C::TI + C::TJ, 0);  // sub-step 0's fragments
+#ifndef ZEST_GEMM_SCHED
+#define ZEST_GEMM_SCHED 1
+#endif
+    if (ZEST_GEMM_SCHED) __builtin_amdgcn_sched_group_barrier(0x100, C::TI + C::TJ, 0);  // sub-step 0's fragments
 #pragma unroll
-    for (int q = 0; q < MFMAS; q++) {
+    for (int q = 0; q < (ZEST_GEMM_SCHED ? MFMAS : 0); q++) {
         if (q < LOADS) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // next step's loads, early
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                // MFMA
         if (q * READS / MFMAS != (q + 1) * READS / MFMAS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
@@ -232,7 +235,7 @@ __device__ inline void mma_step(f32x16 (&acc)[C::TI][C::TJ], uint8_t * smem, con
                 __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
         }
     }
-    if (LOAD) {
+    if (EXPAND) {
         bool any = false;
 #pragma unroll
         for (int u = 0; u < C::U; u++) any |= slow[u];
@@ -309,28 +312,55 @@ __global__ __launch_bounds__(C::NT, 1) void gemm_kernel(const uint8_t * __restri
     for (int i = 0; i < C::TI; i++)
 #pragma unroll
         for (int j = 0; j < C::TJ; j++) acc[i][j] = f32x16{};
-    unit_regs st[C::U];
-
-    // prologue: step 0 into LDS buffer 0
-    load_step<C>(st, ra, a0, rw, w0);
-    store_units<C, 0>(st, smem, ll, 0, C::U);
-    __syncthreads();
-
-    // Step k computes on buffer k&1 and, unless it is the last, loads step
-    // k+1 and expands it into the other buffer.
-    int kc = 0;
-    for (; kc + 2 < nk; kc += 2) {
-        mma_step<C, 0, true>(acc, smem, ll, st, ra, a0 + (kc + 1) * a_kstride, rw, w0 + (kc + 1) * w_kstride);
+    if (C::DEPTH == 1) {
+        // Step k computes on buffer k&1 and, unless it is the last, loads
+        // step k+1 as it starts and expands it into the other buffer.
+        unit_regs st[C::U];
+        load_step<C>(st, ra, a0, rw, w0);
+        store_units<C, 0>(st, smem, ll, 0, C::U);
         __syncthreads();
-        mma_step<C, 1, true>(acc, smem, ll, st, ra, a0 + (kc + 2) * a_kstride, rw, w0 + (kc + 2) * w_kstride);
+        int kc = 0;
+        for (; kc + 2 < nk; kc += 2) {
+            mma_step<C, 0, true, true>(acc, smem, ll, st, st, ra, a0 + (kc + 1) * a_kstride, rw, w0 + (kc + 1) * w_kstride);
+            __syncthreads();
+            mma_step<C, 1, true, true>(acc, smem, ll, st, st, ra, a0 + (kc + 2) * a_kstride, rw, w0 + (kc + 2) * w_kstride);
+            __syncthreads();
+        }
+        if (kc + 1 < nk) {  // 2 left
+            mma_step<C, 0, true, true>(acc, smem, ll, st, st, ra, a0 + (kc + 1) * a_kstride, rw, w0 + (kc + 1) * w_kstride);
+            __syncthreads();
+            mma_step<C, 1, false, false>(acc, smem, ll, st, st, ra, 0, rw, 0);
+        } else {  // 1 left
+            mma_step<C, 0, false, false>(acc, smem, ll, st, st, ra, 0, rw, 0);
+        }
+    } else {
+        // Two staging sets: step k loads step k+2 into one while expanding
+        // step k+1 (loaded during step k-1) from the other.
+        unit_regs sa[C::U], sb[C::U];
+        load_step<C>(sa, ra, a0, rw, w0);
+        if (nk > 1) load_step<C>(sb, ra, a0 + a_kstride, rw, w0 + w_kstride);
+        store_units<C, 0>(sa, smem, ll, 0, C::U);
         __syncthreads();
-    }
-    if (kc + 1 < nk) {  // 2 left
-        mma_step<C, 0, true>(acc, smem, ll, st, ra, a0 + (kc + 1) * a_kstride, rw, w0 + (kc + 1) * w_kstride);
-        __syncthreads();
-        mma_step<C, 1, false>(acc, smem, ll, st, ra, 0, rw, 0);
-    } else {  // 1 left
-        mma_step<C, 0, false>(acc, smem, ll, st, ra, 0, rw, 0);
+        int kc = 0;
+        for (; kc + 3 < nk; kc += 2) {
+            mma_step<C, 0, true, true>(acc, smem, ll, sa, sb, ra, a0 + (kc + 2) * a_kstride, rw, w0 + (kc + 2) * w_kstride);
+            __syncthreads();
+            mma_step<C, 1, true, true>(acc, smem, ll, sb, sa, ra, a0 + (kc + 3) * a_kstride, rw, w0 + (kc + 3) * w_kstride);
+            __syncthreads();
+        }
+        if (kc + 2 < nk) {  // 3 left
+            mma_step<C, 0, true, true>(acc, smem, ll, sa, sb, ra, a0 + (kc + 2) * a_kstride, rw, w0 + (kc + 2) * w_kstride);
+            __syncthreads();
+            mma_step<C, 1, false, true>(acc, smem, ll, sb, sa, ra, 0, rw, 0);
+            __syncthreads();
+            mma_step<C, 0, false, false>(acc, smem, ll, sa, sb, ra, 0, rw, 0);
+        } else if (kc + 1 < nk) {  // 2 left
+            mma_step<C, 0, false, true>(acc, smem, ll, sa, sb, ra, 0, rw, 0);
+            __syncthreads();
+            mma_step<C, 1, false, false>(acc, smem, ll, sa, sb, ra, 0, rw, 0);
+        } else {  // 1 left
+            mma_step<C, 0, false, false>(acc, smem, ll, sa, sb, ra, 0, rw, 0);
+        }
     }
 
     store_tile<C>(acc, Cout, M, N, ldc, m0, n0, wm, wn, lane, nonfinite);
@@ -353,11 +383,14 @@ int launch(const void * a, int64_t M, const void * w, int64_t N, int64_t K, floa
     return zest::check_launch("zest_gemm");
 }
 
+// Measured on MI355X over the BASELINE shapes: 256x128 tiles on 8 waves
+// (128x32 each) with two staging sets lead wherever there are enough tiles;
+// 128x128 on 4 waves for the narrow ones (K/V projections).
 #ifndef ZEST_GEMM_BIG
-#define ZEST_GEMM_BIG 256, 256, 2, 2
+#define ZEST_GEMM_BIG 256, 128, 2, 4, 2, 0
 #endif
 #ifndef ZEST_GEMM_SMALL
-#define ZEST_GEMM_SMALL 128, 128, 2, 2
+#define ZEST_GEMM_SMALL 128, 128, 2, 2, 2, 0
 #endif
 using cfg_big = gemm_cfg<ZEST_GEMM_BIG>;
 using cfg_small = gemm_cfg<ZEST_GEMM_SMALL>;
@@ -377,7 +410,7 @@ extern "C" int zest_gemm(const void * a, int64_t M, const void * w, int64_t N, i
     hipStream_t s = zest::as_stream(stream);
     // 256x256 tiles when they give the GPU enough workgroups, else 128x128
 #ifndef ZEST_GEMM_BIG_MIN_TILES
-#define ZEST_GEMM_BIG_MIN_TILES 192
+#define ZEST_GEMM_BIG_MIN_TILES 160
 #endif
     const int64_t big_tiles = ((M + cfg_big::BM - 1) / cfg_big::BM) * ((N + cfg_big::BN - 1) / cfg_big::BN);
     if (big_tiles >= ZEST_GEMM_BIG_MIN_TILES) return launch<cfg_big>(a, M, w, N, K, c, ldc, nonfinite, s);
