@@ -52,6 +52,7 @@ SIGNATURES = {
     "zest_add": (_c_i, [_c_p, _c_p, _c_i64, _c_i64, _c_i, _c_p, _c_p]),
     "zest_mul_row": (_c_i, [_c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "zest_scale": (_c_i, [_c_p, _c_i64, _c_f, _c_f, _c_p, _c_p]),
+    "zest_check_finite": (_c_i, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p]),
     "zest_rope": (_c_i, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i, _c_i, _c_f, _c_f, _c_f, _c_f,
                          _c_f, _c_f, _c_p, _c_p]),
 }
@@ -213,6 +214,13 @@ def scale(x, s: float, b: float, y=None):
     y = torch.empty_like(x) if y is None else y
     check(lib().zest_scale(_ptr(x), x.numel(), s, b, _ptr(y), _stream()), "zest_scale")
     return y
+
+
+def check_finite(y, flag):
+    """Sets flag[0] (a device uint32/int32 tensor) when y holds NaN or infinity."""
+    rows, cols = (y.shape[0], y.shape[1]) if y.dim() == 2 else (1, y.numel())
+    ld = y.stride(0) if y.dim() == 2 else cols
+    check(lib().zest_check_finite(_ptr(y), rows, cols, ld, _ptr(flag), _stream()), "zest_check_finite")
 
 
 def rope(x, pos, ff, n_dims: int, mode: int, freq_base: float, freq_scale: float, ext_factor: float,

@@ -1,0 +1,733 @@
+// The ggml backend add-on: registration, the device, its HIP buffer type, and
+// the backend whose graph_compute runs the scheduler's pieces on one GPU.
+//
+// The reference (src/ggml-zest.cpp) works next to a Vulkan GPU on a laptop:
+// it reads every input out of Vulkan memory, runs the matmuls on the NPU and
+// the small ops on the host, and writes results back. On an MI355X the model
+// lives in the GPU's own HBM, so this device has its own HIP buffer type and a
+// piece is a sequence of kernel launches on one HIP stream: inputs, weight
+// cache, packed activations and results never leave HBM. Same registry and
+// device names, same gate and settings (policy.cpp), same failure latch; no
+// CPU path.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cmath>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <unordered_set>
+#include <vector>
+
+#include "backend.h"
+#include "zest_hip.h"
+
+namespace zest {
+namespace {
+
+#define XDNA_DESCRIPTION "AMD Instinct MI355X (gfx950): bfp16 prefill MUL_MAT"
+
+// ---- the HIP buffer type -------------------------------------------------------
+
+struct buffer_ctx {
+    void * base = nullptr;
+    size_t size = 0;
+};
+
+void evict_buffer(const ggml_backend_buffer * b);
+
+void buf_free(ggml_backend_buffer_t b) {
+    evict_buffer(b);  // its weights' cache entries go with it
+    auto * c = (buffer_ctx *) b->context;
+    if (c->base) (void) hipFree(c->base);
+    delete c;  // the buffer object itself is deleted by ggml_backend_buffer_free
+}
+void * buf_base(ggml_backend_buffer_t b) { return ((buffer_ctx *) b->context)->base; }
+ggml_status buf_init_tensor(ggml_backend_buffer_t, ggml_tensor *) { return GGML_STATUS_SUCCESS; }
+void buf_memset(ggml_backend_buffer_t, ggml_tensor * t, uint8_t value, size_t offset, size_t size) {
+    (void) hipMemset((char *) t->data + offset, value, size);
+}
+void buf_set(ggml_backend_buffer_t, ggml_tensor * t, const void * data, size_t offset, size_t size) {
+    (void) hipMemcpy((char *) t->data + offset, data, size, hipMemcpyHostToDevice);
+}
+void buf_get(ggml_backend_buffer_t, const ggml_tensor * t, void * data, size_t offset, size_t size) {
+    (void) hipMemcpy(data, (const char *) t->data + offset, size, hipMemcpyDeviceToHost);
+}
+ggml_backend_buffer_type * our_buft();
+bool buf_cpy(ggml_backend_buffer_t, const ggml_tensor * src, ggml_tensor * dst) {
+    if (!src->buffer || src->buffer->buft != our_buft()) return false;
+    return hipMemcpy(dst->data, src->data, nbytes(src), hipMemcpyDeviceToDevice) == hipSuccess;
+}
+void buf_clear(ggml_backend_buffer_t b, uint8_t value) {
+    auto * c = (buffer_ctx *) b->context;
+    (void) hipMemset(c->base, value, c->size);
+}
+
+const ggml_backend_buffer_i buffer_iface = {
+    /* .free_buffer   = */ buf_free,
+    /* .get_base      = */ buf_base,
+    /* .init_tensor   = */ buf_init_tensor,
+    /* .memset_tensor = */ buf_memset,
+    /* .set_tensor    = */ buf_set,
+    /* .get_tensor    = */ buf_get,
+    /* .cpy_tensor    = */ buf_cpy,
+    /* .clear         = */ buf_clear,
+    /* .reset         = */ nullptr,
+};
+
+const char * buft_name(ggml_backend_buffer_type_t) { return GGML_XDNA_DEVICE_NAME; }
+ggml_backend_buffer_t buft_alloc(ggml_backend_buffer_type_t buft, size_t size) {
+    auto * c = new buffer_ctx;
+    c->size = size;
+    if (hipMalloc(&c->base, size ? size : 1) != hipSuccess) {
+        log(LOG_ERROR, "cannot allocate %zu bytes of device memory\n", size);
+        delete c;
+        return nullptr;
+    }
+    return new ggml_backend_buffer{buffer_iface, buft, c, size, GGML_BACKEND_BUFFER_USAGE_ANY};
+}
+size_t buft_alignment(ggml_backend_buffer_type_t) { return 256; }
+size_t buft_max_size(ggml_backend_buffer_type_t) { return SIZE_MAX; }
+bool buft_is_host(ggml_backend_buffer_type_t) { return false; }
+
+ggml_backend_device * our_device();
+
+ggml_backend_buffer_type * our_buft() {
+    static ggml_backend_buffer_type buft = {
+        {buft_name, buft_alloc, buft_alignment, buft_max_size, nullptr, buft_is_host}, nullptr, nullptr};
+    buft.device = our_device();
+    return &buft;
+}
+
+// ---- the backend context ---------------------------------------------------
+
+struct wkey {
+    const void * buffer, * data;
+    int type;
+    int64_t ne0, ne1;
+    bool operator==(const wkey & o) const {
+        return buffer == o.buffer && data == o.data && type == o.type && ne0 == o.ne0 && ne1 == o.ne1;
+    }
+};
+struct wkey_hash {
+    size_t operator()(const wkey & k) const {
+        return std::hash<const void *>()(k.buffer) ^ (std::hash<const void *>()(k.data) * 31) ^ (size_t) k.ne1;
+    }
+};
+wkey key_of(const ggml_tensor * w) { return {w->buffer, w->data, (int) w->type, w->ne[0], w->ne[1]}; }
+
+// GGML_XDNA_FAIL_AFTER=n: every GEMM submission after the n-th fails;
+// GGML_XDNA_NAN_AFTER=n: every GEMM result after the n-th comes back as NaN
+// (src/xdna-npu.cpp:89-112). Both forced from the host: kernels run normally.
+int64_t fail_after() {
+    static const int64_t v = env_int("GGML_XDNA_FAIL_AFTER", -1);
+    return v;
+}
+int64_t nan_after() {
+    static const int64_t v = env_int("GGML_XDNA_NAN_AFTER", -1);
+    return v;
+}
+std::atomic<int64_t> g_submissions{0};
+
+struct context {
+    hipStream_t stream = nullptr;  // compute
+    hipStream_t loader = nullptr;  // weight conversion at load
+    uint32_t * nonfinite = nullptr;
+
+    struct weight_entry {
+        void * packed = nullptr;
+        hipEvent_t ready = nullptr;  // recorded on `loader` when built at load
+    };
+    std::unordered_map<wkey, weight_entry, wkey_hash> weights;
+    int64_t built_at_load = 0, built_in_graph = 0;
+
+    // per-graph device workspace: grow-only blocks, handed out from the start
+    // again by each graph
+    struct block {
+        char * p;
+        size_t size, used;
+    };
+    std::vector<block> blocks;
+
+    // trace
+    double compute_ms = 0;
+    int64_t matmuls = 0, pieces = 0;
+
+    context();
+    ~context();
+    void evict(const ggml_backend_buffer * b);
+
+    bool init(std::string & err) {
+        if (hipSetDevice(device_index()) != hipSuccess || hipStreamCreateWithFlags(&stream, hipStreamNonBlocking) ||
+            hipStreamCreateWithFlags(&loader, hipStreamNonBlocking) || hipMalloc(&nonfinite, 256)) {
+            err = "cannot create streams on the device";
+            return false;
+        }
+        return true;
+    }
+
+
+    void ws_reset() {
+        for (block & b : blocks) b.used = 0;
+    }
+    void * ws_alloc(size_t n) {
+        n = (n + 255) / 256 * 256;
+        for (block & b : blocks)
+            if (b.size - b.used >= n) {
+                void * p = b.p + b.used;
+                b.used += n;
+                return p;
+            }
+        const size_t sz = std::max(n, (size_t) 64 << 20);
+        block b{nullptr, sz, n};
+        if (hipMalloc((void **) &b.p, sz) != hipSuccess) return nullptr;
+        blocks.push_back(b);
+        return b.p;
+    }
+
+    // The weight's cache entry, converted from its raw GGUF bytes where they
+    // are (device memory in our buffers; host memory goes up first) on
+    // `on_stream`; an entry built at load is waited for on the compute stream.
+    bool ensure_weight(const ggml_tensor * w, hipStream_t on_stream, bool at_load, std::string & err) {
+        const wkey key = key_of(w);
+        auto it = weights.find(key);
+        if (it != weights.end()) {
+            if (!at_load && it->second.ready) {
+                if (hipStreamWaitEvent(stream, it->second.ready, 0) != hipSuccess) {
+                    err = "waiting for a weight conversion failed";
+                    return false;
+                }
+            }
+            return true;
+        }
+        const int64_t K = w->ne[0], N = w->ne[1];
+        weight_entry e;
+        if (hipMalloc(&e.packed, zest_bfp16_bytes(N, K)) != hipSuccess) {
+            err = "cannot allocate a weight-cache entry";
+            return false;
+        }
+        const void * raw = w->data;
+        void * tmp = nullptr;
+        if (buffer_is_host(w->buffer)) {
+            const size_t nb = nbytes(w);
+            if (hipMalloc(&tmp, nb) != hipSuccess ||
+                hipMemcpyAsync(tmp, w->data, nb, hipMemcpyHostToDevice, on_stream) != hipSuccess) {
+                err = "cannot upload a host weight";
+                (void) hipFree(e.packed);
+                return false;
+            }
+            raw = tmp;
+        }
+        if (zest_convert_weight(w->type, raw, N, K, e.packed, on_stream) != ZEST_OK) {
+            err = std::string(w->name) + ": " + zest_last_error();
+            (void) hipFree(e.packed);
+            return false;
+        }
+        if (tmp) {
+            (void) hipStreamSynchronize(on_stream);
+            (void) hipFree(tmp);
+        }
+        if (at_load) {
+            (void) hipEventCreateWithFlags(&e.ready, hipEventDisableTiming);
+            (void) hipEventRecord(e.ready, on_stream);
+            built_at_load++;
+        } else {
+            built_in_graph++;
+        }
+        weights.emplace(key, e);
+        return true;
+    }
+};
+
+// Live contexts, so that freeing one of our buffers drops the cache entries of
+// the weights it held (a later buffer may reuse the address).
+std::mutex g_ctx_mu;
+std::unordered_set<context *> g_contexts;
+
+context::context() {
+    std::lock_guard<std::mutex> lk(g_ctx_mu);
+    g_contexts.insert(this);
+}
+
+context::~context() {
+    {
+        std::lock_guard<std::mutex> lk(g_ctx_mu);
+        g_contexts.erase(this);
+    }
+    if (stream) (void) hipStreamSynchronize(stream);
+    if (loader) (void) hipStreamSynchronize(loader);
+    for (auto & kv : weights) {
+        if (kv.second.packed) (void) hipFree(kv.second.packed);
+        if (kv.second.ready) (void) hipEventDestroy(kv.second.ready);
+    }
+    for (block & b : blocks) (void) hipFree(b.p);
+    if (nonfinite) (void) hipFree(nonfinite);
+    if (stream) (void) hipStreamDestroy(stream);
+    if (loader) (void) hipStreamDestroy(loader);
+}
+
+void context::evict(const ggml_backend_buffer * b) {
+    bool synced = false;
+    for (auto it = weights.begin(); it != weights.end();) {
+        if (it->first.buffer != b) {
+            ++it;
+            continue;
+        }
+        if (!synced) {
+            if (stream) (void) hipStreamSynchronize(stream);
+            if (loader) (void) hipStreamSynchronize(loader);
+            synced = true;
+        }
+        if (it->second.packed) (void) hipFree(it->second.packed);
+        if (it->second.ready) (void) hipEventDestroy(it->second.ready);
+        it = weights.erase(it);
+    }
+}
+
+void evict_buffer(const ggml_backend_buffer * b) {
+    std::lock_guard<std::mutex> lk(g_ctx_mu);
+    for (context * c : g_contexts) c->evict(b);
+}
+
+// ---- graph execution ---------------------------------------------------------
+
+int glu_kind_of(int g) {
+    switch (g) {
+        case GGML_GLU_OP_REGLU: return ZEST_GLU_REGLU;
+        case GGML_GLU_OP_GEGLU: return ZEST_GLU_GEGLU;
+        case GGML_GLU_OP_SWIGLU: return ZEST_GLU_SWIGLU;
+        case GGML_GLU_OP_GEGLU_ERF: return ZEST_GLU_GEGLU_ERF;
+        case GGML_GLU_OP_GEGLU_QUICK: return ZEST_GLU_GEGLU_QUICK;
+        default: return -1;
+    }
+}
+
+// ggml_rope_yarn_corr_dims (ggml-base; called by the reference at
+// src/xdna-exec.cpp:221), from the published YaRN formula: the dimension
+// where a frequency turns n_rot times over n_ctx_orig positions.
+void rope_corr_dims(int n_dims, int n_ctx_orig, float base, float beta_fast, float beta_slow, float dims[2]) {
+    auto dim = [&](float n_rot) {
+        return (float) n_dims * logf((float) n_ctx_orig / (n_rot * 2.0f * (float) M_PI)) / (2.0f * logf(base));
+    };
+    dims[0] = std::max(0.0f, floorf(dim(beta_fast)));
+    dims[1] = std::min((float) (n_dims - 1), ceilf(dim(beta_slow)));
+}
+
+struct piece {
+    context & ctx;
+    const ggml_cgraph * g;
+    std::vector<ggml_tensor *> nodes;
+    std::unordered_set<const ggml_tensor *> in_piece;
+    std::unordered_map<const ggml_tensor *, void *> staged;   // host inputs copied up
+    std::unordered_map<const ggml_tensor *, void *> packed;   // owner -> packed bfp16 activations
+    struct pending_out {
+        ggml_tensor * t;
+        void * dev;
+    };
+    std::vector<pending_out> host_outs;  // results of nodes whose memory is on the host
+    std::string err;
+
+    piece(context & c, const ggml_cgraph * graph) : ctx(c), g(graph) {
+        for (int i = 0; i < g->n_nodes; i++) {
+            nodes.push_back(g->nodes[i]);
+            in_piece.insert(g->nodes[i]);
+        }
+    }
+
+    bool fail(const std::string & e) {
+        err = e;
+        return false;
+    }
+
+    // A device pointer to t's data (host tensors are copied up once per piece).
+    const void * in(const ggml_tensor * t) {
+        if (!buffer_is_host(t->buffer)) return t->data;
+        auto it = staged.find(t);
+        if (it != staged.end()) return it->second;
+        const size_t nb = nbytes(t);
+        void * p = ctx.ws_alloc(nb);
+        if (!p || hipMemcpyAsync(p, t->data, nb, hipMemcpyHostToDevice, ctx.stream) != hipSuccess) return nullptr;
+        staged[t] = p;
+        return p;
+    }
+    // Where a node writes: its own memory, or device scratch copied down after.
+    void * out(ggml_tensor * t) {
+        if (!buffer_is_host(t->buffer)) return t->data;
+        void * p = ctx.ws_alloc(nbytes(t));
+        if (p) {
+            host_outs.push_back({t, p});
+            staged[t] = p;
+        }
+        return p;
+    }
+
+    // The tensor whose packed copy a matmul input x can use: its owner when x
+    // reads the owner's rows exactly (itself, or a reshape of the same rows),
+    // else x itself (no packed copy is ever made for a partial view).
+    static const ggml_tensor * packed_key(const ggml_tensor * x) {
+        const ggml_tensor * o = owner(x);
+        if (x == o) return x;
+        return x->data == o->data && x->ne[0] == o->ne[0] && nrows(x) == nrows(o) && is_contiguous(x) ? o : x;
+    }
+    // whether some MUL_MAT of this piece reads t's rows as its input
+    bool feeds_matmul(const ggml_tensor * t) const {
+        for (const ggml_tensor * n : nodes)
+            if (n->op == GGML_OP_MUL_MAT && packed_key(n->src[1]) == t) return true;
+        return false;
+    }
+    // the only reader of t, inside the piece and out, is `only`
+    bool only_reader(const ggml_tensor * t, const ggml_tensor * only) const {
+        for (const ggml_tensor * n : nodes)
+            for (int j = 0; j < GGML_MAX_SRC; j++)
+                if (n != only && n->src[j] && owner(n->src[j]) == t) return false;
+        return !read_outside(t, in_piece);
+    }
+    // packed bfp16 space for a matmul input produced in this piece
+    void * packed_for(const ggml_tensor * t, int64_t rows, int64_t K) {
+        if (K % 8 != 0 || !feeds_matmul(t)) return nullptr;
+        void * p = ctx.ws_alloc(zest_bfp16_bytes(rows, K));
+        if (p) packed[t] = p;
+        return p;
+    }
+
+    bool check(int st, const char * what) {
+        if (st == ZEST_OK) return true;
+        return fail(std::string(what) + ": " + zest_last_error());
+    }
+
+    bool mul_mat(ggml_tensor * n) {
+        const ggml_tensor * w = n->src[0], * x = n->src[1];
+        const int64_t K = w->ne[0], N = w->ne[1], M = x->ne[1];
+        if (!is_weight(w) || x->type != GGML_TYPE_F32 || !is_contiguous(x) || K % 8) return fail("a matmul this backend does not take");
+        if (!ctx.ensure_weight(w, ctx.stream, false, err)) return false;
+        const void * wp = ctx.weights.at(key_of(w)).packed;
+        void * ap = nullptr;
+        auto it = packed.find(packed_key(x));
+        if (it != packed.end()) {
+            ap = it->second;
+        } else {
+            const void * xd = in(x);
+            ap = ctx.ws_alloc(zest_bfp16_bytes(M, K));
+            if (!xd || !ap) return fail("out of device memory for a matmul input");
+            if (!check(zest_pack_act((const float *) xd, M, K, (int64_t) (x->nb[1] / 4), ap, ctx.stream), "pack"))
+                return false;
+            packed[packed_key(x)] = ap;
+        }
+        float * y = (float *) out(n);
+        if (!y) return fail("out of device memory for a matmul result");
+        const int64_t ldc = (int64_t) (n->nb[1] / 4);
+        const int64_t s = ++g_submissions;
+        if (fail_after() >= 0 && s > fail_after()) return fail("an injected failure (GGML_XDNA_FAIL_AFTER)");
+        if (!check(zest_gemm(ap, M, wp, N, K, y, ldc, ctx.nonfinite, ctx.stream), "gemm")) return false;
+        if (nan_after() >= 0 && s > nan_after()) {
+            (void) hipMemsetAsync(y, 0xff, (size_t) ((M - 1) * ldc + N) * 4, ctx.stream);
+            if (!check(zest_check_finite(y, M, N, ldc, ctx.nonfinite, ctx.stream), "finite check")) return false;
+        }
+        ctx.matmuls++;
+        return true;
+    }
+
+    bool rms_norm(ggml_tensor * n, size_t & i) {
+        const ggml_tensor * x = n->src[0];
+        const float eps = param_f32(n, 0);
+        const int64_t d = x->ne[0], rows = nrows(x);
+        const void * xd = in(x);
+        if (!xd) return fail("out of device memory");
+        // RMS_NORM then MUL by a scale row, the norm read by nothing else: one kernel
+        ggml_tensor * next = i + 1 < nodes.size() ? nodes[i + 1] : nullptr;
+        if (next && next->op == GGML_OP_MUL && next->src[0] == n && exec_supports(next) && only_reader(n, next)) {
+            const void * wd = in(next->src[1]);
+            float * y = (float *) out(next);
+            if (!wd || !y) return fail("out of device memory");
+            void * pk = packed_for(next, rows, d);
+            i++;
+            return check(zest_rms_norm((const float *) xd, rows, d, eps, (const float *) wd, y, pk, ctx.stream),
+                         "rms_norm+mul");
+        }
+        float * y = (float *) out(n);
+        if (!y) return fail("out of device memory");
+        return check(zest_rms_norm((const float *) xd, rows, d, eps, nullptr, y, packed_for(n, rows, d), ctx.stream),
+                     "rms_norm");
+    }
+
+    bool glu(ggml_tensor * n) {
+        const ggml_tensor * a = n->src[0], * b = n->src[1];
+        const int kind = glu_kind_of(param_i32(n, 0));
+        const int64_t f = n->ne[0], rows = nrows(n);
+        const float * ad = (const float *) in(a);
+        const float * gd, * ud;
+        int64_t sg, su;
+        if (b) {
+            gd = ad;
+            ud = (const float *) in(b);
+            sg = (int64_t) (a->nb[1] / 4);
+            su = (int64_t) (b->nb[1] / 4);
+        } else {
+            const bool swapped = param_i32(n, 1) != 0;
+            gd = ad ? ad + (swapped ? f : 0) : nullptr;
+            ud = ad ? ad + (swapped ? 0 : f) : nullptr;
+            sg = su = (int64_t) (a->nb[1] / 4);
+        }
+        float * y = (float *) out(n);
+        if (!gd || !ud || !y || kind < 0) return fail("bad GLU");
+        return check(zest_glu(kind, gd, sg, ud, su, rows, f, y, packed_for(n, rows, f), ctx.stream), "glu");
+    }
+
+    bool rope(ggml_tensor * n) {
+        const ggml_tensor * x = n->src[0], * pos = n->src[1], * ff = n->src[2];
+        const int n_dims = param_i32(n, 1), mode = param_i32(n, 2), n_ctx_orig = param_i32(n, 4);
+        const float base = param_f32(n, 5), fs = param_f32(n, 6), ext = param_f32(n, 7), attn = param_f32(n, 8);
+        float corr[2];
+        rope_corr_dims(n_dims, n_ctx_orig, base, param_f32(n, 9), param_f32(n, 10), corr);
+        const void * xd = in(x), * pd = in(pos), * fd = ff ? in(ff) : nullptr;
+        float * y = (float *) out(n);
+        if (!xd || !pd || (ff && !fd) || !y) return fail("out of device memory");
+        return check(zest_rope((const float *) xd, x->ne[2], x->ne[1], x->ne[0], (const int32_t *) pd,
+                               (const float *) fd, n_dims, mode, base, fs, ext, attn, corr[0], corr[1], y, ctx.stream),
+                     "rope");
+    }
+
+    bool run() {
+        for (size_t i = 0; i < nodes.size(); i++) {
+            ggml_tensor * n = nodes[i];
+            if (is_noop(n)) continue;
+            bool ok = true;
+            switch (n->op) {
+                case GGML_OP_MUL_MAT: ok = mul_mat(n); break;
+                case GGML_OP_RMS_NORM: ok = rms_norm(n, i); break;
+                case GGML_OP_GLU: ok = glu(n); break;
+                case GGML_OP_ROPE: ok = rope(n); break;
+                case GGML_OP_MUL: {
+                    const void * xd = in(n->src[0]), * wd = in(n->src[1]);
+                    float * y = (float *) out(n);
+                    ok = xd && wd && y &&
+                         check(zest_mul_row((const float *) xd, (const float *) wd, nrows(n), n->ne[0], y, ctx.stream),
+                               "mul");
+                    break;
+                }
+                case GGML_OP_ADD: {
+                    const ggml_tensor * a = n->src[0], * b = n->src[1];
+                    const void * ad = in(a), * bd = in(b);
+                    float * y = (float *) out(n);
+                    const int row = !same_shape(a, b);
+                    ok = ad && bd && y &&
+                         check(zest_add((const float *) ad, (const float *) bd, nrows(n), n->ne[0], row, y, ctx.stream),
+                               "add");
+                    break;
+                }
+                case GGML_OP_SCALE: {
+                    const void * xd = in(n->src[0]);
+                    float * y = (float *) out(n);
+                    ok = xd && y &&
+                         check(zest_scale((const float *) xd, nelements(n), param_f32(n, 0), param_f32(n, 1), y,
+                                          ctx.stream),
+                               "scale");
+                    break;
+                }
+                default: return fail(std::string("unsupported op ") + op_name(n->op) + " (" + n->name + ")");
+            }
+            if (!ok) return false;
+        }
+        for (const pending_out & o : host_outs)
+            if (hipMemcpyAsync(o.t->data, o.dev, nbytes(o.t), hipMemcpyDeviceToHost, ctx.stream) != hipSuccess)
+                return fail("copying a result to host memory failed");
+        return true;
+    }
+};
+
+// ---- the backend ---------------------------------------------------------------
+
+const char * backend_name(ggml_backend_t) { return GGML_XDNA_DEVICE_NAME; }
+
+void backend_free(ggml_backend_t backend) {
+    delete (context *) backend->context;
+    delete backend;
+    budget_context_freed();
+}
+
+ggml_status graph_compute(ggml_backend_t backend, ggml_cgraph * cgraph) {
+    context & ctx = *(context *) backend->context;
+    budget_report();
+    say_notes();
+    if (mode() != run_mode::gpu || !ctx.stream) {
+        log(LOG_ERROR, "graph_compute without a GPU\n");
+        return GGML_STATUS_FAILED;
+    }
+    if (broken()) {
+        log(LOG_ERROR, "graph_compute after the GPU path failed\n");
+        return GGML_STATUS_FAILED;
+    }
+    const auto t0 = std::chrono::steady_clock::now();
+    ctx.ws_reset();
+    (void) hipMemsetAsync(ctx.nonfinite, 0, sizeof(uint32_t), ctx.stream);
+    piece p(ctx, cgraph);
+    bool ok = p.run();
+    const hipError_t se = hipStreamSynchronize(ctx.stream);
+    if (ok && se != hipSuccess) ok = p.fail(std::string("the GPU reported ") + hipGetErrorString(se));
+    if (ok) {
+        uint32_t nf = 0;
+        if (hipMemcpy(&nf, ctx.nonfinite, sizeof(nf), hipMemcpyDeviceToHost) != hipSuccess || nf)
+            ok = p.fail("the results held NaN or infinity");
+    }
+    ctx.compute_ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    ctx.pieces++;
+    if (trace() && ctx.matmuls >= 196) {
+        fprintf(stderr, "xdna times, %lld matmuls in %lld pieces: all %.1f ms; weight copies %lld at load, %lld in pieces\n",
+                (long long) ctx.matmuls, (long long) ctx.pieces, ctx.compute_ms, (long long) ctx.built_at_load,
+                (long long) ctx.built_in_graph);
+        ctx.compute_ms = 0;
+        ctx.matmuls = ctx.pieces = 0;
+    }
+    if (!ok) {
+        mark_broken(p.err);
+        return GGML_STATUS_FAILED;
+    }
+    return GGML_STATUS_SUCCESS;
+}
+
+// The first time a piece's weights appear (llama.cpp plans graphs at load),
+// their cache entries start converting on a stream of their own, so the first
+// prompt does not wait for them (src/ggml-zest.cpp:928-965).
+// GGML_XDNA_COPY_AT_LOAD=0 leaves them to the first graph_compute.
+void graph_optimize(ggml_backend_t backend, ggml_cgraph * cgraph, ggml_backend_graph_optimize_params *) {
+    static const bool at_load = env_int("GGML_XDNA_COPY_AT_LOAD", 1) != 0;
+    if (!at_load || mode() != run_mode::gpu || broken()) return;
+    context & ctx = *(context *) backend->context;
+    if (!ctx.loader) return;
+    for (int i = 0; i < cgraph->n_nodes; i++) {
+        const ggml_tensor * n = cgraph->nodes[i];
+        if (n->op != GGML_OP_MUL_MAT) continue;
+        const ggml_tensor * w = n->src[0];
+        if (!w->data || !in_weight_buffer(w) || !is_weight(w) || w->ne[0] % 8) continue;
+        std::string err;
+        if (!ctx.ensure_weight(w, ctx.loader, true, err)) {
+            mark_broken("building a weight-cache entry at load: " + err);
+            return;
+        }
+    }
+}
+
+ggml_guid_t backend_guid() {
+    static ggml_guid guid = {0x5a, 0x35, 0x35, 0x58, 0x9d, 0x3a, 0x4e, 0x12, 0xb6, 0x0f, 0x8c, 0x71, 0x2d, 0xe4, 0x90, 0x33};
+    return &guid;
+}
+
+const ggml_backend_i backend_iface = {
+    /* .get_name            = */ backend_name,
+    /* .free                = */ backend_free,
+    /* .set_tensor_async    = */ nullptr,
+    /* .get_tensor_async    = */ nullptr,
+    /* .set_tensor_2d_async = */ nullptr,
+    /* .get_tensor_2d_async = */ nullptr,
+    /* .cpy_tensor_async    = */ nullptr,
+    /* .synchronize         = */ nullptr,
+    /* .graph_plan_create   = */ nullptr,
+    /* .graph_plan_free     = */ nullptr,
+    /* .graph_plan_update   = */ nullptr,
+    /* .graph_plan_compute  = */ nullptr,
+    /* .graph_compute       = */ graph_compute,
+    /* .event_record        = */ nullptr,
+    /* .event_wait          = */ nullptr,
+    /* .graph_optimize      = */ graph_optimize,
+};
+
+// ---- the device ------------------------------------------------------------------
+
+const char * dev_name(ggml_backend_dev_t) { return GGML_XDNA_DEVICE_NAME; }
+const char * dev_description(ggml_backend_dev_t) { return XDNA_DESCRIPTION; }
+
+// The GPU's own memory: the model's weights live there with their cache.
+void dev_memory(ggml_backend_dev_t, size_t * free, size_t * total) {
+    *free = *total = 0;
+    if (mode() == run_mode::gpu && hipMemGetInfo(free, total) != hipSuccess) *free = *total = 0;
+}
+ggml_backend_dev_type dev_type(ggml_backend_dev_t) { return GGML_BACKEND_DEVICE_TYPE_GPU; }
+
+void dev_props(ggml_backend_dev_t dev, ggml_backend_dev_props * props) {
+    props->name = dev_name(dev);
+    props->description = dev_description(dev);
+    props->type = dev_type(dev);
+    props->device_id = nullptr;
+    dev_memory(dev, &props->memory_free, &props->memory_total);
+    // graph_compute returns with its results done: no async, no events
+    props->caps = {false, false, false, false, false};
+}
+
+ggml_backend_t dev_init(ggml_backend_dev_t dev, const char *) {
+    if (mode() != run_mode::gpu) return nullptr;
+    auto * ctx = new context;
+    std::string err;
+    if (!env_int("GGML_XDNA_PLAN_ONLY", 0) && !ctx->init(err)) {
+        log(LOG_ERROR, "%s\n", err.c_str());
+        delete ctx;
+        return nullptr;
+    }
+    budget_context_added();
+    return new ggml_backend{backend_guid(), backend_iface, dev, ctx};
+}
+
+ggml_backend_buffer_type_t dev_buffer_type(ggml_backend_dev_t) { return our_buft(); }
+
+bool dev_supports_op(ggml_backend_dev_t, const ggml_tensor * op) { return supports_op(op); }
+
+// Our device memory, and host buffers (graph inputs such as positions are read
+// from there directly, copied up inside graph_compute).
+bool dev_supports_buft(ggml_backend_dev_t, ggml_backend_buffer_type_t buft) {
+    return buft == our_buft() || (buft->iface.is_host && buft->iface.is_host(buft));
+}
+
+const ggml_backend_device_i device_iface = {
+    /* .get_name             = */ dev_name,
+    /* .get_description      = */ dev_description,
+    /* .get_memory           = */ dev_memory,
+    /* .get_type             = */ dev_type,
+    /* .get_props            = */ dev_props,
+    /* .init_backend         = */ dev_init,
+    /* .get_buffer_type      = */ dev_buffer_type,
+    /* .get_host_buffer_type = */ nullptr,
+    /* .buffer_from_host_ptr = */ nullptr,
+    /* .supports_op          = */ dev_supports_op,
+    /* .supports_buft        = */ dev_supports_buft,
+    // deliberately no offload_op: that path copies the weights per op
+    /* .offload_op           = */ nullptr,
+    /* .event_new            = */ nullptr,
+    /* .event_free           = */ nullptr,
+    /* .event_synchronize    = */ nullptr,
+};
+
+// ---- the registry -----------------------------------------------------------------
+
+const char * reg_name(ggml_backend_reg_t) { return GGML_XDNA_NAME; }
+size_t reg_device_count(ggml_backend_reg_t) { return mode() == run_mode::off ? 0 : 1; }
+ggml_backend_dev_t reg_device_get(ggml_backend_reg_t, size_t index) { return index == 0 ? our_device() : nullptr; }
+
+const ggml_backend_reg_i reg_iface = {
+    /* .get_name         = */ reg_name,
+    /* .get_device_count = */ reg_device_count,
+    /* .get_device       = */ reg_device_get,
+    /* .get_proc_address = */ nullptr,
+};
+
+ggml_backend_device * our_device() {
+    static ggml_backend_device dev = {device_iface, nullptr, nullptr};
+    dev.reg = ggml_backend_xdna_reg();
+    return &dev;
+}
+
+} // namespace
+} // namespace zest
+
+extern "C" {
+
+ggml_backend_reg_t ggml_backend_xdna_reg(void) {
+    static ggml_backend_reg reg = {GGML_BACKEND_API_VERSION, zest::reg_iface, nullptr};
+    return &reg;
+}
+
+ggml_backend_reg_t ggml_backend_init(void) { return ggml_backend_xdna_reg(); }
+
+int ggml_backend_score(void) { return 1; }
+
+} // extern "C"

@@ -163,6 +163,16 @@ __global__ __launch_bounds__(256) void scale_kernel(const float * __restrict__ x
     y[i] = x[i] * s + b;
 }
 
+// NaN or infinity anywhere in rows x cols (row stride ld) sets *flag. The test
+// is on the bits (exponent field all ones), so no fast-math can fold it away.
+__global__ __launch_bounds__(256) void check_finite_kernel(const float * __restrict__ y, int64_t cols, int64_t ld,
+                                                           int64_t n, uint32_t * flag) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint32_t bits = __float_as_uint(y[(i / cols) * ld + i % cols]);
+    if ((bits & 0x7f800000u) == 0x7f800000u) atomicOr(flag, 1u);
+}
+
 // ROPE: one workgroup per (token, head); thread p < n_dims/2 owns pair p.
 // theta for pair p is pos * theta_scale^p built by p float multiplications,
 // as the reference's table loop does (src/xdna-exec.cpp:225-233); the
@@ -265,6 +275,14 @@ int zest_rope(const float * x, int64_t T, int64_t heads, int64_t d, const int32_
     hipLaunchKernelGGL(rope_kernel, dim3((unsigned) (T * heads)), dim3(64), 0, zest::as_stream(stream), x, heads, d, pos,
                        ff, n_dims, mode == 2, theta_scale, freq_scale, ext_factor, attn_factor, corr0, corr1, y);
     return zest::check_launch("zest_rope");
+}
+
+int zest_check_finite(const float * y, int64_t rows, int64_t cols, int64_t ld, uint32_t * flag, void * stream) {
+    ZEST_REQUIRE(y && flag && rows > 0 && cols > 0 && ld >= cols, "zest_check_finite: bad arguments");
+    const int64_t n = rows * cols;
+    hipLaunchKernelGGL(check_finite_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, zest::as_stream(stream), y, cols,
+                       ld, n, flag);
+    return zest::check_launch("zest_check_finite");
 }
 
 } // extern "C"

@@ -34,7 +34,8 @@ enum zest_status {
 /* Weight types, numbered as ggml's enum ggml_type. */
 enum zest_type { ZEST_TYPE_F32 = 0, ZEST_TYPE_Q8_0 = 8, ZEST_TYPE_Q4_K = 12 };
 
-/* GLU kinds, numbered as ggml's enum ggml_glu_op. */
+/* GLU kinds. Not ggml's numbering (ggml_glu_op has SWIGLU_OAI at 3, which
+ * this library does not run): a ggml caller maps by kind. */
 enum zest_glu_kind {
     ZEST_GLU_REGLU = 0,
     ZEST_GLU_GEGLU = 1,
@@ -115,6 +116,12 @@ ZEST_API int zest_scale(const float *x, int64_t n, float s, float b, float *y, v
 ZEST_API int zest_rope(const float *x, int64_t T, int64_t heads, int64_t d, const int32_t *pos, const float *ff,
                        int n_dims, int mode, float freq_base, float freq_scale, float ext_factor, float attn_factor,
                        float corr0, float corr1, float *y, void *stream);
+
+/* Sets *flag (device memory, nonzero stays) when any of rows x cols floats at
+ * y (row stride ld) is NaN or infinite: the check the reference makes on each
+ * NPU result before using it (src/xdna-npu.cpp:57-85), for results that
+ * no zest_gemm produced. */
+ZEST_API int zest_check_finite(const float *y, int64_t rows, int64_t cols, int64_t ld, uint32_t *flag, void *stream);
 
 #ifdef __cplusplus
 }
