@@ -384,6 +384,22 @@ struct piece {
                 if (n != only && n->src[j] && owner(n->src[j]) == t) return false;
         return !read_outside(t, in_piece);
     }
+    // Every reader of t is a matmul of this piece taking t's rows as its
+    // input (views in between are free): its packed copy then serves them
+    // all and its fp32 values need not be written (src/ggml-zest.cpp:1100-1109).
+    bool only_matmuls_read(const ggml_tensor * t) const {
+        bool any = false;
+        for (const ggml_tensor * n : nodes) {
+            if (is_noop(n)) continue;
+            for (int j = 0; j < GGML_MAX_SRC; j++) {
+                const ggml_tensor * s = n->src[j];
+                if (!s || owner(s) != t) continue;
+                if (n->op != GGML_OP_MUL_MAT || j != 1 || packed_key(s) != t) return false;
+                any = true;
+            }
+        }
+        return any && !read_outside(t, in_piece);
+    }
     // packed bfp16 space for a matmul input produced in this piece
     void * packed_for(const ggml_tensor * t, int64_t rows, int64_t K) {
         if (K % 8 != 0 || !feeds_matmul(t)) return nullptr;
@@ -439,17 +455,17 @@ struct piece {
         ggml_tensor * next = i + 1 < nodes.size() ? nodes[i + 1] : nullptr;
         if (next && next->op == GGML_OP_MUL && next->src[0] == n && exec_supports(next) && only_reader(n, next)) {
             const void * wd = in(next->src[1]);
-            float * y = (float *) out(next);
-            if (!wd || !y) return fail("out of device memory");
             void * pk = packed_for(next, rows, d);
+            float * y = pk && only_matmuls_read(next) ? nullptr : (float *) out(next);
+            if (!wd || (!y && !pk)) return fail("out of device memory");
             i++;
             return check(zest_rms_norm((const float *) xd, rows, d, eps, (const float *) wd, y, pk, ctx.stream),
                          "rms_norm+mul");
         }
-        float * y = (float *) out(n);
-        if (!y) return fail("out of device memory");
-        return check(zest_rms_norm((const float *) xd, rows, d, eps, nullptr, y, packed_for(n, rows, d), ctx.stream),
-                     "rms_norm");
+        void * pk = packed_for(n, rows, d);
+        float * y = pk && only_matmuls_read(n) ? nullptr : (float *) out(n);
+        if (!y && !pk) return fail("out of device memory");
+        return check(zest_rms_norm((const float *) xd, rows, d, eps, nullptr, y, pk, ctx.stream), "rms_norm");
     }
 
     bool glu(ggml_tensor * n) {
@@ -470,9 +486,10 @@ struct piece {
             ud = ad ? ad + (swapped ? 0 : f) : nullptr;
             sg = su = (int64_t) (a->nb[1] / 4);
         }
-        float * y = (float *) out(n);
-        if (!gd || !ud || !y || kind < 0) return fail("bad GLU");
-        return check(zest_glu(kind, gd, sg, ud, su, rows, f, y, packed_for(n, rows, f), ctx.stream), "glu");
+        void * pk = packed_for(n, rows, f);
+        float * y = pk && only_matmuls_read(n) ? nullptr : (float *) out(n);
+        if (!gd || !ud || (!y && !pk) || kind < 0) return fail("bad GLU");
+        return check(zest_glu(kind, gd, sg, ud, su, rows, f, y, pk, ctx.stream), "glu");
     }
 
     bool rope(ggml_tensor * n) {

@@ -167,7 +167,7 @@ int main() {
         }
         const result r = judge(c, got, wdata, x);
         test_check(r.ok_bound && r.nrmse <= 1e-2 && r.cos > 0.9999,
-                   "%-28s bound use %.3f, nrmse vs raw %.2e, cos %.6f", c.name, r.worst, r.nrmse, r.cos);
+                   "%-28s bound use %.2e, nrmse vs raw %.2e, cos %.6f", c.name, r.worst, r.nrmse, r.cos);
     }
 
     ggml_backend_free(be);
