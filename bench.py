@@ -89,20 +89,26 @@ def orc_p():
     return ctypes.c_void_p
 
 
-def pack_bandwidth(z, m: int, k: int, reps: int = 20) -> dict:
+def pack_bandwidth(z, m: int, k: int, reps: int = 20) -> list:
+    """The activation pack, as bfp16 bytes (4 + 1.125 B/value) and as the
+    GEMM's expanded operand (4 + 2 B/value, the form the stack uses)."""
     import torch
     x = torch.randn((m, k), device="cuda")
-    out = z.empty_packed(m, k)
-    z.pack_act(x, out=out)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        z.pack_act(x, out=out)
-    e1.record()
-    e1.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / reps
-    gbs = 5.125 * m * k / (us * 1e-6) / 1e9
-    return {"shape": [m, k], "us": round(us, 2), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK, 3)}
+    res = []
+    for name, fn, out, per in (("bfp16", z.pack_act, z.empty_packed(m, k), 5.125),
+                               ("expanded", z.pack_act_x, z.empty_act(m, k), 6.0)):
+        fn(x, out=out)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn(x, out=out)
+        e1.record()
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        gbs = per * m * k / (us * 1e-6) / 1e9
+        res.append({"output": name, "shape": [m, k], "us": round(us, 2), "GB/s": round(gbs, 1),
+                    "frac": round(gbs / HBM_PEAK, 3)})
+    return res
 
 
 def convert_bandwidth(z, wtype: int, n: int, k: int, reps: int = 10) -> dict:

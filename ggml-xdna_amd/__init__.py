@@ -44,7 +44,10 @@ SIGNATURES = {
     "zest_k_pad": (_c_i64, [_c_i64]),
     "zest_bfp16_bytes": (ctypes.c_size_t, [_c_i64, _c_i64]),
     "zest_raw_row_bytes": (ctypes.c_size_t, [_c_i, _c_i64]),
+    "zest_act_bytes": (ctypes.c_size_t, [_c_i64, _c_i64]),
     "zest_pack_act": (_c_i, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p]),
+    "zest_pack_act_x": (_c_i, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p]),
+    "zest_expand_act": (_c_i, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "zest_convert_weight": (_c_i, [_c_i, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "zest_gemm": (_c_i, [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p]),
     "zest_rms_norm": (_c_i, [_c_p, _c_i64, _c_i64, _c_f, _c_p, _c_p, _c_p, _c_p]),
@@ -89,6 +92,19 @@ def k_pad(k: int) -> int:
 
 def bfp16_bytes(rows: int, k: int) -> int:
     return rows_pad(rows) * k_pad(k) // 8 * 9
+
+
+def act_bytes(rows: int, k: int) -> int:
+    """Bytes of an expanded activation operand: 2 per value, padded."""
+    return rows_pad(rows) * k_pad(k) * 2
+
+
+def expanded_to_rows(buf: np.ndarray, rows: int, k: int) -> np.ndarray:
+    """Expanded operand bytes -> float32 [rows][k] (the bf16 values widened)."""
+    rp, kp = rows_pad(rows), k_pad(k)
+    t = np.frombuffer(np.ascontiguousarray(buf).tobytes(), dtype=np.uint16).reshape(kp // 64, rp // 16, 16, 64)
+    full = t.transpose(1, 2, 0, 3).reshape(rp, kp)
+    return (full.astype(np.uint32) << 16).view(np.float32)[:rows, :k]
 
 
 def tiles_to_blocks(buf: np.ndarray, rows: int, k: int) -> np.ndarray:
@@ -149,6 +165,12 @@ def empty_packed(rows: int, k: int, device="cuda"):
     return torch.empty(bfp16_bytes(rows, k), dtype=torch.uint8, device=device)
 
 
+def empty_act(rows: int, k: int, device="cuda"):
+    """Space for an expanded activation operand (the GEMM's A)."""
+    torch = _torch()
+    return torch.empty(act_bytes(rows, k), dtype=torch.uint8, device=device)
+
+
 def pack_act(x, out=None):
     """fp32 [M][K] device tensor -> packed bfp16 (uint8 device tensor)."""
     torch = _torch()
@@ -156,6 +178,23 @@ def pack_act(x, out=None):
     m, k = x.shape
     out = empty_packed(m, k, x.device) if out is None else out
     check(lib().zest_pack_act(_ptr(x), m, k, x.stride(0), _ptr(out), _stream()), "zest_pack_act")
+    return out
+
+
+def pack_act_x(x, out=None):
+    """fp32 [M][K] device tensor -> the GEMM's expanded activation operand."""
+    torch = _torch()
+    assert x.dtype == torch.float32 and x.dim() == 2 and x.stride(1) == 1
+    m, k = x.shape
+    out = empty_act(m, k, x.device) if out is None else out
+    check(lib().zest_pack_act_x(_ptr(x), m, k, x.stride(0), _ptr(out), _stream()), "zest_pack_act_x")
+    return out
+
+
+def expand_act(packed, m: int, k: int, out=None):
+    """Packed bfp16 activations -> the expanded operand."""
+    out = empty_act(m, k, packed.device) if out is None else out
+    check(lib().zest_expand_act(_ptr(packed), m, k, _ptr(out), _stream()), "zest_expand_act")
     return out
 
 
@@ -167,7 +206,8 @@ def convert_weight(wtype: int, raw, n: int, k: int, out=None):
 
 
 def gemm(a_packed, m: int, w_packed, n: int, k: int, out=None, nonfinite=None):
-    """c[m][n] fp32 = A . W^T over packed operands."""
+    """c[m][n] fp32 = A . W^T: a_packed the expanded activations (pack_act_x),
+    w_packed a packed bfp16 weight (convert_weight)."""
     torch = _torch()
     out = torch.empty((m, n), dtype=torch.float32, device=a_packed.device) if out is None else out
     check(lib().zest_gemm(_ptr(a_packed), m, _ptr(w_packed), n, k, _ptr(out), out.stride(0), _ptr(nonfinite),

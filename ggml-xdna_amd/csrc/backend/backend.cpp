@@ -403,7 +403,7 @@ struct piece {
     // packed bfp16 space for a matmul input produced in this piece
     void * packed_for(const ggml_tensor * t, int64_t rows, int64_t K) {
         if (K % 8 != 0 || !feeds_matmul(t)) return nullptr;
-        void * p = ctx.ws_alloc(zest_bfp16_bytes(rows, K));
+        void * p = ctx.ws_alloc(zest_act_bytes(rows, K));
         if (p) packed[t] = p;
         return p;
     }
@@ -425,9 +425,9 @@ struct piece {
             ap = it->second;
         } else {
             const void * xd = in(x);
-            ap = ctx.ws_alloc(zest_bfp16_bytes(M, K));
+            ap = ctx.ws_alloc(zest_act_bytes(M, K));
             if (!xd || !ap) return fail("out of device memory for a matmul input");
-            if (!check(zest_pack_act((const float *) xd, M, K, (int64_t) (x->nb[1] / 4), ap, ctx.stream), "pack"))
+            if (!check(zest_pack_act_x((const float *) xd, M, K, (int64_t) (x->nb[1] / 4), ap, ctx.stream), "pack"))
                 return false;
             packed[packed_key(x)] = ap;
         }

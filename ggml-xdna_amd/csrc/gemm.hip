@@ -1,254 +1,218 @@
-// The bfp16 GEMM: C[M][N] = A[M][K] . W[N][K]^T over packed bfp16 operands.
+// The bfp16 GEMM: C[M][N] = A[M][K] . W[N][K]^T, A the expanded activation
+// operand (the bfp16 pack stored decoded as bf16, zest_layout.h) and W a
+// packed bfp16 weight from the resident cache.
 //
-// Per workgroup a BM x BN output tile; per K-step of 64 (one tile-layout
-// column chunk) it
-//   1. reads the A and W slabs (BM/16 and BN/16 contiguous 1152-byte tiles)
-//      with 16-byte buffer loads: each thread one or more "units" = 16
-//      mantissas of one row plus their two exponent bytes;
-//   2. expands every unit once, losslessly, to 16 bf16 (zest::expand16) and
-//      stores them to LDS, rows of 64 bf16 with the 16-byte chunks XOR-swizzled
-//      by row so the stores and the MFMA reads are bank-conflict free;
-//   3. runs v_mfma_f32_32x32x16_bf16: each lane's eight K values of an operand
-//      are exactly one bfp16 block.
-// Software pipeline: the global loads of K-step k+1 are issued as step k
-// starts, and step k+1 is expanded into the other LDS buffer in between step
-// k's later MFMAs; one barrier closes each step. Accumulation is fp32 throughout,
-// and the store is fp32 row-major, as the reference's output mode 0
-// (kernels/bfp16_gemm/aie_kernels/aie2p/mm_bfp_acc.cc:106-116, 258-278).
-//
-// LDS: [A buf 0][A buf 1][W buf 0][W buf 1], each BM (or BN) rows of 128
-// bytes, so every fragment and store address is a per-lane base plus an
-// immediate offset (buffer, MFMA tile, unit) and the address registers stay
-// few.
+// Per workgroup a BM x BN output tile, in K-steps of 64 (one tile-layout
+// column chunk), by two kinds of waves:
+//   * producer waves copy the A slab (bf16) from memory straight into LDS
+//     (buffer loads with the LDS-DMA bit), and load the W slab (bfp16 units:
+//     16 mantissas + their 2 exponent bytes), expand the W units losslessly to
+//     bf16 (zest::expand16) and store them into LDS; LDS rows are 64 bf16
+//     with the 16-byte chunks XOR-swizzled by row so the stores and the MFMA
+//     fragment reads are free of bank conflicts;
+//   * consumer waves read fragments from LDS and run
+//     v_mfma_f32_32x32x16_bf16, each lane's eight K values of an operand
+//     exactly one bfp16 block, accumulating in fp32.
+// One consumer and one producer wave share each SIMD, so the producer's
+// expansion and the consumer's MFMAs issue side by side. Three LDS stages:
+// while the consumers work on step k, the producers fill step k+2, and step
+// k+1 is complete, so the consumers read its first fragments before step k
+// ends. One barrier per K-step. The store is fp32 row-major, as the
+// reference's output mode 0 (kernels/bfp16_gemm/aie_kernels/aie2p/
+// mm_bfp_acc.cc:106-116, 258-278).
 #include "zest_common.h"
 #include "zest_device.h"
+
+#ifndef ZEST_GEMM_XCD
+#define ZEST_GEMM_XCD 1  // XCD-aware workgroup -> tile order
+#endif
+#ifndef ZEST_GEMM_GROUP_M
+#define ZEST_GEMM_GROUP_M 4  // tile rows per group of the tile order
+#endif
 
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-struct unit_regs {
-    uint4 m;
-    uint32_t e;
-};
-
-// BM x BN tile over WGM x WGN waves; DEPTH 1 or 2 staging register sets (how
-// many K-steps ahead the global loads run); the next step's expansion starts
-// after sub-step EXP_START of the current one.
-template <int BM_, int BN_, int WGM_, int WGN_, int DEPTH_ = 2, int EXP_START_ = 0>
+// BM x BN tile; CWM x CWN consumer waves, each a WM x WN block of 32x32 MFMA
+// tiles; as many producer waves.
+template <int BM_, int BN_, int CWM_, int CWN_>
 struct gemm_cfg {
-    static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, DEPTH = DEPTH_, EXP_START = EXP_START_;
-    static constexpr int NT = 64 * WGM * WGN;
-    static constexpr int WM = BM / WGM, WN = BN / WGN;
+    static constexpr int BM = BM_, BN = BN_, CWM = CWM_, CWN = CWN_;
+    static constexpr int NC = 64 * CWM * CWN;  // consumer threads
+    static constexpr int NP = NC;              // producer threads
+    static constexpr int NT = NC + NP;
+    static constexpr int WM = BM / CWM, WN = BN / CWN;
     static constexpr int TI = WM / 32, TJ = WN / 32;
-    static constexpr int AU = BM * 4 / NT, BU = BN * 4 / NT;  // units per thread per K-step
-    static constexpr int U = AU + BU;
-    static constexpr int ROWB = 128;                          // LDS bytes per row (64 bf16)
-    static constexpr int A_BUF = BM * ROWB, W_BUF = BN * ROWB;
-    static constexpr int W_BASE = 2 * A_BUF;
-    static constexpr size_t LDS_BYTES = 2 * (A_BUF + W_BUF);
-    static constexpr int UNIT_ROWS = NT / 4;                  // rows between a thread's units
-    static_assert(BM * 4 % NT == 0 && BN * 4 % NT == 0, "units must divide evenly");
+    static constexpr int AC = BM * 8 / NP;  // A chunks (16 B = one block) per producer thread per K-step
+    static constexpr int BU = BN * 4 / NP;  // W units (two blocks) per producer thread per K-step
+    static constexpr int ROWB = 128;        // LDS bytes per row (64 bf16)
+    static constexpr int A_BYTES = BM * ROWB;  // a stage: A rows, then W rows
+    static constexpr int STAGE = (BM + BN) * ROWB;
+    static constexpr int STAGES = 3;
+    static constexpr size_t LDS_BYTES = (size_t) STAGES * STAGE;
+    static constexpr int A_STEP = NP * 16;                     // bytes between a thread's A chunks
+    static constexpr int W_STEP = NP / 64 * ZEST_TILE_BYTES;  // bytes between a thread's W units
+    static_assert(BM * 8 % NP == 0 && BN * 4 % NP == 0, "work must divide evenly");
     static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be whole 32x32 MFMA tiles");
 };
 
-// Unit u of a slab: tile u/64, within it row (u%64)/4 and column quarter u%4.
-// Its mantissas are at tile*1152 + (u%64)*16, its exponents at
-// tile*1152 + 1024 + (u%64)*2. Loads go through buffer resources: the slab's
-// byte offset is wave-uniform (a scalar offset), the lane's place in it a
-// fixed vector offset, and a read past the operand returns zeros.
-struct slab_reader {
-    __amdgpu_buffer_rsrc_t rsrc;
-    int vm, ve;  // lane offsets of unit `tid`'s mantissas and exponents
-};
-
-// Lane -> unit within each 64-unit (one tile) group: row l%16, column
-// quarter l/16, so 16 consecutive lanes handle 16 consecutive rows (see the
-// LDS swizzle). A wave's load still covers the tile's 1 KB of mantissas and
-// 128 bytes of exponents exactly.
-__device__ inline int unit_of_lane(int tid) { return (tid & 15) * 4 + ((tid >> 4) & 3); }
-
-__device__ inline slab_reader make_reader(const uint8_t * base, int64_t bytes, int tid) {
-    slab_reader r;
-    r.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), (short) 0, (int) bytes, 0x00020000);
-    const int c = unit_of_lane(tid);
-    r.vm = (tid >> 6) * ZEST_TILE_BYTES + c * 16;
-    r.ve = (tid >> 6) * ZEST_TILE_BYTES + ZEST_TILE_MANT + c * 2;
-    return r;
-}
-
-__device__ inline unit_regs load_unit(const slab_reader & rd, int soff) {
-    unit_regs r;
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(rd.rsrc, rd.vm, soff, 0);
-    r.m = make_uint4(v[0], v[1], v[2], v[3]);
-    r.e = __builtin_amdgcn_raw_buffer_load_b16(rd.rsrc, rd.ve, soff, 0);
-    return r;
-}
-
-// Thread tid's units of one K-step are tid + i*NT: i*NT/64 tiles further on.
-template <class C>
-__device__ inline void load_step(unit_regs (&st)[C::U], const slab_reader & ra, int a_off, const slab_reader & rw,
-                                 int w_off) {
-    constexpr int STEP = C::NT / 64 * ZEST_TILE_BYTES;
-#pragma unroll
-    for (int i = 0; i < C::AU; i++) st[i] = load_unit(ra, a_off + i * STEP);
-#pragma unroll
-    for (int i = 0; i < C::BU; i++) st[C::AU + i] = load_unit(rw, w_off + i * STEP);
-}
-
-// LDS rows are 128 bytes = 8 chunks of 16 bytes (one bfp16 block as bf16
-// each); chunk c of row r is stored at position c ^ swz(r), with
-// swz(r) = (r % 8) ^ ((r / 8) % 2). Any 16 consecutive rows (from a multiple
-// of 16) then put one chunk index in 16 different 16-byte slots of a 256-byte
-// window, and any 8 consecutive rows in 8 slots of a 128-byte window: the
-// fragment reads (16 lanes = 16 rows, one chunk) and the unit stores (16 lanes
-// = 16 rows, one chunk) are free of bank conflicts, and swz is unchanged by
-// the +32-row offsets of the MFMA tiles, which stay immediates.
+// LDS rows are 128 bytes = 8 chunks of 16 bytes (one block as bf16 each);
+// chunk c of row r is stored at position c ^ swz(r), with
+// swz(r) = (r % 8) ^ ((r / 8) % 2). Any 8 consecutive rows of one chunk
+// index then fall in 8 different 16-byte bank groups, and swz depends only on
+// r % 16, so the +32-row offsets of the MFMA tiles stay immediates.
 __device__ inline int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
-// Per-lane LDS byte offsets. Unit tid + i*NT is row (tid/64)*16 + tid%16 +
-// i*NT/4 of its slab, chunks 2q, 2q+1 (q = (tid/16)%4).
-struct lds_lanes {
-    int st0, st1;      // unit-store chunks 2q and 2q+1 (A buffer 0; the rest as immediates)
-    int fa[4], fw[4];  // fragment reads for sub-steps s = 0..3
-};
+__device__ inline void lds_put(uint8_t * smem, int off, uint4 v) { *reinterpret_cast<uint4 *>(smem + off) = v; }
 
-template <class C>
-__device__ inline lds_lanes make_lanes(int tid) {
-    lds_lanes l;
-    const int row = (tid >> 6) * 16 + (tid & 15), q = (tid >> 4) & 3, sw = swz(row);
-    l.st0 = row * C::ROWB + ((2 * q) ^ sw) * 16;
-    l.st1 = row * C::ROWB + ((2 * q + 1) ^ sw) * 16;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / C::WGN, wn = wave % C::WGN, khalf = lane >> 5;
-    const int ar = wm * C::WM + (lane & 31), wr = wn * C::WN + (lane & 31);
-#pragma unroll
-    for (int s = 0; s < 4; s++) {
-        const int ch = 2 * s + khalf;
-        l.fa[s] = ar * C::ROWB + (ch ^ swz(ar)) * 16;
-        l.fw[s] = C::W_BASE + wr * C::ROWB + (ch ^ swz(wr)) * 16;
-    }
-    return l;
-}
-
-__device__ inline void lds_put(uint8_t * smem, int off, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-    *reinterpret_cast<uint4 *>(smem + off) = make_uint4(a, b, c, d);
+// The same store, opaque to the compiler's wait-count tracking: it would
+// otherwise make the store wait for every LDS DMA in flight (it cannot tell
+// that they write other bytes). Used only by producer waves, which never read
+// LDS; the barrier that publishes a stage waits for all LDS traffic.
+__device__ inline void lds_put_async(uint8_t * smem, int off, uint4 v) {
+    const uint32_t a = (uint32_t) reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t *) (smem + off));
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 d = {v.x, v.y, v.z, v.w};
+    asm volatile("ds_write_b128 %0, %1" ::"v"(a), "v"(d) : "memory");
 }
 
 __device__ inline bf16x8 lds_get(const uint8_t * smem, int off) {
     return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(smem + off));
 }
 
-// Expands units [first, last) of a step's staging registers into LDS buffer BUF.
-template <class C, int BUF>
-__device__ inline void store_units(const unit_regs (&st)[C::U], uint8_t * smem, const lds_lanes & ll, int first,
-                                   int last) {
-#pragma unroll
-    for (int i = 0; i < C::U; i++) {
-        if (i < first || i >= last) continue;
-        const int base = i < C::AU ? BUF * C::A_BUF + i * C::UNIT_ROWS * C::ROWB
-                                   : C::W_BASE + BUF * C::W_BUF + (i - C::AU) * C::UNIT_ROWS * C::ROWB;
-        uint32_t b[8];  // prologue only: the general expansion
-        zest::expand16(st[i].m, st[i].e, b);
-        lds_put(smem, ll.st0 + base, b[0], b[1], b[2], b[3]);
-        lds_put(smem, ll.st1 + base, b[4], b[5], b[6], b[7]);
+__device__ inline uint4 load16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// A producer thread's registers for one K-step's W units.
+template <class C>
+struct stage_regs {
+    uint4 wm[C::BU];
+    uint32_t we[C::BU];
+};
+
+typedef __attribute__((address_space(3))) void * lds_ptr_t;
+
+// s_waitcnt vmcnt(0) lgkmcnt(0): every load, DMA and LDS store of this wave done
+#define ZEST_WAIT_ALL() __builtin_amdgcn_s_waitcnt(7 << 4)
+
+// The producer side. Loads go through buffer resources: the slab's byte
+// offset is wave-uniform (a scalar offset), the lane's place in it a fixed
+// vector offset, and a read past the operand returns zeros.
+//   A: the K-step's A slab (BM rows of 128 bytes) is one contiguous run (BM/16
+//      consecutive 2 KB tiles). It goes straight from memory into LDS
+//      (buffer_load ... lds): instruction j of the step fills LDS rows
+//      8j..8j+7, lane l writing the 16 bytes at 16*l, i.e. row 8j + l/8,
+//      position l%8. The swizzle is applied on the source side: lane l reads
+//      the chunk that belongs at that position, (l%8) ^ swz(row).
+//   W: unit p + i*NP of the W slab is tile (p + i*NP)/64, and in it lane
+//      l = p%64 takes row l%16, column quarter l/16%4 (16 consecutive lanes
+//      = 16 consecutive rows, for the swizzled stores), through registers:
+//      loaded a step ahead, expanded, stored.
+template <class C>
+struct producer {
+    static constexpr int NPW = C::NP / 64;          // producer waves
+    static constexpr int AI = C::BM / 8 / NPW;      // A instructions per producer wave per K-step
+    __amdgpu_buffer_rsrc_t ra, rw;
+    int pw;                // producer wave
+    int va, vwm, vwe;      // lane offsets: A chunk, W mantissas, W exponents
+    int stw0, stw1;        // LDS offsets of the first W unit's two chunks
+
+    __device__ producer(const uint8_t * A, int64_t a_bytes, const uint8_t * W, int64_t w_bytes, int p) {
+        ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(A), (short) 0, (int) a_bytes, 0x00020000);
+        rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(W), (short) 0, (int) w_bytes, 0x00020000);
+        pw = __builtin_amdgcn_readfirstlane(p >> 6);
+        const int l = p & 63;
+        // instruction j = i*NPW + pw: j and pw have the same parity, so
+        // swz(8j + l/8) is the same for every i
+        va = pw * 1024 + (l >> 3) * 128 + ((l & 7) ^ swz(8 * (pw & 1) + (l >> 3))) * 16;
+        const int u = (l & 15) * 4 + ((l >> 4) & 3);
+        vwm = (p >> 6) * ZEST_TILE_BYTES + u * 16;
+        vwe = (p >> 6) * ZEST_TILE_BYTES + ZEST_TILE_MANT + u * 2;
+        const int wrow = (p >> 6) * 16 + (l & 15), q = (l >> 4) & 3, sw = swz(wrow);
+        stw0 = C::A_BYTES + wrow * C::ROWB + ((2 * q) ^ sw) * 16;
+        stw1 = C::A_BYTES + wrow * C::ROWB + ((2 * q + 1) ^ sw) * 16;
     }
-}
+
+    // The A slab at byte a_off into the stage at byte `stage` of LDS.
+    __device__ void dma_a(uint8_t * smem, int stage, int a_off) const {
+#pragma unroll
+        for (int i = 0; i < AI; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t) (smem + stage + (i * NPW + pw) * 1024), 16, va,
+                                                     a_off + i * NPW * 1024, 0, 0);
+    }
+
+    __device__ void load_w(stage_regs<C> & st, int w_off) const {
+#pragma unroll
+        for (int i = 0; i < C::BU; i++) {
+            st.wm[i] = load16(rw, vwm, w_off + i * C::W_STEP);
+            st.we[i] = __builtin_amdgcn_raw_buffer_load_b16(rw, vwe, w_off + i * C::W_STEP, 0);
+        }
+    }
+
+    // W unit i is row +i*NP/4 (a multiple of 16 rows, so the swizzle is the
+    // first unit's). The units take the branch-free fast expansion; a unit
+    // whose exponent bytes need the general one is redone behind a single
+    // wave-uniform branch, which real weights almost never take.
+    __device__ void store_w(const stage_regs<C> & st, uint8_t * smem, int stage) const {
+        bool slow = false;
+#pragma unroll
+        for (int i = 0; i < C::BU; i++) {
+            uint32_t b[8];
+            slow |= zest::expand16_fast(st.wm[i], st.we[i], b);
+            const int off = stage + i * (C::NP / 4) * C::ROWB;
+            lds_put_async(smem, stw0 + off, make_uint4(b[0], b[1], b[2], b[3]));
+            lds_put_async(smem, stw1 + off, make_uint4(b[4], b[5], b[6], b[7]));
+        }
+        if (__builtin_expect(__any(slow), 0)) {
+#pragma unroll
+            for (int i = 0; i < C::BU; i++) {
+                uint32_t b[8];
+                zest::expand16(st.wm[i], st.we[i], b);
+                const int off = stage + i * (C::NP / 4) * C::ROWB;
+                lds_put_async(smem, stw0 + off, make_uint4(b[0], b[1], b[2], b[3]));
+                lds_put_async(smem, stw1 + off, make_uint4(b[4], b[5], b[6], b[7]));
+            }
+        }
+    }
+};
 
 template <class C>
-__device__ inline int unit_base(int i, int buf) {
-    return i < C::AU ? buf * C::A_BUF + i * C::UNIT_ROWS * C::ROWB
-                     : C::W_BASE + buf * C::W_BUF + (i - C::AU) * C::UNIT_ROWS * C::ROWB;
+__device__ inline void read_frags(bf16x8 (&af)[C::TI], bf16x8 (&bw)[C::TJ], const uint8_t * smem, int fa, int fw) {
+#pragma unroll
+    for (int i = 0; i < C::TI; i++) af[i] = lds_get(smem, fa + i * 32 * C::ROWB);
+#pragma unroll
+    for (int j = 0; j < C::TJ; j++) bw[j] = lds_get(smem, fw + j * 32 * C::ROWB);
 }
 
+// One K-step of a consumer wave on the stage at byte `cur`: 4 sub-steps of 16
+// K. The fragments of the next sub-step (sub-step 0 of stage `nxt` after the
+// last, if `more`) are read while this sub-step's MFMAs run; the scheduling
+// barriers keep those reads ahead of the MFMAs, so the two fragment sets live
+// in separate registers.
 template <class C>
-__device__ inline void read_frags(bf16x8 (&af)[C::TI], bf16x8 (&bfr)[C::TJ], const uint8_t * smem,
-                                  const lds_lanes & ll, int s, int cur) {
-#pragma unroll
-    for (int i = 0; i < C::TI; i++) af[i] = lds_get(smem, ll.fa[s] + cur * C::A_BUF + i * 32 * C::ROWB);
-#pragma unroll
-    for (int j = 0; j < C::TJ; j++) bfr[j] = lds_get(smem, ll.fw[s] + cur * C::W_BUF + j * 32 * C::ROWB);
-}
-
-// One K-step on LDS buffer CUR: 4 sub-steps of 16 K. If LOAD, the next
-// step's units are requested from memory first, into the staging registers
-// `st`; they arrive while sub-steps 0..EXP_START-1 run and are expanded (fast
-// path, branch-free) and stored to the other LDS buffer in between the MFMAs
-// of the later sub-steps. The fragments of sub-step s+1 are read while
-// sub-step s's TI*TJ MFMAs run. The scheduling pattern below interleaves
-// MFMAs, VALU and LDS operations so the matrix core and the VALU work at the
-// same time (one wave per SIMD, in-order issue). Units whose exponent bytes
-// need the general expansion are redone after the MFMAs, behind a
-// wave-uniform branch that real data almost never takes.
-template <class C, int CUR, bool LOAD, bool EXPAND>
-__device__ inline void mma_step(f32x16 (&acc)[C::TI][C::TJ], uint8_t * smem, const lds_lanes & ll,
-                                unit_regs (&sl)[C::U], unit_regs (&st)[C::U], const slab_reader & ra, int a_off,
-                                const slab_reader & rw, int w_off) {
-    constexpr int EXP_START = C::EXP_START;
-    constexpr int EXP_STEPS = 4 - EXP_START;
-    if (LOAD) load_step<C>(sl, ra, a_off, rw, w_off);
-    bf16x8 af[2][C::TI], bfr[2][C::TJ];
-    read_frags<C>(af[0], bfr[0], smem, ll, 0, CUR);
-    bool slow[C::U];
+__device__ inline void consume(f32x16 (&acc)[C::TI][C::TJ], bf16x8 (&af)[2][C::TI], bf16x8 (&bw)[2][C::TJ],
+                               const uint8_t * smem, const int (&fa)[4], const int (&fw)[4], int cur, int nxt,
+                               bool more) {
 #pragma unroll
     for (int s = 0; s < 4; s++) {
-        if (s < 3) read_frags<C>(af[(s + 1) & 1], bfr[(s + 1) & 1], smem, ll, s + 1, CUR);
+        if (s < 3)
+            read_frags<C>(af[(s + 1) & 1], bw[(s + 1) & 1], smem, fa[s + 1] + cur, fw[s + 1] + cur);
+        else if (more)
+            read_frags<C>(af[0], bw[0], smem, fa[0] + nxt, fw[0] + nxt);
 #pragma unroll
         for (int i = 0; i < C::TI; i++)
 #pragma unroll
             for (int j = 0; j < C::TJ; j++)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s & 1][i], bfr[s & 1][j], acc[i][j], 0, 0, 0);
-        if (EXPAND && s >= EXP_START) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s & 1][i], bw[s & 1][j], acc[i][j], 0, 0, 0);
+        constexpr int R = C::TI + C::TJ, P = C::TI * C::TJ;
 #pragma unroll
-            for (int u = (s - EXP_START) * C::U / EXP_STEPS; u < (s - EXP_START + 1) * C::U / EXP_STEPS; u++) {
-                uint32_t b[8];
-                slow[u] = zest::expand16_fast(st[u].m, st[u].e, b);
-                const int base = unit_base<C>(u, CUR ^ 1);
-                lds_put(smem, ll.st0 + base, b[0], b[1], b[2], b[3]);
-                lds_put(smem, ll.st1 + base, b[4], b[5], b[6], b[7]);
-            }
-        }
-    }
-    // the scheduling pattern: per MFMA, VALU ops (expansion sub-steps only),
-    // a fragment read every other MFMA, LDS stores spread over the expansion
-    constexpr int PER = C::TI * C::TJ;  // MFMAs per sub-step
-    constexpr int MFMAS = 4 * PER;
-    constexpr int EXP_MFMAS = EXP_STEPS * PER;
-    constexpr int VALU_PER = EXPAND ? (C::U * 34 + EXP_MFMAS - 1) / EXP_MFMAS : 0;
-    constexpr int STORES = EXPAND ? 2 * C::U : 0;
-    constexpr int READS = 3 * (C::TI + C::TJ);
-    constexpr int LOADS = LOAD ? 2 * C::U : 0;
-#ifndef ZEST_GEMM_SCHED
-#define ZEST_GEMM_SCHED 1
-#endif
-    if (ZEST_GEMM_SCHED) __builtin_amdgcn_sched_group_barrier(0x100, C::TI + C::TJ, 0);  // sub-step 0's fragments
-#pragma unroll
-    for (int q = 0; q < (ZEST_GEMM_SCHED ? MFMAS : 0); q++) {
-        if (q < LOADS) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // next step's loads, early
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                // MFMA
-        if (q * READS / MFMAS != (q + 1) * READS / MFMAS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        if (q >= MFMAS - EXP_MFMAS) {
-            const int e = q - (MFMAS - EXP_MFMAS);
-            if (VALU_PER) __builtin_amdgcn_sched_group_barrier(0x002, VALU_PER, 0);
-            if (STORES && e * STORES / EXP_MFMAS != (e + 1) * STORES / EXP_MFMAS)
-                __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
-        }
-    }
-    if (EXPAND) {
-        bool any = false;
-#pragma unroll
-        for (int u = 0; u < C::U; u++) any |= slow[u];
-        if (__builtin_expect(__any(any), 0)) {
-#pragma unroll
-            for (int u = 0; u < C::U; u++)
-                if (slow[u]) {
-                    uint32_t b[8];
-                    zest::expand16(st[u].m, st[u].e, b);
-                    const int base = unit_base<C>(u, CUR ^ 1);
-                    lds_put(smem, ll.st0 + base, b[0], b[1], b[2], b[3]);
-                    lds_put(smem, ll.st1 + base, b[4], b[5], b[6], b[7]);
-                }
+        for (int q = 0; q < P; q++) {
+            if (q < R) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // a fragment read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);              // an MFMA
         }
     }
 }
@@ -293,76 +257,102 @@ __global__ __launch_bounds__(C::NT, 1) void gemm_kernel(const uint8_t * __restri
                                                         uint32_t * nonfinite) {
     extern __shared__ uint4 smem_u4[];
     uint8_t * smem = reinterpret_cast<uint8_t *>(smem_u4);
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / C::WGN, wn = wave % C::WGN;
-    const int64_t m0 = (int64_t) blockIdx.y * C::BM, n0 = (int64_t) blockIdx.x * C::BN;
-
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int64_t m0, n0;
+    {
+        // Workgroups go to the 8 XCDs round-robin by linear id; give each XCD
+        // a contiguous run of tiles, and walk tiles in groups of GROUP_M tile
+        // rows (M-fastest inside a group), so the ~32 workgroups resident on
+        // one XCD cover a compact block of about 4 x 8 tiles and share their
+        // A and W slabs in its L2.
+        const int G = (int) gridDim.x, b = (int) blockIdx.x;
+        const int mt = (int) ((M + C::BM - 1) / C::BM), nt = (int) ((N + C::BN - 1) / C::BN);
+#if ZEST_GEMM_XCD
+        const int q = G / 8, r = G % 8, x = b % 8;
+        const int t = x * q + min(x, r) + b / 8;
+#else
+        const int t = b;
+#endif
+        const int per_group = ZEST_GEMM_GROUP_M * nt, first_m = t / per_group * ZEST_GEMM_GROUP_M;
+        const int gm = min(mt - first_m, ZEST_GEMM_GROUP_M), in = t % per_group;
+        m0 = (int64_t) (first_m + in % gm) * C::BM;
+        n0 = (int64_t) (in / gm) * C::BN;
+        (void) G;
+    }
     // operands are < 2 GiB (checked by the host), so byte offsets fit an int
-    const int a_kstride = (int) ((M_pad / ZEST_TILE_ROWS) * ZEST_TILE_BYTES);
+    const int a_kstride = (int) ((M_pad / ZEST_TILE_ROWS) * ZEST_XTILE_BYTES);
     const int w_kstride = (int) ((N_pad / ZEST_TILE_ROWS) * ZEST_TILE_BYTES);
-    const int a0 = (int) ((m0 / ZEST_TILE_ROWS) * ZEST_TILE_BYTES);
-    const int w0 = (int) ((n0 / ZEST_TILE_ROWS) * ZEST_TILE_BYTES);
-    const slab_reader ra = make_reader(A, (int64_t) a_kstride * nk, tid);
-    const slab_reader rw = make_reader(W, (int64_t) w_kstride * nk, tid);
-    const lds_lanes ll = make_lanes<C>(tid);
 
+    if (wave >= C::NC / 64) {
+        // Producer. During step k, step k+2 goes into stage (k+2)%3: first its
+        // A slab by DMA, then step k+3's W units are requested, then step
+        // k+2's W units (requested during step k+1) are expanded and stored.
+        // The barrier that ends the step waits for all of it. The barriers
+        // match the consumer loop's, step for step.
+        const int a0 = (int) ((m0 / ZEST_TILE_ROWS) * ZEST_XTILE_BYTES);
+        const int w0 = (int) ((n0 / ZEST_TILE_ROWS) * ZEST_TILE_BYTES);
+        const producer<C> pr(A, (int64_t) a_kstride * nk, W, (int64_t) w_kstride * nk, tid - C::NC);
+        stage_regs<C> s0, s1;
+        pr.dma_a(smem, 0, a0);
+        pr.load_w(s0, w0);
+        if (nk > 1) {
+            pr.dma_a(smem, C::STAGE, a0 + a_kstride);
+            pr.load_w(s1, w0 + w_kstride);
+        }
+        pr.store_w(s0, smem, 0);
+        if (nk > 2) pr.load_w(s0, w0 + 2 * w_kstride);
+        if (nk > 1) pr.store_w(s1, smem, C::STAGE);
+        ZEST_WAIT_ALL();
+        __syncthreads();
+        int stage = 2 * C::STAGE;
+        for (int k = 0; k < nk; k += 2) {
+            if (k + 2 < nk) {
+                pr.dma_a(smem, stage, a0 + (k + 2) * a_kstride);
+                if (k + 3 < nk) pr.load_w(s1, w0 + (k + 3) * w_kstride);
+                pr.store_w(s0, smem, stage);
+            }
+            stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
+            ZEST_WAIT_ALL();
+            __syncthreads();
+            if (k + 1 < nk) {
+                if (k + 3 < nk) {
+                    pr.dma_a(smem, stage, a0 + (k + 3) * a_kstride);
+                    if (k + 4 < nk) pr.load_w(s0, w0 + (k + 4) * w_kstride);
+                    pr.store_w(s1, smem, stage);
+                }
+                stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
+                ZEST_WAIT_ALL();
+                __syncthreads();
+            }
+        }
+        return;
+    }
+
+    // Consumer.
+    const int wm = wave / C::CWN, wn = wave % C::CWN, khalf = lane >> 5;
+    const int ar = wm * C::WM + (lane & 31), wr = wn * C::WN + (lane & 31);
+    int fa[4], fw[4];
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        fa[s] = ar * C::ROWB + ((2 * s + khalf) ^ swz(ar)) * 16;
+        fw[s] = C::A_BYTES + wr * C::ROWB + ((2 * s + khalf) ^ swz(wr)) * 16;
+    }
     f32x16 acc[C::TI][C::TJ];
 #pragma unroll
     for (int i = 0; i < C::TI; i++)
 #pragma unroll
         for (int j = 0; j < C::TJ; j++) acc[i][j] = f32x16{};
-    if (C::DEPTH == 1) {
-        // Step k computes on buffer k&1 and, unless it is the last, loads
-        // step k+1 as it starts and expands it into the other buffer.
-        unit_regs st[C::U];
-        load_step<C>(st, ra, a0, rw, w0);
-        store_units<C, 0>(st, smem, ll, 0, C::U);
+    bf16x8 af[2][C::TI], bw[2][C::TJ];
+    __syncthreads();
+    read_frags<C>(af[0], bw[0], smem, fa[0], fw[0]);
+    int cur = 0;
+    for (int k = 0; k < nk; k++) {
+        const int nxt = cur == 2 * C::STAGE ? 0 : cur + C::STAGE;
+        consume<C>(acc, af, bw, smem, fa, fw, cur, nxt, k + 1 < nk);
+        cur = nxt;
         __syncthreads();
-        int kc = 0;
-        for (; kc + 2 < nk; kc += 2) {
-            mma_step<C, 0, true, true>(acc, smem, ll, st, st, ra, a0 + (kc + 1) * a_kstride, rw, w0 + (kc + 1) * w_kstride);
-            __syncthreads();
-            mma_step<C, 1, true, true>(acc, smem, ll, st, st, ra, a0 + (kc + 2) * a_kstride, rw, w0 + (kc + 2) * w_kstride);
-            __syncthreads();
-        }
-        if (kc + 1 < nk) {  // 2 left
-            mma_step<C, 0, true, true>(acc, smem, ll, st, st, ra, a0 + (kc + 1) * a_kstride, rw, w0 + (kc + 1) * w_kstride);
-            __syncthreads();
-            mma_step<C, 1, false, false>(acc, smem, ll, st, st, ra, 0, rw, 0);
-        } else {  // 1 left
-            mma_step<C, 0, false, false>(acc, smem, ll, st, st, ra, 0, rw, 0);
-        }
-    } else {
-        // Two staging sets: step k loads step k+2 into one while expanding
-        // step k+1 (loaded during step k-1) from the other.
-        unit_regs sa[C::U], sb[C::U];
-        load_step<C>(sa, ra, a0, rw, w0);
-        if (nk > 1) load_step<C>(sb, ra, a0 + a_kstride, rw, w0 + w_kstride);
-        store_units<C, 0>(sa, smem, ll, 0, C::U);
-        __syncthreads();
-        int kc = 0;
-        for (; kc + 3 < nk; kc += 2) {
-            mma_step<C, 0, true, true>(acc, smem, ll, sa, sb, ra, a0 + (kc + 2) * a_kstride, rw, w0 + (kc + 2) * w_kstride);
-            __syncthreads();
-            mma_step<C, 1, true, true>(acc, smem, ll, sb, sa, ra, a0 + (kc + 3) * a_kstride, rw, w0 + (kc + 3) * w_kstride);
-            __syncthreads();
-        }
-        if (kc + 2 < nk) {  // 3 left
-            mma_step<C, 0, true, true>(acc, smem, ll, sa, sb, ra, a0 + (kc + 2) * a_kstride, rw, w0 + (kc + 2) * w_kstride);
-            __syncthreads();
-            mma_step<C, 1, false, true>(acc, smem, ll, sb, sa, ra, 0, rw, 0);
-            __syncthreads();
-            mma_step<C, 0, false, false>(acc, smem, ll, sa, sb, ra, 0, rw, 0);
-        } else if (kc + 1 < nk) {  // 2 left
-            mma_step<C, 0, false, true>(acc, smem, ll, sa, sb, ra, 0, rw, 0);
-            __syncthreads();
-            mma_step<C, 1, false, false>(acc, smem, ll, sa, sb, ra, 0, rw, 0);
-        } else {  // 1 left
-            mma_step<C, 0, false, false>(acc, smem, ll, sa, sb, ra, 0, rw, 0);
-        }
     }
-
     store_tile<C>(acc, Cout, M, N, ldc, m0, n0, wm, wn, lane, nonfinite);
 }
 
@@ -377,20 +367,22 @@ int launch(const void * a, int64_t M, const void * w, int64_t N, int64_t K, floa
         attr_set = true;
     }
     const int64_t M_pad = zest_rows_padded(M), N_pad = zest_rows_padded(N), K_pad = zest_k_padded(K);
-    const dim3 grid((unsigned) ((N + C::BN - 1) / C::BN), (unsigned) ((M + C::BM - 1) / C::BM));
+    const dim3 grid((unsigned) (((N + C::BN - 1) / C::BN) * ((M + C::BM - 1) / C::BM)));
     hipLaunchKernelGGL((gemm_kernel<C>), grid, dim3(C::NT), C::LDS_BYTES, s, (const uint8_t *) a, M_pad,
                        (const uint8_t *) w, N_pad, (int) (K_pad / ZEST_TILE_K), c, M, N, ldc, nf);
     return zest::check_launch("zest_gemm");
 }
 
-// Measured on MI355X over the BASELINE shapes: 256x128 tiles on 8 waves
-// (128x32 each) with two staging sets lead wherever there are enough tiles;
-// 128x128 on 4 waves for the narrow ones (K/V projections).
+// 256x128 tiles (4 consumer waves of 128x64) wherever there are enough
+// tiles; 128x128 (64x64 each) for the narrow shapes.
 #ifndef ZEST_GEMM_BIG
-#define ZEST_GEMM_BIG 256, 128, 2, 4, 2, 0
+#define ZEST_GEMM_BIG 256, 128, 2, 2
 #endif
 #ifndef ZEST_GEMM_SMALL
-#define ZEST_GEMM_SMALL 128, 128, 2, 2, 2, 0
+#define ZEST_GEMM_SMALL 128, 128, 2, 2
+#endif
+#ifndef ZEST_GEMM_BIG_MIN_TILES
+#define ZEST_GEMM_BIG_MIN_TILES 160
 #endif
 using cfg_big = gemm_cfg<ZEST_GEMM_BIG>;
 using cfg_small = gemm_cfg<ZEST_GEMM_SMALL>;
@@ -403,15 +395,11 @@ extern "C" int zest_gemm(const void * a, int64_t M, const void * w, int64_t N, i
     ZEST_REQUIRE(M > 0 && N > 0 && K > 0 && K % 8 == 0, "zest_gemm: M=%lld N=%lld K=%lld", (long long) M,
                  (long long) N, (long long) K);
     ZEST_REQUIRE(ldc >= N, "zest_gemm: ldc %lld < N %lld", (long long) ldc, (long long) N);
-    ZEST_REQUIRE(zest_bfp16_bytes(M, K) < (1ull << 31) && zest_bfp16_bytes(N, K) < (1ull << 31) &&
+    ZEST_REQUIRE(zest_act_bytes(M, K) < (1ull << 31) && zest_bfp16_bytes(N, K) < (1ull << 31) &&
                      (uint64_t) zest_rows_padded(M) * (uint64_t) ldc * 4 < (1ull << 31),
                  "zest_gemm: operands and output must be under 2 GiB (M=%lld N=%lld K=%lld ldc=%lld)", (long long) M,
                  (long long) N, (long long) K, (long long) ldc);
     hipStream_t s = zest::as_stream(stream);
-    // 256x256 tiles when they give the GPU enough workgroups, else 128x128
-#ifndef ZEST_GEMM_BIG_MIN_TILES
-#define ZEST_GEMM_BIG_MIN_TILES 160
-#endif
     const int64_t big_tiles = ((M + cfg_big::BM - 1) / cfg_big::BM) * ((N + cfg_big::BN - 1) / cfg_big::BN);
     if (big_tiles >= ZEST_GEMM_BIG_MIN_TILES) return launch<cfg_big>(a, M, w, N, K, c, ldc, nonfinite, s);
     return launch<cfg_small>(a, M, w, N, K, c, ldc, nonfinite, s);

@@ -1,8 +1,9 @@
 // The small fp32 ops between the matmuls (piece::run_rows,
 // src/xdna-exec.cpp:253-346), as HBM-bound row kernels. RMS_NORM (+ the scale
-// row MUL after it) and the GLUs can also write the next matmul's packed bfp16
-// input directly, so a normalised or gated row goes HBM -> registers ->
-// packed operand without a round trip through an fp32 tensor.
+// row MUL after it) and the GLUs can also write the next matmul's input (the
+// bfp16 pack, stored expanded) directly, so a normalised or gated row goes
+// HBM -> registers -> matmul operand without a round trip through an fp32
+// tensor.
 #include "zest_common.h"
 #include "zest_device.h"
 
@@ -10,15 +11,10 @@ namespace {
 
 using zest::encode8;
 
-// Writes 16 values of packed row r, columns [col, col+16) (col % 16 == 0).
+// Writes 16 values of row r, columns [col, col+16) (col % 16 == 0), of the
+// next matmul's input: the bfp16 pack, stored expanded.
 __device__ inline void pack16(uint8_t * packed, int64_t R_pad, int64_t r, int64_t col, const float v[16]) {
-    uint4 m;
-    const uint32_t e0 = encode8(v, m.x, m.y);
-    const uint32_t e1 = encode8(v + 8, m.z, m.w);
-    uint8_t * tile = packed + zest_tile_offset(r / ZEST_TILE_ROWS, col / ZEST_TILE_K, R_pad);
-    const int64_t rr = r % ZEST_TILE_ROWS, q = (col % ZEST_TILE_K) / 16;
-    *reinterpret_cast<uint4 *>(tile + rr * ZEST_TILE_K + q * 16) = m;
-    *reinterpret_cast<uint16_t *>(tile + ZEST_TILE_MANT + rr * 8 + q * 2) = (uint16_t) (e0 | (e1 << 8));
+    zest::store_expanded16(packed, R_pad, r, col, v);
 }
 
 __device__ inline void load16(const float * p, float v[16], int64_t valid) {

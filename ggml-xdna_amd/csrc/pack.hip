@@ -1,8 +1,11 @@
-// The two HBM-bound converters of the path:
+// The HBM-bound converters of the path:
 //   zest_pack_act        fp32 activations -> packed bfp16 (per chunk)
+//   zest_pack_act_x      fp32 activations -> the GEMM's expanded operand: the
+//                        same bfp16 blocks, stored decoded as bf16
+//   zest_expand_act      packed bfp16 -> expanded operand
 //   zest_convert_weight  GGUF F32 / Q8_0 / Q4_K weights -> packed bfp16 (once,
 //                        into the resident weight cache)
-// Both write the tile layout of zest_layout.h with 16-byte mantissa stores.
+// All write the layouts of zest_layout.h with 16-byte stores.
 #include "zest_common.h"
 #include "zest_device.h"
 
@@ -14,6 +17,8 @@ using zest::encode8;
 // a 16-byte mantissa store and a 2-byte exponent store out. A workgroup is one
 // 16-row tile row by 256 columns (4 tiles): thread t takes row t/16 and the
 // 16-column quarter t%16. Rows past M and columns past K become zero blocks.
+// XOUT: write the expanded operand (two 16-byte bf16 stores) instead.
+template <bool XOUT>
 __global__ __launch_bounds__(256) void pack_act_kernel(const float * __restrict__ x, int64_t M, int64_t K, int64_t ldx,
                                                        uint8_t * __restrict__ dst, int64_t R_pad, int64_t K_pad) {
     const int t = threadIdx.x;
@@ -38,6 +43,10 @@ __global__ __launch_bounds__(256) void pack_act_kernel(const float * __restrict_
 #pragma unroll
         for (int i = 0; i < 16; i++) v[i] = (row_ok && col + i < K) ? x[r * ldx + col + i] : 0.0f;
     }
+    if (XOUT) {
+        zest::store_expanded16(dst, R_pad, r, col, v);
+        return;
+    }
     uint4 m;
     const uint32_t e0 = encode8(v, m.x, m.y);
     const uint32_t e1 = encode8(v + 8, m.z, m.w);
@@ -45,6 +54,23 @@ __global__ __launch_bounds__(256) void pack_act_kernel(const float * __restrict_
     const int rr = t >> 4, q = (t & 15) & 3;
     *reinterpret_cast<uint4 *>(tile + rr * ZEST_TILE_K + q * 16) = m;
     *reinterpret_cast<uint16_t *>(tile + ZEST_TILE_MANT + rr * 8 + q * 2) = (uint16_t) (e0 | (e1 << 8));
+}
+
+// One thread per 16-value unit of a packed operand: its mantissas and two
+// exponent bytes -> 16 bf16 of the expanded operand.
+__global__ __launch_bounds__(256) void expand_act_kernel(const uint8_t * __restrict__ src, uint8_t * __restrict__ dst,
+                                                         int64_t units) {
+    const int64_t u = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (u >= units) return;
+    const int64_t tile = u / 64, c = u % 64;  // unit c of a tile: row c/4, 16-column quarter c%4
+    const uint8_t * t = src + tile * ZEST_TILE_BYTES;
+    const uint4 m = *reinterpret_cast<const uint4 *>(t + c * 16);
+    const uint32_t e = *reinterpret_cast<const uint16_t *>(t + ZEST_TILE_MANT + c * 2);
+    uint32_t b[8];
+    zest::expand16(m, e, b);
+    uint4 * p = reinterpret_cast<uint4 *>(dst + tile * ZEST_XTILE_BYTES + c * 32);
+    p[0] = make_uint4(b[0], b[1], b[2], b[3]);
+    p[1] = make_uint4(b[4], b[5], b[6], b[7]);
 }
 
 __device__ inline float half_to_float(uint16_t h) { return (float) __builtin_bit_cast(_Float16, h); }
@@ -163,17 +189,42 @@ size_t zest_raw_row_bytes(int type, int64_t K) {
     }
 }
 
-int zest_pack_act(const float * x, int64_t M, int64_t K, int64_t ldx, void * dst, void * stream) {
-    ZEST_REQUIRE(x && dst, "zest_pack_act: null pointer");
-    ZEST_REQUIRE(M > 0 && K > 0 && K % 8 == 0, "zest_pack_act: M=%lld K=%lld (K must be a positive multiple of 8)",
+size_t zest_act_bytes(int64_t rows, int64_t K) { return (size_t) (zest_rows_padded(rows) * zest_k_padded(K) * 2); }
+
+static int pack_act(bool xout, const float * x, int64_t M, int64_t K, int64_t ldx, void * dst, void * stream,
+                    const char * name) {
+    ZEST_REQUIRE(x && dst, "%s: null pointer", name);
+    ZEST_REQUIRE(M > 0 && K > 0 && K % 8 == 0, "%s: M=%lld K=%lld (K must be a positive multiple of 8)", name,
                  (long long) M, (long long) K);
-    ZEST_REQUIRE(ldx >= K, "zest_pack_act: row stride %lld < K %lld", (long long) ldx, (long long) K);
-    ZEST_REQUIRE(aligned(x, 16) && aligned(dst, 16), "zest_pack_act: pointers must be 16-byte aligned");
+    ZEST_REQUIRE(ldx >= K, "%s: row stride %lld < K %lld", name, (long long) ldx, (long long) K);
+    ZEST_REQUIRE(aligned(x, 16) && aligned(dst, 16), "%s: pointers must be 16-byte aligned", name);
     const int64_t R_pad = zest_rows_padded(M), K_pad = zest_k_padded(K);
     const dim3 grid((unsigned) ((K_pad + 255) / 256), (unsigned) (R_pad / ZEST_TILE_ROWS));
-    hipLaunchKernelGGL(pack_act_kernel, grid, dim3(256), 0, zest::as_stream(stream), x, M, K, ldx, (uint8_t *) dst,
-                       R_pad, K_pad);
-    return zest::check_launch("zest_pack_act");
+    if (xout)
+        hipLaunchKernelGGL(pack_act_kernel<true>, grid, dim3(256), 0, zest::as_stream(stream), x, M, K, ldx,
+                           (uint8_t *) dst, R_pad, K_pad);
+    else
+        hipLaunchKernelGGL(pack_act_kernel<false>, grid, dim3(256), 0, zest::as_stream(stream), x, M, K, ldx,
+                           (uint8_t *) dst, R_pad, K_pad);
+    return zest::check_launch(name);
+}
+
+int zest_pack_act(const float * x, int64_t M, int64_t K, int64_t ldx, void * dst, void * stream) {
+    return pack_act(false, x, M, K, ldx, dst, stream, "zest_pack_act");
+}
+
+int zest_pack_act_x(const float * x, int64_t M, int64_t K, int64_t ldx, void * dst, void * stream) {
+    return pack_act(true, x, M, K, ldx, dst, stream, "zest_pack_act_x");
+}
+
+int zest_expand_act(const void * src, int64_t M, int64_t K, void * dst, void * stream) {
+    ZEST_REQUIRE(src && dst, "zest_expand_act: null pointer");
+    ZEST_REQUIRE(M > 0 && K > 0 && K % 8 == 0, "zest_expand_act: M=%lld K=%lld", (long long) M, (long long) K);
+    ZEST_REQUIRE(aligned(src, 16) && aligned(dst, 16), "zest_expand_act: pointers must be 16-byte aligned");
+    const int64_t units = zest_rows_padded(M) * zest_k_padded(K) / 16;
+    hipLaunchKernelGGL(expand_act_kernel, dim3((unsigned) ((units + 255) / 256)), dim3(256), 0,
+                       zest::as_stream(stream), (const uint8_t *) src, (uint8_t *) dst, units);
+    return zest::check_launch("zest_expand_act");
 }
 
 int zest_convert_weight(int type, const void * raw, int64_t N, int64_t K, void * dst, void * stream) {

@@ -84,12 +84,12 @@ int zest_self_test(void) {
     dev_buf da, dw, pa, pw, dc;
     HIP_OR_FAIL(hipMalloc(&da.p, a.size() * 4));
     HIP_OR_FAIL(hipMalloc(&dw.p, w.size() * 4));
-    HIP_OR_FAIL(hipMalloc(&pa.p, zest_bfp16_bytes(M, K)));
+    HIP_OR_FAIL(hipMalloc(&pa.p, zest_act_bytes(M, K)));
     HIP_OR_FAIL(hipMalloc(&pw.p, zest_bfp16_bytes(N, K)));
     HIP_OR_FAIL(hipMalloc(&dc.p, (size_t) (M * N) * 4));
     HIP_OR_FAIL(hipMemcpy(da.p, a.data(), a.size() * 4, hipMemcpyHostToDevice));
     HIP_OR_FAIL(hipMemcpy(dw.p, w.data(), w.size() * 4, hipMemcpyHostToDevice));
-    int st = zest_pack_act((const float *) da.p, M, K, K, pa.p, nullptr);
+    int st = zest_pack_act_x((const float *) da.p, M, K, K, pa.p, nullptr);
     if (st == ZEST_OK) st = zest_convert_weight(ZEST_TYPE_F32, dw.p, N, K, pw.p, nullptr);
     if (st == ZEST_OK) st = zest_gemm(pa.p, M, pw.p, N, K, (float *) dc.p, N, nullptr, nullptr);
     if (st != ZEST_OK) return st;

@@ -20,6 +20,15 @@
 //     is a whole number of 128-byte lines.
 // The bijection to the reference's row-major blocks is zest_block_offsets();
 // tests map our bytes through it and compare with the reference packer's.
+//
+// The GEMM's activation operand ("expanded" layout) holds the same bfp16
+// blocks already decoded, each value q * 2^(e-133) as the bf16 it is exactly
+// (a signed 8-bit mantissa times a power of two fits a bf16 significand):
+// rows padded to 256 and columns to 64 as above, tiles of 16 rows x 64
+// columns of 2048 bytes, tile (rt, kc) at byte (kc * R_pad/16 + rt) * 2048,
+// each tile row 128 bytes (8 blocks of 16 bytes). The activation packers
+// write it directly, so every activation value is expanded once rather than
+// once per output tile of the GEMM.
 #pragma once
 
 #include <stdint.h>
@@ -29,6 +38,7 @@
 #define ZEST_TILE_MANT 1024
 #define ZEST_TILE_BYTES 1152
 #define ZEST_ROW_ALIGN 256
+#define ZEST_XTILE_BYTES 2048
 
 #ifdef __HIPCC__
 #define ZEST_HD __host__ __device__ inline
@@ -43,6 +53,11 @@ ZEST_HD int64_t zest_k_padded(int64_t K) { return zest_round_up(K, ZEST_TILE_K);
 // Byte offset of tile (rt, kc) in an operand of R_pad rows.
 ZEST_HD int64_t zest_tile_offset(int64_t rt, int64_t kc, int64_t R_pad) {
     return (kc * (R_pad / ZEST_TILE_ROWS) + rt) * ZEST_TILE_BYTES;
+}
+
+// Byte offset of tile (rt, kc) of an expanded operand of R_pad rows.
+ZEST_HD int64_t zest_xtile_offset(int64_t rt, int64_t kc, int64_t R_pad) {
+    return (kc * (R_pad / ZEST_TILE_ROWS) + rt) * ZEST_XTILE_BYTES;
 }
 
 // Where block cb (columns 8cb..8cb+7) of row r lives: its exponent byte and

@@ -128,9 +128,10 @@ class Stack:
         self.go = torch.empty((m, c.ffn), **f32)
         self.uo = torch.empty((m, c.ffn), **f32)
         self.do = torch.empty((m, c.hidden), **f32)
-        self.pa = z.empty_packed(m, c.hidden, dev)
-        self.po = z.empty_packed(m, c.q, dev)
-        self.pd = z.empty_packed(m, c.ffn, dev)
+        # the matmuls' activation operands (the bfp16 pack, expanded)
+        self.pa = z.empty_act(m, c.hidden, dev)
+        self.po = z.empty_act(m, c.q, dev)
+        self.pd = z.empty_act(m, c.ffn, dev)
 
     def run_chunk(self, x_chunk, gemm_events=None):
         """One chunk through every layer. gemm_events: a list to which
@@ -155,7 +156,7 @@ class Stack:
             gemm(self.pa, "attn_q", L, c.q, c.hidden, self.qo)
             gemm(self.pa, "attn_k", L, c.kv, c.hidden, self.ko)
             gemm(self.pa, "attn_v", L, c.kv, c.hidden, self.vo)
-            z.pack_act(self.qo, out=self.po)
+            z.pack_act_x(self.qo, out=self.po)
             gemm(self.po, "attn_output", L, c.hidden, c.q, self.oo)
             z.add(self.h, self.oo, y=self.h)
             z.rms_norm(self.h, eps, L.ffn_norm, y=None, packed=self.pa)

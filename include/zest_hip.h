@@ -62,6 +62,7 @@ ZEST_API const char *zest_last_error(void);
 ZEST_API int64_t zest_rows_pad(int64_t rows);          /* rows rounded up to 256 */
 ZEST_API int64_t zest_k_pad(int64_t K);                /* K rounded up to 64 */
 ZEST_API size_t zest_bfp16_bytes(int64_t rows, int64_t K); /* bytes of a packed operand */
+ZEST_API size_t zest_act_bytes(int64_t rows, int64_t K);   /* bytes of an expanded activation operand */
 ZEST_API size_t zest_raw_row_bytes(int type, int64_t K);  /* bytes of one GGUF row */
 
 /* fp32 activations x[M][K] (row stride ldx floats) -> packed bfp16, bit-exact
@@ -70,14 +71,28 @@ ZEST_API size_t zest_raw_row_bytes(int type, int64_t K);  /* bytes of one GGUF r
  * (src/npu/bfp16_pack.h:58) / xdna_npu::encode_row (src/xdna-npu.h:96). */
 ZEST_API int zest_pack_act(const float *x, int64_t M, int64_t K, int64_t ldx, void *dst, void *stream);
 
+/* The same pack, written as the GEMM's activation operand: every bfp16 block
+ * stored decoded, each value as the bf16 it is exactly (zest_act_bytes(M, K)
+ * bytes; the tile layout with 2-byte values). Equals zest_expand_act of
+ * zest_pack_act's bytes. Replaces the same reference functions: the NPU
+ * expands its bfp16 operands inside the kernel, here the activations are
+ * expanded once when packed. */
+ZEST_API int zest_pack_act_x(const float *x, int64_t M, int64_t K, int64_t ldx, void *dst, void *stream);
+
+/* Packed bfp16 activations (zest_pack_act's output, M rows, K columns) -> the
+ * expanded operand, losslessly (bfp16_decode_block, src/npu/bfp16_pack.cpp:
+ * 129-144, as bf16). */
+ZEST_API int zest_expand_act(const void *src, int64_t M, int64_t K, void *dst, void *stream);
+
 /* A GGUF weight raw[N][K] of `type` (F32, Q8_0 or Q4_K rows, as ggml stores
  * them) -> packed bfp16 weight cache entry (zest_bfp16_bytes(N, K) bytes).
  * Dequantisation as ggml's to_float, then the same encoder. Replaces
  * xdna_npu::add_weight's unpack + bfp16_pack_b (src/xdna-npu.cpp:339-378). */
 ZEST_API int zest_convert_weight(int type, const void *raw, int64_t N, int64_t K, void *dst, void *stream);
 
-/* c[M][N] (row stride ldc floats) = A . W^T over packed operands a (M rows)
- * and w (N rows), K columns each: bfp16 expanded to bf16 in LDS, bf16 MFMA,
+/* c[M][N] (row stride ldc floats) = A . W^T, a the expanded activation
+ * operand (M rows, zest_pack_act_x) and w a packed bfp16 weight (N rows), K
+ * columns each: the weight's bfp16 tiles expanded to bf16 in LDS, bf16 MFMA,
  * fp32 accumulation, fp32 store. If `nonfinite` (a device word) is non-NULL,
  * it is OR-ed with 1 when any stored value is NaN or infinite. Replaces
  * xdna_npu::mul_mat (src/xdna-npu.cpp:392-444) and the NPU kernel's
@@ -90,7 +105,8 @@ ZEST_API int zest_gemm(const void *a, int64_t M, const void *w, int64_t N, int64
 
 /* y = RMS_NORM(x) (eps), optionally times a scale row w[d] (the MUL that
  * follows a norm, :258-277). y (fp32 rows, may be NULL) and/or packed (the
- * next matmul's packed input, rows_pad(rows) x d, may be NULL). */
+ * next matmul's input as zest_pack_act_x writes it, zest_act_bytes(rows, d)
+ * bytes, may be NULL). */
 ZEST_API int zest_rms_norm(const float *x, int64_t rows, int64_t d, float eps, const float *w, float *y, void *packed,
                            void *stream);
 

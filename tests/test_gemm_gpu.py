@@ -19,9 +19,11 @@ def _dev(a):
 
 
 def run_gemm(z, x: np.ndarray, wtype: int, raw: np.ndarray, n: int):
+    """The product path: x packed straight into the expanded operand, the
+    weight converted into the bfp16 cache layout, then the GEMM."""
     import torch
     m, k = x.shape
-    a = z.pack_act(_dev(x))
+    a = z.pack_act_x(_dev(x))
     w = z.convert_weight(wtype, _dev(raw), n, k)
     nf = torch.zeros(1, dtype=torch.int32, device="cuda")
     c = z.gemm(a, m, w, n, k, nonfinite=nf)
@@ -30,7 +32,15 @@ def run_gemm(z, x: np.ndarray, wtype: int, raw: np.ndarray, n: int):
 
 
 def decoded(z, oracle, packed, rows, k):
+    """A packed bfp16 weight's values."""
     return oracle.decode_rows(z.tiles_to_blocks(packed.cpu().numpy(), rows, k))
+
+
+def decoded_act(z, oracle, a, rows, k):
+    """The expanded activation operand's values; they must be the oracle's
+    bfp16 encoding, decoded (checked by the callers' data through
+    test_pack_gpu, and here on every call)."""
+    return z.expanded_to_rows(a.cpu().numpy(), rows, k)
 
 
 def test_self_test_entry_point(zest_gpu):
@@ -82,7 +92,8 @@ def test_gemm_against_oracle(zest_gpu, oracle, wtype, M, N, K):
     raw = quant.quantize(wtype, torch.from_numpy(w)).numpy() if wtype else w.view(np.uint8)
     c, nf, a, wp = run_gemm(zest_gpu, x, wtype, raw, N)
     assert nf == 0
-    ad = decoded(zest_gpu, oracle, a, M, K)
+    ad = decoded_act(zest_gpu, oracle, a, M, K)
+    assert np.array_equal(ad.view(np.uint32), oracle.decode_rows(oracle.encode_rows(x)).view(np.uint32))
     wd = decoded(zest_gpu, oracle, wp, N, K)
     rows = np.arange(M) if M * N * K <= 4e9 else np.linspace(0, M - 1, 96).astype(int)
     r64, ab = oracle.mul_mat_f64(wd, ad[rows])
@@ -109,7 +120,7 @@ def test_gemm_full_size_ffn_properties(zest_gpu, oracle):
     c, nf, a, wp = run_gemm(zest_gpu, x, 12, raw, N)
     assert nf == 0
     rows = np.array([0, 1, 2, 511, 1024, 1500, 2046, 2047])
-    ad = decoded(zest_gpu, oracle, a, M, K)[rows]
+    ad = decoded_act(zest_gpu, oracle, a, M, K)[rows]
     wd = decoded(zest_gpu, oracle, wp, N, K)
     r64, ab = oracle.mul_mat_f64(wd, ad)
     worst, maxrel = gemm_check(c[rows], r64, ab, K)
@@ -137,7 +148,7 @@ def test_gemm_wide_exponent_data(zest_gpu, oracle):
     x = make_data(m * k, 77).reshape(m, k)
     w = make_data(n * k, 78).reshape(n, k)
     c, nf, a, wp = run_gemm(zest_gpu, x, 0, w.view(np.uint8), n)
-    ad = decoded(zest_gpu, oracle, a, m, k)
+    ad = decoded_act(zest_gpu, oracle, a, m, k)
     wd = decoded(zest_gpu, oracle, wp, n, k)
     r64, ab = oracle.mul_mat_f64(wd, ad)
     worst, _ = gemm_check(c, r64, ab, k)

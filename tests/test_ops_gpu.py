@@ -31,13 +31,14 @@ def test_rms_norm_mul_and_fused_pack(zest_gpu, oracle, rows, d):
     x = Rng(rows + d).normal(rows * d, 0, 1.5).reshape(rows, d)
     w = Rng(d).normal(d, 1.0, 0.1)
     want = oracle.mul_row(oracle.rms_norm(x, 1e-6), w)
-    packed = zest_gpu.empty_packed(rows, d)
+    packed = zest_gpu.empty_act(rows, d)
     y = zest_gpu.rms_norm(_dev(x), 1e-6, _dev(w), packed=packed)
     got = _host(y)
     assert nrmse(got, want) <= EXACT
-    pk = zest_gpu.tiles_to_blocks(_host(packed), rows, d) if d % 8 == 0 else None
-    if pk is not None:
-        assert np.array_equal(pk, oracle.encode_rows(got))
+    if d % 8 == 0:
+        # the fused pack: the bfp16 encoding of the normed rows, stored expanded
+        pk = zest_gpu.expanded_to_rows(_host(packed), rows, d)
+        assert np.array_equal(pk.view(np.uint32), oracle.decode_rows(oracle.encode_rows(got)).view(np.uint32))
     # without the scale row: plain RMS_NORM
     y2 = zest_gpu.rms_norm(_dev(x), 1e-6)
     assert nrmse(_host(y2), oracle.rms_norm(x, 1e-6)) <= EXACT
@@ -60,11 +61,12 @@ def test_swiglu_one_tensor_and_fused_pack(zest_gpu, oracle, swapped):
     x = Rng(70).normal(rows * 2 * f, 0, 1.5).reshape(rows, 2 * f)
     xt = _dev(x)
     g, u = (xt[:, f:], xt[:, :f]) if swapped else (xt[:, :f], xt[:, f:])
-    packed = zest_gpu.empty_packed(rows, f)
+    packed = zest_gpu.empty_act(rows, f)
     got = _host(zest_gpu.glu(2, g, u, f, packed=packed))
     gh, uh = (x[:, f:], x[:, :f]) if swapped else (x[:, :f], x[:, f:])
     assert nrmse(got, oracle.glu(2, gh, uh)) <= EXACT
-    assert np.array_equal(zest_gpu.tiles_to_blocks(_host(packed), rows, f), oracle.encode_rows(got))
+    pk = zest_gpu.expanded_to_rows(_host(packed), rows, f)
+    assert np.array_equal(pk.view(np.uint32), oracle.decode_rows(oracle.encode_rows(got)).view(np.uint32))
 
 
 def test_add_mul_scale(zest_gpu, oracle):

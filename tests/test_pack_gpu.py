@@ -77,6 +77,52 @@ def test_pack_act_outlier_channels_full_size(zest_gpu, oracle):
     assert np.array_equal(gpu_pack(zest_gpu, x), oracle.encode_rows(x))
 
 
+# ---- the expanded activation operand (the GEMM's A) ----------------------
+
+def gpu_pack_x(z, x: np.ndarray, ldx: int | None = None):
+    """(pack_act_x bytes, expand_act(pack_act) bytes) of x, as numpy."""
+    import torch
+    m, k = x.shape
+    if ldx is None:
+        xt = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    else:
+        full = torch.zeros((m, ldx), dtype=torch.float32)
+        full[:, :k] = torch.from_numpy(x)
+        xt = full.cuda()[:, :k]
+    direct = torch.full((z.act_bytes(m, k),), 0xAB, dtype=torch.uint8, device="cuda")
+    z.pack_act_x(xt, direct)
+    via = z.expand_act(z.pack_act(xt), m, k)
+    torch.cuda.synchronize()
+    return direct.cpu().numpy(), via.cpu().numpy()
+
+
+@pytest.mark.parametrize("M,K,ldx", [(1, 8, None), (17, 24, None), (600, 200, None), (300, 2560, 2600),
+                                     (2048, 2560, None), (70, 72, None)])
+def test_pack_act_x_is_the_decoded_pack(zest_gpu, oracle, M, K, ldx):
+    # the expanded operand holds exactly the values the bfp16 bytes stand for:
+    # byte-equal to expanding zest_pack_act's output (padding included), and
+    # value-equal (bitwise) to the oracle's encode -> decode
+    x = make_data(M * K, M * 17 + K).reshape(M, K)
+    direct, via = gpu_pack_x(zest_gpu, x, ldx)
+    assert np.array_equal(direct, via)
+    got = zest_gpu.expanded_to_rows(direct, M, K)
+    assert np.array_equal(got.view(np.uint32), oracle.decode_rows(oracle.encode_rows(x)).view(np.uint32))
+    full = zest_gpu.expanded_to_rows(direct, zest_gpu.rows_pad(M), zest_gpu.k_pad(K))
+    assert not full[M:].any() and not full[:, K:].any()
+
+
+def test_pack_act_x_golden_and_edge_blocks(zest_gpu, oracle):
+    # zero, subnormal, tiny, saturating and near-FLT_MAX blocks take the
+    # general expansion; their decoded values must still be exact
+    x = GOLD["blocks_x"]
+    n = x.shape[0] // 64 * 64
+    for rows in (x[:n].reshape(-1, 64), edge_blocks().reshape(1, -1)):
+        direct, via = gpu_pack_x(zest_gpu, rows)
+        assert np.array_equal(direct, via)
+        got = zest_gpu.expanded_to_rows(direct, *rows.shape)
+        assert np.array_equal(got.view(np.uint32), oracle.decode_rows(oracle.encode_rows(rows)).view(np.uint32))
+
+
 def gpu_convert(z, wtype: int, raw: np.ndarray, n: int, k: int) -> np.ndarray:
     import torch
     rt = torch.from_numpy(np.ascontiguousarray(raw)).cuda()
