@@ -5,8 +5,8 @@ Workload (the north star's target): the Qwen3-4B-shaped
 36-layer decoder stack, random-init Q4_K (Q/K/V/gate/up) and Q8_0 (O/down)
 weights converted once into the resident bfp16 cache, an 8192-token fp32
 N(0,1) prompt processed in 2048-token chunks: per layer RMSNorm -> packed
-Q/K/V GEMMs, O GEMM + residual, RMSNorm -> gate/up GEMMs, SwiGLU -> packed
-down GEMM + residual. Attention is excluded, as BASELINE states. One step =
+Q/K/V GEMMs, O GEMM + residual, RMSNorm -> one fused gate/up GEMM whose
+epilogue computes the SwiGLU and packs it -> down GEMM + residual. Attention is excluded, as BASELINE states. One step =
 one whole prompt (4 chunks x 36 layers); inputs resident in HBM.
 
 Prints one JSON line: value = MUL_MAT TFLOP/s of the whole step (matmul FLOPs
@@ -139,6 +139,7 @@ def main() -> int:
     ap.add_argument("--workload", default="qwen3-4b")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=2048)
+    ap.add_argument("--unfused", action="store_true", help="gate and up as two GEMMs plus a SwiGLU kernel")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
@@ -154,7 +155,7 @@ def main() -> int:
     z.self_test()
     cfg = CONFIGS[args.workload]
     t_build = time.perf_counter()
-    stack = Stack(cfg, seed=0)
+    stack = Stack(cfg, seed=0, fused=not args.unfused)
     torch.cuda.synchronize()
     print(f"[bench] {cfg.name}: weights converted in {time.perf_counter() - t_build:.1f} s "
           f"(kernel time {stack.convert_ms:.1f} ms)", file=sys.stderr, flush=True)
@@ -198,6 +199,8 @@ def main() -> int:
         "config": {"workload": f"{cfg.name} stack: {cfg.layers} layers, hidden {cfg.hidden}, {cfg.tokens}-token "
                                f"prompt in {cfg.chunk}-token chunks, random-init GGUF weights, attention excluded",
                    "tokens": cfg.tokens, "chunk": cfg.chunk, "layers": cfg.layers,
+                   "gate_up": "two GEMMs + SwiGLU kernel" if args.unfused else
+                              "one fused GEMM, SwiGLU and pack in its epilogue",
                    "operands": "bfp16 (8-value blocks, shared exponent, int8 mantissas) expanded to bf16 for "
                                "MFMA, fp32 accumulate and output"},
         "pct_bf16_peak": round(100 * value / BF16_PEAK, 2),

@@ -50,6 +50,8 @@ SIGNATURES = {
     "zest_expand_act": (_c_i, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "zest_convert_weight": (_c_i, [_c_i, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "zest_gemm": (_c_i, [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p]),
+    "zest_convert_weight_gu": (_c_i, [_c_i, _c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
+    "zest_gemm_glu": (_c_i, [_c_i, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_p]),
     "zest_rms_norm": (_c_i, [_c_p, _c_i64, _c_i64, _c_f, _c_p, _c_p, _c_p, _c_p]),
     "zest_glu": (_c_i, [_c_i, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p]),
     "zest_add": (_c_i, [_c_p, _c_p, _c_i64, _c_i64, _c_i, _c_p, _c_p]),
@@ -213,6 +215,28 @@ def gemm(a_packed, m: int, w_packed, n: int, k: int, out=None, nonfinite=None):
     check(lib().zest_gemm(_ptr(a_packed), m, _ptr(w_packed), n, k, _ptr(out), out.stride(0), _ptr(nonfinite),
                           _stream()), "zest_gemm")
     return out
+
+
+def convert_weight_gu(wtype: int, gate, up, f: int, k: int, out=None):
+    """A GLU's gate and up GGUF weights (uint8 device tensors, f rows each) ->
+    one packed weight of 2f rows, interleaved by 32-row groups."""
+    out = empty_packed(2 * f, k, gate.device) if out is None else out
+    check(lib().zest_convert_weight_gu(wtype, _ptr(gate), _ptr(up), f, k, _ptr(out), _stream()),
+          "zest_convert_weight_gu")
+    return out
+
+
+def gemm_glu(kind: int, a_packed, m: int, w_gu, f: int, k: int, xout=True, h=None, nonfinite=None):
+    """The fused gate/up GEMM: glu(A . gate^T, A . up^T) written as the next
+    matmul's expanded operand (xout: True allocates one) and/or fp32 rows h.
+    Returns (xout, h)."""
+    torch = _torch()
+    xo = empty_act(m, f, a_packed.device) if xout is True else xout
+    ht = torch.empty((m, f), dtype=torch.float32, device=a_packed.device) if h is True else h
+    ldh = ht.stride(0) if ht is not None else 0
+    check(lib().zest_gemm_glu(kind, _ptr(a_packed), m, _ptr(w_gu), f, k, _ptr(xo), _ptr(ht), ldh, _ptr(nonfinite),
+                              _stream()), "zest_gemm_glu")
+    return xo, ht
 
 
 def rms_norm(x, eps: float, w=None, y=True, packed=None):

@@ -250,11 +250,92 @@ __device__ inline void store_tile(const f32x16 (&acc)[C::TI][C::TJ], float * Cou
     if (nonfinite && __any(bad) && lane == 0) atomicOr(nonfinite, 1u);
 }
 
-template <class C>
+// The fused gate/up epilogue: the weight is a gate/up pair interleaved by
+// 32-row groups (zest_convert_weight_gu), so with 64-row wave tiles (TJ = 2)
+// accumulator tile j = 0 holds gate values and j = 1 the up values of the
+// same 32 output columns, lane l%32 = column. Computes h = glu(g, u) in fp32
+// (the GLU kernel's arithmetic) and optionally stores it. For the down
+// projection's operand the wave stages its WM x 32 block of h in LDS (the
+// K loop is over and every stage consumed), then reads it back by rows: lane
+// l takes 16 consecutive columns of one row, i.e. two whole bfp16 blocks,
+// which it encodes and stores decoded as the activation packer does
+// (store_expanded16: two 16-byte stores). Each wave has its own LDS region,
+// so no barrier is needed: a wave's LDS operations complete in order.
+// Rows and columns past M and F come from zero padding and store zeros, as
+// the packer's padding is.
+template <class C, int KIND>
+__device__ inline void store_glu(const f32x16 (&acc)[C::TI][C::TJ], uint8_t * smem, uint8_t * xout, float * h,
+                                 int64_t ldh, int64_t M, int64_t F, int64_t m0, int64_t n0, int wave, int wm, int wn,
+                                 int lane, uint32_t * nonfinite) {
+    static_assert(C::TJ == 2 && C::WN == 64, "the fused GLU needs 64-row wave tiles: gate and up");
+    // staged rows of 36 floats: the 16-lane groups of the row reads below
+    // (rows r..r+15, one 16-byte column chunk) then hit distinct banks
+    constexpr int P = 36;
+    static_assert((size_t) (C::NC / 64) * C::WM * P * 4 <= C::LDS_BYTES, "staging must fit the LDS ring");
+    float * st = reinterpret_cast<float *>(smem) + wave * (C::WM * P);
+    const int64_t c0 = n0 / 2 + wn * 32, col = c0 + (lane & 31);
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < C::TI; i++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int rw = i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);  // row in the wave tile
+            const int64_t row = m0 + wm * C::WM + rw;
+            const float g = acc[i][0][v], u = acc[i][1][v];
+            const float hv = zest::glu(KIND, g, u);
+            bad |= !(__builtin_fabsf(g) <= 3.402823466e38f) || !(__builtin_fabsf(u) <= 3.402823466e38f) ||
+                   !(__builtin_fabsf(hv) <= 3.402823466e38f);
+            if (h && row < M && col < F) h[row * ldh + col] = hv;
+            if (xout) st[rw * P + (lane & 31)] = hv;
+        }
+    if (xout) {
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        const int64_t M_pad = zest_rows_padded(M);
+        const int half = lane >> 5;
+#pragma unroll
+        for (int j = 0; j < C::TI; j++) {
+            const int rw = j * 32 + (lane & 31);
+            const float4 * p = reinterpret_cast<const float4 *>(st + rw * P + half * 16);
+            float v[16];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float4 f = p[q];
+                v[4 * q] = f.x;
+                v[4 * q + 1] = f.y;
+                v[4 * q + 2] = f.z;
+                v[4 * q + 3] = f.w;
+            }
+            zest::store_expanded16(xout, M_pad, m0 + wm * C::WM + rw, c0 + half * 16, v);
+        }
+        // The last tile row also zeroes the operand's rows that no tile
+        // reaches, [m0 + BM, M_pad): 4 lanes per row, 16 bytes each.
+        if (m0 + C::BM >= M) {
+            uint8_t * base = xout + zest_xtile_offset(0, c0 / ZEST_TILE_K, M_pad) + (c0 % ZEST_TILE_K) * 2 +
+                             (lane & 3) * 16;
+            for (int64_t row = m0 + C::BM + wm * 16 + (lane >> 2); row < M_pad; row += 16 * C::CWM)
+                *reinterpret_cast<uint4 *>(base + (row / ZEST_TILE_ROWS) * ZEST_XTILE_BYTES +
+                                           (row % ZEST_TILE_ROWS) * 128) = make_uint4(0, 0, 0, 0);
+        }
+    }
+    if (nonfinite && __any(bad) && lane == 0) atomicOr(nonfinite, 1u);
+}
+
+// Where the consumers' accumulators go: C as fp32 (plain GEMM), or the fused
+// GLU's outputs.
+struct epilogue {
+    float * c;
+    int64_t ldc;
+    uint8_t * xout;
+    float * h;
+    int64_t ldh;
+};
+
+// EPI < 0: the plain GEMM's fp32 store; EPI >= 0: the fused GLU of that kind.
+template <class C, int EPI>
 __global__ __launch_bounds__(C::NT, 1) void gemm_kernel(const uint8_t * __restrict__ A, int64_t M_pad,
                                                         const uint8_t * __restrict__ W, int64_t N_pad, int nk,
-                                                        float * __restrict__ Cout, int64_t M, int64_t N, int64_t ldc,
-                                                        uint32_t * nonfinite) {
+                                                        epilogue ep, int64_t M, int64_t N, uint32_t * nonfinite) {
     extern __shared__ uint4 smem_u4[];
     uint8_t * smem = reinterpret_cast<uint8_t *>(smem_u4);
     const int tid = threadIdx.x, lane = tid & 63;
@@ -353,24 +434,27 @@ __global__ __launch_bounds__(C::NT, 1) void gemm_kernel(const uint8_t * __restri
         cur = nxt;
         __syncthreads();
     }
-    store_tile<C>(acc, Cout, M, N, ldc, m0, n0, wm, wn, lane, nonfinite);
+    if constexpr (EPI < 0)
+        store_tile<C>(acc, ep.c, M, N, ep.ldc, m0, n0, wm, wn, lane, nonfinite);
+    else
+        store_glu<C, EPI>(acc, smem, ep.xout, ep.h, ep.ldh, M, N / 2, m0, n0, wave, wm, wn, lane, nonfinite);
 }
 
-template <class C>
-int launch(const void * a, int64_t M, const void * w, int64_t N, int64_t K, float * c, int64_t ldc, uint32_t * nf,
-           hipStream_t s) {
+template <class C, int EPI>
+int launch(const void * a, int64_t M, const void * w, int64_t N, int64_t K, const epilogue & ep, uint32_t * nf,
+           hipStream_t s, const char * name) {
     static bool attr_set = false;
     if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_kernel<C>),
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_kernel<C, EPI>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int) C::LDS_BYTES);
-        if (e != hipSuccess) return zest::fail(ZEST_E_HIP, "zest_gemm: LDS attribute: %s", hipGetErrorString(e));
+        if (e != hipSuccess) return zest::fail(ZEST_E_HIP, "%s: LDS attribute: %s", name, hipGetErrorString(e));
         attr_set = true;
     }
     const int64_t M_pad = zest_rows_padded(M), N_pad = zest_rows_padded(N), K_pad = zest_k_padded(K);
     const dim3 grid((unsigned) (((N + C::BN - 1) / C::BN) * ((M + C::BM - 1) / C::BM)));
-    hipLaunchKernelGGL((gemm_kernel<C>), grid, dim3(C::NT), C::LDS_BYTES, s, (const uint8_t *) a, M_pad,
-                       (const uint8_t *) w, N_pad, (int) (K_pad / ZEST_TILE_K), c, M, N, ldc, nf);
-    return zest::check_launch("zest_gemm");
+    hipLaunchKernelGGL((gemm_kernel<C, EPI>), grid, dim3(C::NT), C::LDS_BYTES, s, (const uint8_t *) a, M_pad,
+                       (const uint8_t *) w, N_pad, (int) (K_pad / ZEST_TILE_K), ep, M, N, nf);
+    return zest::check_launch(name);
 }
 
 // 256x128 tiles (4 consumer waves of 128x64) wherever there are enough
@@ -389,6 +473,16 @@ using cfg_small = gemm_cfg<ZEST_GEMM_SMALL>;
 
 } // namespace
 
+// The tile shape of a launch: 256x128 when there are enough tiles to fill
+// the GPU, else 128x128.
+template <int EPI>
+static int launch_any(const void * a, int64_t M, const void * w, int64_t N, int64_t K, const epilogue & ep,
+                      uint32_t * nf, hipStream_t s, const char * name) {
+    const int64_t big_tiles = ((M + cfg_big::BM - 1) / cfg_big::BM) * ((N + cfg_big::BN - 1) / cfg_big::BN);
+    if (big_tiles >= ZEST_GEMM_BIG_MIN_TILES) return launch<cfg_big, EPI>(a, M, w, N, K, ep, nf, s, name);
+    return launch<cfg_small, EPI>(a, M, w, N, K, ep, nf, s, name);
+}
+
 extern "C" int zest_gemm(const void * a, int64_t M, const void * w, int64_t N, int64_t K, float * c, int64_t ldc,
                          uint32_t * nonfinite, void * stream) {
     ZEST_REQUIRE(a && w && c, "zest_gemm: null pointer");
@@ -399,8 +493,30 @@ extern "C" int zest_gemm(const void * a, int64_t M, const void * w, int64_t N, i
                      (uint64_t) zest_rows_padded(M) * (uint64_t) ldc * 4 < (1ull << 31),
                  "zest_gemm: operands and output must be under 2 GiB (M=%lld N=%lld K=%lld ldc=%lld)", (long long) M,
                  (long long) N, (long long) K, (long long) ldc);
+    const epilogue ep{c, ldc, nullptr, nullptr, 0};
+    return launch_any<-1>(a, M, w, N, K, ep, nonfinite, zest::as_stream(stream), "zest_gemm");
+}
+
+extern "C" int zest_gemm_glu(int kind, const void * a, int64_t M, const void * w_gu, int64_t F, int64_t K,
+                             void * xout, float * h, int64_t ldh, uint32_t * nonfinite, void * stream) {
+    ZEST_REQUIRE(a && w_gu && (xout || h), "zest_gemm_glu: null pointer");
+    ZEST_REQUIRE(M > 0 && F > 0 && F % 32 == 0 && K > 0 && K % 8 == 0, "zest_gemm_glu: M=%lld F=%lld K=%lld",
+                 (long long) M, (long long) F, (long long) K);
+    ZEST_REQUIRE(!h || ldh >= F, "zest_gemm_glu: ldh %lld < F %lld", (long long) ldh, (long long) F);
+    ZEST_REQUIRE(zest_act_bytes(M, K) < (1ull << 31) && zest_bfp16_bytes(2 * F, K) < (1ull << 31) &&
+                     zest_act_bytes(M, F) < (1ull << 31),
+                 "zest_gemm_glu: operands must be under 2 GiB (M=%lld F=%lld K=%lld)", (long long) M, (long long) F,
+                 (long long) K);
+    const epilogue ep{nullptr, 0, (uint8_t *) xout, h, ldh};
     hipStream_t s = zest::as_stream(stream);
-    const int64_t big_tiles = ((M + cfg_big::BM - 1) / cfg_big::BM) * ((N + cfg_big::BN - 1) / cfg_big::BN);
-    if (big_tiles >= ZEST_GEMM_BIG_MIN_TILES) return launch<cfg_big>(a, M, w, N, K, c, ldc, nonfinite, s);
-    return launch<cfg_small>(a, M, w, N, K, c, ldc, nonfinite, s);
+    const int64_t N = 2 * F;
+    const char * name = "zest_gemm_glu";
+    switch (kind) {
+        case ZEST_GLU_SWIGLU: return launch_any<ZEST_GLU_SWIGLU>(a, M, w_gu, N, K, ep, nonfinite, s, name);
+        case ZEST_GLU_GEGLU: return launch_any<ZEST_GLU_GEGLU>(a, M, w_gu, N, K, ep, nonfinite, s, name);
+        case ZEST_GLU_GEGLU_ERF: return launch_any<ZEST_GLU_GEGLU_ERF>(a, M, w_gu, N, K, ep, nonfinite, s, name);
+        case ZEST_GLU_GEGLU_QUICK: return launch_any<ZEST_GLU_GEGLU_QUICK>(a, M, w_gu, N, K, ep, nonfinite, s, name);
+        case ZEST_GLU_REGLU: return launch_any<ZEST_GLU_REGLU>(a, M, w_gu, N, K, ep, nonfinite, s, name);
+        default: return zest::fail(ZEST_E_UNSUPPORTED, "zest_gemm_glu: GLU kind %d", kind);
+    }
 }

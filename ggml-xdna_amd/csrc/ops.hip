@@ -98,15 +98,6 @@ __global__ __launch_bounds__(NORM_THREADS) void rms_norm_kernel(const float * __
     }
 }
 
-__device__ inline float act(int kind, float g) {
-    switch (kind) {
-        case ZEST_GLU_SWIGLU: return g / (1.0f + expf(-g));
-        case ZEST_GLU_GEGLU: return 0.5f * g * (1.0f + tanhf(0.7978845608f * g * (1.0f + 0.044715f * g * g)));
-        case ZEST_GLU_GEGLU_ERF: return 0.5f * g * (1.0f + erff(g * 0.7071067812f));
-        case ZEST_GLU_GEGLU_QUICK: return g / (1.0f + expf(-1.702f * g));
-        default: return g > 0.0f ? g : 0.0f;
-    }
-}
 
 // One thread per 16 outputs of one row: y = act(g) * u (REGLU as g > 0 ? g*u : 0).
 template <int KIND>
@@ -123,8 +114,7 @@ __global__ __launch_bounds__(256) void glu_kernel(const float * __restrict__ g, 
         load16(g + r * sg + c, gv, f - c);
         load16(u + r * su + c, uv, f - c);
 #pragma unroll
-        for (int i = 0; i < 16; i++) o[i] = (KIND == ZEST_GLU_REGLU) ? (gv[i] > 0.0f ? gv[i] * uv[i] : 0.0f)
-                                                                     : act(KIND, gv[i]) * uv[i];
+        for (int i = 0; i < 16; i++) o[i] = zest::glu(KIND, gv[i], uv[i]);
         if (y) store16(y + r * f + c, o, f - c);
     } else {
 #pragma unroll

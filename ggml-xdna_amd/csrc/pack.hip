@@ -13,6 +13,14 @@ namespace {
 
 using zest::encode8;
 
+// Row r of a weight in the packed operand: itself, or (gu = 0 / 1) its place
+// in a gate/up pair interleaved by 32-row groups: rows 64g..64g+31 hold gate
+// rows 32g..32g+31 and rows 64g+32..64g+63 the matching up rows (the
+// reference's bfp16_interleave_gate_up, src/npu/bfp16_pack.cpp:231-237, at
+// the GEMM's 32-row MFMA granularity), so one output tile of the fused GEMM
+// holds a gate value and its up value in the same lane.
+__device__ inline int64_t dst_row(int64_t r, int gu) { return gu < 0 ? r : (r >> 5) * 64 + gu * 32 + (r & 31); }
+
 // One thread encodes two blocks (16 values) of one row: 64 bytes of fp32 in,
 // a 16-byte mantissa store and a 2-byte exponent store out. A workgroup is one
 // 16-row tile row by 256 columns (4 tiles): thread t takes row t/16 and the
@@ -20,10 +28,10 @@ using zest::encode8;
 // XOUT: write the expanded operand (two 16-byte bf16 stores) instead.
 template <bool XOUT>
 __global__ __launch_bounds__(256) void pack_act_kernel(const float * __restrict__ x, int64_t M, int64_t K, int64_t ldx,
-                                                       uint8_t * __restrict__ dst, int64_t R_pad, int64_t K_pad) {
+                                                       uint8_t * __restrict__ dst, int64_t R_pad, int64_t K_pad, int gu) {
     const int t = threadIdx.x;
-    const int64_t rt = blockIdx.y;
-    const int64_t r = rt * ZEST_TILE_ROWS + (t >> 4);
+    const int64_t r = (int64_t) blockIdx.y * ZEST_TILE_ROWS + (t >> 4);
+    const int64_t rt = dst_row((int64_t) blockIdx.y * ZEST_TILE_ROWS, gu) / ZEST_TILE_ROWS;  // 16-row groups stay whole
     const int64_t col = (int64_t) blockIdx.x * 256 + (t & 15) * 16;
     if (col >= K_pad) return;
     float v[16];
@@ -44,7 +52,7 @@ __global__ __launch_bounds__(256) void pack_act_kernel(const float * __restrict_
         for (int i = 0; i < 16; i++) v[i] = (row_ok && col + i < K) ? x[r * ldx + col + i] : 0.0f;
     }
     if (XOUT) {
-        zest::store_expanded16(dst, R_pad, r, col, v);
+        zest::store_expanded16(dst, R_pad, rt * ZEST_TILE_ROWS + (t >> 4), col, v);
         return;
     }
     uint4 m;
@@ -79,12 +87,13 @@ __device__ inline float half_to_float(uint16_t h) { return (float) __builtin_bit
 // thread takes one GGUF block = half a tile row: 32 mantissa bytes (two
 // 16-byte stores) and four exponent bytes. Workgroup: 8 rows x 32 blocks.
 __global__ __launch_bounds__(256) void convert_q8_0_kernel(const uint8_t * __restrict__ raw, int64_t N, int64_t K,
-                                                           uint8_t * __restrict__ dst, int64_t R_pad, int64_t K_pad) {
+                                                           uint8_t * __restrict__ dst, int64_t R_pad, int64_t K_pad,
+                                                           int64_t R_src, int gu) {
     const int t = threadIdx.x;
     const int64_t r = (int64_t) blockIdx.y * 8 + (t >> 5);
     const int64_t jb = (int64_t) blockIdx.x * 32 + (t & 31);  // 32-column block
     const int64_t col = jb * 32;
-    if (col >= K_pad || r >= R_pad) return;
+    if (col >= K_pad || r >= R_src) return;
     uint4 m0 = make_uint4(0, 0, 0, 0), m1 = make_uint4(0, 0, 0, 0);
     uint32_t ex = 0;
     if (r < N && col < K) {
@@ -105,8 +114,9 @@ __global__ __launch_bounds__(256) void convert_q8_0_kernel(const uint8_t * __res
         e[3] = encode8(v + 24, m1.z, m1.w);
         ex = e[0] | (e[1] << 8) | (e[2] << 16) | (e[3] << 24);
     }
-    uint8_t * tile = dst + zest_tile_offset(r / ZEST_TILE_ROWS, col / ZEST_TILE_K, R_pad);
-    const int64_t rr = r % ZEST_TILE_ROWS, half = (col % ZEST_TILE_K) / 32;
+    const int64_t dr = dst_row(r, gu);
+    uint8_t * tile = dst + zest_tile_offset(dr / ZEST_TILE_ROWS, col / ZEST_TILE_K, R_pad);
+    const int64_t rr = dr % ZEST_TILE_ROWS, half = (col % ZEST_TILE_K) / 32;
     uint4 * mp = reinterpret_cast<uint4 *>(tile + rr * ZEST_TILE_K + half * 32);
     mp[0] = m0;
     mp[1] = m1;
@@ -120,12 +130,13 @@ __global__ __launch_bounds__(256) void convert_q8_0_kernel(const uint8_t * __res
 // is the subtraction's and fma gives the same float. One thread per
 // sub-block; workgroup 8 rows x 32 sub-blocks (4 super-blocks).
 __global__ __launch_bounds__(256) void convert_q4_k_kernel(const uint8_t * __restrict__ raw, int64_t N, int64_t K,
-                                                           uint8_t * __restrict__ dst, int64_t R_pad, int64_t K_pad) {
+                                                           uint8_t * __restrict__ dst, int64_t R_pad, int64_t K_pad,
+                                                           int64_t R_src, int gu) {
     const int t = threadIdx.x;
     const int64_t r = (int64_t) blockIdx.y * 8 + (t >> 5);
     const int64_t sb = (int64_t) blockIdx.x * 32 + (t & 31);  // 32-column sub-block
     const int64_t col = sb * 32;
-    if (col >= K_pad || r >= R_pad) return;
+    if (col >= K_pad || r >= R_src) return;
     uint4 m0 = make_uint4(0, 0, 0, 0), m1 = make_uint4(0, 0, 0, 0);
     uint32_t ex = 0;
     if (r < N && col < K) {
@@ -160,8 +171,9 @@ __global__ __launch_bounds__(256) void convert_q4_k_kernel(const uint8_t * __res
         e[3] = encode8(v + 24, m1.z, m1.w);
         ex = e[0] | (e[1] << 8) | (e[2] << 16) | (e[3] << 24);
     }
-    uint8_t * tile = dst + zest_tile_offset(r / ZEST_TILE_ROWS, col / ZEST_TILE_K, R_pad);
-    const int64_t rr = r % ZEST_TILE_ROWS, half = (col % ZEST_TILE_K) / 32;
+    const int64_t dr = dst_row(r, gu);
+    uint8_t * tile = dst + zest_tile_offset(dr / ZEST_TILE_ROWS, col / ZEST_TILE_K, R_pad);
+    const int64_t rr = dr % ZEST_TILE_ROWS, half = (col % ZEST_TILE_K) / 32;
     uint4 * mp = reinterpret_cast<uint4 *>(tile + rr * ZEST_TILE_K + half * 32);
     mp[0] = m0;
     mp[1] = m1;
@@ -202,10 +214,10 @@ static int pack_act(bool xout, const float * x, int64_t M, int64_t K, int64_t ld
     const dim3 grid((unsigned) ((K_pad + 255) / 256), (unsigned) (R_pad / ZEST_TILE_ROWS));
     if (xout)
         hipLaunchKernelGGL(pack_act_kernel<true>, grid, dim3(256), 0, zest::as_stream(stream), x, M, K, ldx,
-                           (uint8_t *) dst, R_pad, K_pad);
+                           (uint8_t *) dst, R_pad, K_pad, -1);
     else
         hipLaunchKernelGGL(pack_act_kernel<false>, grid, dim3(256), 0, zest::as_stream(stream), x, M, K, ldx,
-                           (uint8_t *) dst, R_pad, K_pad);
+                           (uint8_t *) dst, R_pad, K_pad, -1);
     return zest::check_launch(name);
 }
 
@@ -227,34 +239,58 @@ int zest_expand_act(const void * src, int64_t M, int64_t K, void * dst, void * s
     return zest::check_launch("zest_expand_act");
 }
 
+// Converts one weight (N rows) into dst, a packed operand of R_pad rows:
+// rows as they are (gu < 0), or into the gate (0) / up (1) slots of an
+// interleaved pair (then R_pad is the pair's and N % 32 == 0).
+static int convert(int type, const void * raw, int64_t N, int64_t K, void * dst, int64_t R_pad, int gu,
+                   hipStream_t s, const char * name) {
+    const int64_t K_pad = zest_k_padded(K), R_src = gu < 0 ? R_pad : R_pad / 2;
+    switch (type) {
+        case ZEST_TYPE_F32: {
+            ZEST_REQUIRE(aligned(raw, 16), "%s: F32 rows must be 16-byte aligned", name);
+            const dim3 grid((unsigned) ((K_pad + 255) / 256), (unsigned) (R_src / ZEST_TILE_ROWS));
+            hipLaunchKernelGGL(pack_act_kernel<false>, grid, dim3(256), 0, s, (const float *) raw, N, K, K,
+                               (uint8_t *) dst, R_pad, K_pad, gu);
+            return zest::check_launch(name);
+        }
+        case ZEST_TYPE_Q8_0: {
+            ZEST_REQUIRE(K % 32 == 0, "%s: Q8_0 needs K %% 32 == 0 (K=%lld)", name, (long long) K);
+            ZEST_REQUIRE(aligned(raw, 2), "%s: Q8_0 rows must be 2-byte aligned", name);
+            const dim3 grid((unsigned) ((K_pad / 32 + 31) / 32), (unsigned) (R_src / 8));
+            hipLaunchKernelGGL(convert_q8_0_kernel, grid, dim3(256), 0, s, (const uint8_t *) raw, N, K, (uint8_t *) dst,
+                               R_pad, K_pad, R_src, gu);
+            return zest::check_launch(name);
+        }
+        case ZEST_TYPE_Q4_K: {
+            ZEST_REQUIRE(K % 256 == 0, "%s: Q4_K needs K %% 256 == 0 (K=%lld)", name, (long long) K);
+            ZEST_REQUIRE(aligned(raw, 16), "%s: Q4_K rows must be 16-byte aligned", name);
+            const dim3 grid((unsigned) ((K_pad / 32 + 31) / 32), (unsigned) (R_src / 8));
+            hipLaunchKernelGGL(convert_q4_k_kernel, grid, dim3(256), 0, s, (const uint8_t *) raw, N, K, (uint8_t *) dst,
+                               R_pad, K_pad, R_src, gu);
+            return zest::check_launch(name);
+        }
+        default:
+            return zest::fail(ZEST_E_UNSUPPORTED, "%s: weight type %d has no converter", name, type);
+    }
+}
+
 int zest_convert_weight(int type, const void * raw, int64_t N, int64_t K, void * dst, void * stream) {
     ZEST_REQUIRE(raw && dst, "zest_convert_weight: null pointer");
     ZEST_REQUIRE(N > 0 && K > 0 && K % 8 == 0, "zest_convert_weight: N=%lld K=%lld", (long long) N, (long long) K);
     ZEST_REQUIRE(aligned(dst, 16), "zest_convert_weight: dst must be 16-byte aligned");
-    const int64_t R_pad = zest_rows_padded(N), K_pad = zest_k_padded(K);
+    return convert(type, raw, N, K, dst, zest_rows_padded(N), -1, zest::as_stream(stream), "zest_convert_weight");
+}
+
+int zest_convert_weight_gu(int type, const void * gate, const void * up, int64_t F, int64_t K, void * dst,
+                           void * stream) {
+    ZEST_REQUIRE(gate && up && dst, "zest_convert_weight_gu: null pointer");
+    ZEST_REQUIRE(F > 0 && F % 32 == 0 && K > 0 && K % 8 == 0,
+                 "zest_convert_weight_gu: F=%lld K=%lld (F must be a multiple of 32)", (long long) F, (long long) K);
+    ZEST_REQUIRE(aligned(dst, 16), "zest_convert_weight_gu: dst must be 16-byte aligned");
+    const int64_t R_pad = zest_rows_padded(2 * F);
     hipStream_t s = zest::as_stream(stream);
-    switch (type) {
-        case ZEST_TYPE_F32:
-            return zest_pack_act((const float *) raw, N, K, K, dst, stream);
-        case ZEST_TYPE_Q8_0: {
-            ZEST_REQUIRE(K % 32 == 0, "zest_convert_weight: Q8_0 needs K %% 32 == 0 (K=%lld)", (long long) K);
-            ZEST_REQUIRE(aligned(raw, 2), "zest_convert_weight: Q8_0 rows must be 2-byte aligned");
-            const dim3 grid((unsigned) ((K_pad / 32 + 31) / 32), (unsigned) (R_pad / 8));
-            hipLaunchKernelGGL(convert_q8_0_kernel, grid, dim3(256), 0, s, (const uint8_t *) raw, N, K, (uint8_t *) dst,
-                               R_pad, K_pad);
-            return zest::check_launch("zest_convert_weight(Q8_0)");
-        }
-        case ZEST_TYPE_Q4_K: {
-            ZEST_REQUIRE(K % 256 == 0, "zest_convert_weight: Q4_K needs K %% 256 == 0 (K=%lld)", (long long) K);
-            ZEST_REQUIRE(aligned(raw, 16), "zest_convert_weight: Q4_K rows must be 16-byte aligned");
-            const dim3 grid((unsigned) ((K_pad / 32 + 31) / 32), (unsigned) (R_pad / 8));
-            hipLaunchKernelGGL(convert_q4_k_kernel, grid, dim3(256), 0, s, (const uint8_t *) raw, N, K, (uint8_t *) dst,
-                               R_pad, K_pad);
-            return zest::check_launch("zest_convert_weight(Q4_K)");
-        }
-        default:
-            return zest::fail(ZEST_E_UNSUPPORTED, "zest_convert_weight: weight type %d has no converter", type);
-    }
+    const int st = convert(type, gate, F, K, dst, R_pad, 0, s, "zest_convert_weight_gu(gate)");
+    return st != ZEST_OK ? st : convert(type, up, F, K, dst, R_pad, 1, s, "zest_convert_weight_gu(up)");
 }
 
 } // extern "C"

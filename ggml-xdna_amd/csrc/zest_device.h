@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "zest_hip.h"
 #include "zest_layout.h"
 
 namespace zest {
@@ -129,6 +130,29 @@ __device__ inline void expand16(const uint4 & m, uint32_t e2, uint32_t out[8]) {
     } else {
         expand8(m.x, m.y, e0, out);
         expand8(m.z, m.w, e1, out + 4);
+    }
+}
+
+// e^-x as the hardware exp2 of -x log2(e) (v_exp_f32, about 1 ulp), and
+// 1 / (1 + e^-x) through the hardware reciprocal (v_rcp_f32, 1 ulp): the
+// logistic function in 4 VALU ops, against about 30 for libm's expf and a
+// correctly rounded divide. Its relative error (a few ulp, ~3e-7) is far
+// inside the 1e-5 nrmse the host ops are held to against the CPU's
+// x / (1 + expf(-x)). x -> -inf gives 1 / inf = 0, x -> +inf gives 1.
+__device__ inline float sigmoid(float x) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+}
+
+// The GLU of one gate value g and up value u (src/xdna-exec.cpp:296-320):
+// act(g) * u, ReGLU as g > 0 ? g * u : 0. Shared by the GLU kernel and the
+// fused gate/up GEMM's epilogue, so both give the same floats.
+__device__ inline float glu(int kind, float g, float u) {
+    switch (kind) {
+        case ZEST_GLU_SWIGLU: return g * sigmoid(g) * u;
+        case ZEST_GLU_GEGLU: return 0.5f * g * (1.0f + tanhf(0.7978845608f * g * (1.0f + 0.044715f * g * g))) * u;
+        case ZEST_GLU_GEGLU_ERF: return 0.5f * g * (1.0f + erff(g * 0.7071067812f)) * u;
+        case ZEST_GLU_GEGLU_QUICK: return g * sigmoid(1.702f * g) * u;
+        default: return g > 0.0f ? g * u : 0.0f;
     }
 }
 

@@ -7,9 +7,11 @@ A layer, for one chunk of M tokens with residual stream h [M][H] (fp32):
     (attention is excluded; the O projection's input is a stand-in: Q's output)
     pack(Q) ; O = GEMM(., Wo) ; h = h + O
     RMS_NORM(h) * w_ffn    -> packed (fused)
-    G, U = GEMM(packed, Wgate / Wup)
-    SiLU(G) * U            -> packed (fused)        the down projection's input
+    SiLU(packed . Wgate) * (packed . Wup) -> packed  one fused gate/up GEMM
+                                                    (xdna-exec's find_fusions)
     D = GEMM(., Wdown) ; h = h + D
+With fused=False the gate and up are two GEMMs and the SwiGLU its own kernel,
+as for a GLU that cannot be fused.
 Weights are random-init N(0, 0.02), quantised to GGUF on the GPU, converted
 once into the resident bfp16 cache (timed separately, as the reference
 reports warm prefill with its one-time copy build apart).
@@ -76,9 +78,9 @@ class Layer:
 class Stack:
     """Weights resident in HBM plus per-chunk work buffers."""
 
-    def __init__(self, cfg: StackConfig, seed: int = 0, device: str = "cuda"):
+    def __init__(self, cfg: StackConfig, seed: int = 0, device: str = "cuda", fused: bool = True):
         import torch
-        self.cfg, self.device = cfg, device
+        self.cfg, self.device, self.fused = cfg, device, fused
         g = torch.Generator(device=device)
         g.manual_seed(seed)
         self.layers: list[Layer] = []
@@ -96,13 +98,25 @@ class Stack:
                     w = torch.randn((n, k), generator=g, device=device) * 0.02
                     raw_by_shape[key] = quant.quantize(t, w)
                     del w
+                if fused and name == "ffn_gate" and ("ffn_up", n, k, t) not in raw_by_shape:
+                    w = torch.randn((n, k), generator=g, device=device) * 0.02
+                    raw_by_shape[("ffn_up", n, k, t)] = quant.quantize(t, w)
+                    del w
                 raw = raw_by_shape[key]
+                if fused and name == "ffn_up":
+                    continue  # converted with the gate, below
                 ev0.record()
-                L.w[name] = z.convert_weight(t, raw, n, k)
+                if fused and name == "ffn_gate":
+                    up = raw_by_shape[("ffn_up", n, k, t)]
+                    L.w["ffn_gate_up"] = z.convert_weight_gu(t, raw, up, n, k)
+                    nbytes = raw.numel() + up.numel() + 2 * n * k * 9 / 8
+                else:
+                    L.w[name] = z.convert_weight(t, raw, n, k)
+                    nbytes = raw.numel() + n * k * 9 / 8
                 ev1.record()
                 ev1.synchronize()
                 self.convert_ms += ev0.elapsed_time(ev1)
-                self.convert_bytes += raw.numel() + n * k * 9 / 8
+                self.convert_bytes += nbytes
             L.attn_norm = 1.0 + 0.1 * torch.randn(cfg.hidden, generator=g, device=device)
             L.ffn_norm = 1.0 + 0.1 * torch.randn(cfg.hidden, generator=g, device=device)
             self.layers.append(L)
@@ -125,8 +139,9 @@ class Stack:
         self.ko = torch.empty((m, c.kv), **f32)
         self.vo = torch.empty((m, c.kv), **f32)
         self.oo = torch.empty((m, c.hidden), **f32)
-        self.go = torch.empty((m, c.ffn), **f32)
-        self.uo = torch.empty((m, c.ffn), **f32)
+        if not self.fused:
+            self.go = torch.empty((m, c.ffn), **f32)
+            self.uo = torch.empty((m, c.ffn), **f32)
         self.do = torch.empty((m, c.hidden), **f32)
         # the matmuls' activation operands (the bfp16 pack, expanded)
         self.pa = z.empty_act(m, c.hidden, dev)
@@ -141,15 +156,18 @@ class Stack:
         eps = 1e-6
         self.h.copy_(x_chunk)
 
+        def timed(fn, flops):
+            if gemm_events is None:
+                fn()
+                return
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            gemm_events.append((e0, e1, flops))
+
         def gemm(a, wname, L, n, k, out):
-            if gemm_events is not None:
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record()
-                z.gemm(a, m, L.w[wname], n, k, out=out)
-                e1.record()
-                gemm_events.append((e0, e1, 2.0 * m * n * k))
-            else:
-                z.gemm(a, m, L.w[wname], n, k, out=out)
+            timed(lambda: z.gemm(a, m, L.w[wname], n, k, out=out), 2.0 * m * n * k)
 
         for L in self.layers:
             z.rms_norm(self.h, eps, L.attn_norm, y=None, packed=self.pa)
@@ -160,9 +178,13 @@ class Stack:
             gemm(self.po, "attn_output", L, c.hidden, c.q, self.oo)
             z.add(self.h, self.oo, y=self.h)
             z.rms_norm(self.h, eps, L.ffn_norm, y=None, packed=self.pa)
-            gemm(self.pa, "ffn_gate", L, c.ffn, c.hidden, self.go)
-            gemm(self.pa, "ffn_up", L, c.ffn, c.hidden, self.uo)
-            z.glu(z.GLU_SWIGLU, self.go, self.uo, c.ffn, y=None, packed=self.pd)
+            if self.fused:
+                timed(lambda: z.gemm_glu(z.GLU_SWIGLU, self.pa, m, L.w["ffn_gate_up"], c.ffn, c.hidden,
+                                         xout=self.pd), 4.0 * m * c.ffn * c.hidden)
+            else:
+                gemm(self.pa, "ffn_gate", L, c.ffn, c.hidden, self.go)
+                gemm(self.pa, "ffn_up", L, c.ffn, c.hidden, self.uo)
+                z.glu(z.GLU_SWIGLU, self.go, self.uo, c.ffn, y=None, packed=self.pd)
             gemm(self.pd, "ffn_down", L, c.hidden, c.ffn, self.do)
             z.add(self.h, self.do, y=self.h)
         return self.h

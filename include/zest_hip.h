@@ -101,6 +101,31 @@ ZEST_API int zest_convert_weight(int type, const void *raw, int64_t N, int64_t K
 ZEST_API int zest_gemm(const void *a, int64_t M, const void *w, int64_t N, int64_t K, float *c, int64_t ldc,
                        uint32_t *nonfinite, void *stream);
 
+/* A GLU's gate[F][K] and up[F][K] weights (GGUF rows of `type`, the same for
+ * both; for a weight holding the gate and then the up, up = gate + F rows)
+ * -> one packed weight of 2F rows for zest_gemm_glu (zest_bfp16_bytes(2F, K)
+ * bytes), its rows interleaved by 32-row groups: 32 gate rows, the 32 up
+ * rows that pair with them, and so on. Each row's bytes are zest_convert_
+ * weight's. F % 32 == 0. Replaces xdna_npu::add_fused (src/xdna-npu.cpp:
+ * 380-390) and bfp16_interleave_gate_up (src/npu/bfp16_pack.cpp:231-237),
+ * which interleave by the NPU tile's 8 rows where this uses the MFMA's 32. */
+ZEST_API int zest_convert_weight_gu(int type, const void *gate, const void *up, int64_t F, int64_t K, void *dst,
+                                    void *stream);
+
+/* The fused gate/up GEMM: with w_gu from zest_convert_weight_gu, computes
+ * g = A . gate^T and u = A . up^T as zest_gemm does, and in the same kernel
+ * h[M][F] = glu(g, u) of `kind` (zest_glu's arithmetic), written as the next
+ * matmul's operand (xout, as zest_pack_act_x writes it, zest_act_bytes(M, F)
+ * bytes) and/or as fp32 rows (h, row stride ldh floats); either may be NULL,
+ * not both. xout is bit-exact with zest_pack_act_x of zest_glu(zest_gemm(gate),
+ * zest_gemm(up)). `nonfinite` as for zest_gemm, over g, u and h. F % 32 == 0.
+ * Replaces the reference's fused SwiGLU matmul: find_fusions
+ * (src/xdna-exec.cpp:399-431) and the NPU kernel's output mode 2
+ * (kernels/bfp16_gemm/aie_kernels/aie2p/mm_bfp_acc.cc:258-278), which stores
+ * SiLU(gate)*up as bf16. */
+ZEST_API int zest_gemm_glu(int kind, const void *a, int64_t M, const void *w_gu, int64_t F, int64_t K, void *xout,
+                           float *h, int64_t ldh, uint32_t *nonfinite, void *stream);
+
 /* ---- the fused host ops (piece::run_rows, src/xdna-exec.cpp:253-346) ---- */
 
 /* y = RMS_NORM(x) (eps), optionally times a scale row w[d] (the MUL that

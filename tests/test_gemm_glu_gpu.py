@@ -1,0 +1,178 @@
+"""The fused gate/up GEMM (zest_convert_weight_gu + zest_gemm_glu): the
+reference's fused SwiGLU matmul (src/xdna-exec.cpp:399-431, output mode 2 of
+kernels/bfp16_gemm/aie_kernels/aie2p/mm_bfp_acc.cc:258-278).
+
+Its result must be bit-exact with the unfused chain the same library runs
+when nothing is fused: zest_gemm(gate) and zest_gemm(up) (pinned against the
+oracle in test_gemm_gpu), zest_glu (pinned in test_ops_gpu) and
+zest_pack_act_x (bit-exact with the oracle's encoder in test_pack_gpu). The
+fused GEMM sums each output over K in the same order as the plain one, so
+the gate and up values, and everything after them, are the same floats.
+The chain's end is also checked against the oracle here on sampled rows.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+from gen import Rng
+from helpers import load_quant, nrmse
+
+pytestmark = pytest.mark.gpu
+
+KINDS = {"reglu": 0, "geglu": 1, "swiglu": 2, "geglu_erf": 3, "geglu_quick": 4}
+
+
+def _dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _weights(wtype: int, f: int, k: int, seed: int):
+    """Gate and up GGUF rows (uint8 device tensors) of `wtype`."""
+    import torch
+    quant = load_quant()
+    out = []
+    for s in (seed, seed + 1):
+        w = Rng(s).normal(f * k, 0, 0.05).reshape(f, k)
+        raw = quant.quantize(wtype, torch.from_numpy(w).cuda()).cpu().numpy() if wtype else w.view(np.uint8)
+        out.append(_dev(raw))
+    return out
+
+
+def unfused(z, kind, a, m, gate, up, wtype, f, k):
+    """gate and up as two GEMMs, their GLU, then the down projection's operand."""
+    wg = z.convert_weight(wtype, gate, f, k)
+    wu = z.convert_weight(wtype, up, f, k)
+    g = z.gemm(a, m, wg, f, k)
+    u = z.gemm(a, m, wu, f, k)
+    h = z.glu(kind, g, u, f)
+    return z.pack_act_x(h), h, g, u
+
+
+@pytest.mark.parametrize("wtype,M,F,K", [
+    (0, 300, 96, 200),      # F % 64 == 32: half a K-tile of the output operand is padding
+    (0, 37, 64, 64),
+    (8, 1024, 2560, 1536),
+    (12, 520, 8960 // 10, 1536),
+    (12, 2048, 9728, 2560),  # BASELINE config 2's gate/up: 2048 x 9728 x 2560, Q4_K
+])
+def test_gemm_glu_matches_unfused_swiglu(zest_gpu, oracle, wtype, M, F, K):
+    import torch
+    x = Rng(M + F + K).normal(M * K).reshape(M, K)
+    gate, up = _weights(wtype, F, K, F + K)
+    a = zest_gpu.pack_act_x(_dev(x))
+    x_ref, h_ref, g, u = unfused(zest_gpu, 2, a, M, gate, up, wtype, F, K)
+    wgu = zest_gpu.convert_weight_gu(wtype, gate, up, F, K)
+    nf = torch.zeros(1, dtype=torch.int32, device="cuda")
+    xo, h = zest_gpu.gemm_glu(2, a, M, wgu, F, K, h=True, nonfinite=nf)
+    torch.cuda.synchronize()
+    assert int(nf.item()) == 0
+    assert torch.equal(h.view(torch.int32), h_ref.view(torch.int32))
+    assert torch.equal(xo, x_ref)
+    # the operand's values are the oracle's bfp16 encoding of h (sampled rows)
+    rows = np.unique(np.linspace(0, M - 1, min(M, 64)).astype(int))
+    hs = h.cpu().numpy()[rows]
+    xd = zest_gpu.expanded_to_rows(xo.cpu().numpy(), M, F)[rows]
+    assert np.array_equal(xd.view(np.uint32), oracle.decode_rows(oracle.encode_rows(hs)).view(np.uint32))
+    # and h is the oracle's SwiGLU of the gate and up products
+    gs, us = g.cpu().numpy()[rows], u.cpu().numpy()[rows]
+    assert nrmse(hs, oracle.glu(2, gs, us)) <= 1e-5  # tests/test-host-ops.cpp's bar
+
+
+@pytest.mark.parametrize("kind", list(KINDS))
+def test_gemm_glu_every_kind(zest_gpu, kind):
+    import torch
+    M, F, K = 300, 160, 256
+    x = Rng(5).normal(M * K).reshape(M, K)
+    gate, up = _weights(0, F, K, 9)
+    a = zest_gpu.pack_act_x(_dev(x))
+    x_ref, h_ref, _, _ = unfused(zest_gpu, KINDS[kind], a, M, gate, up, 0, F, K)
+    wgu = zest_gpu.convert_weight_gu(0, gate, up, F, K)
+    xo, h = zest_gpu.gemm_glu(KINDS[kind], a, M, wgu, F, K, h=True)
+    torch.cuda.synchronize()
+    assert torch.equal(h.view(torch.int32), h_ref.view(torch.int32)), kind
+    assert torch.equal(xo, x_ref), kind
+
+
+def test_gemm_glu_outputs_alone_and_strided(zest_gpu):
+    # xout only, h only into rows of a wider buffer: the same values
+    import torch
+    M, F, K = 700, 320, 512
+    x = Rng(11).normal(M * K).reshape(M, K)
+    gate, up = _weights(8, F, K, 13)
+    a = zest_gpu.pack_act_x(_dev(x))
+    wgu = zest_gpu.convert_weight_gu(8, gate, up, F, K)
+    xo, h = zest_gpu.gemm_glu(2, a, M, wgu, F, K, h=True)
+    xo_only, none = zest_gpu.gemm_glu(2, a, M, wgu, F, K)
+    wide = torch.full((M, F + 40), 7.0, device="cuda")
+    _, h2 = zest_gpu.gemm_glu(2, a, M, wgu, F, K, xout=None, h=wide)
+    torch.cuda.synchronize()
+    assert none is None
+    assert torch.equal(xo_only, xo)
+    assert torch.equal(wide[:, :F], h) and bool((wide[:, F:] == 7.0).all())
+
+
+def test_gemm_glu_one_weight_gate_then_up(zest_gpu):
+    # a GLU over one matmul whose weight holds the gate rows, then the up rows
+    # (the reference's Phi case, src/xdna-exec.cpp:402-403)
+    import torch
+    quant = load_quant()
+    M, F, K = 512, 256, 1024
+    w = Rng(17).normal(2 * F * K, 0, 0.05).reshape(2 * F, K)
+    raw = _dev(quant.quantize(12, torch.from_numpy(w).cuda()).cpu().numpy()).reshape(-1)
+    rb = zest_gpu.raw_row_bytes(12, K)
+    x = Rng(19).normal(M * K).reshape(M, K)
+    a = zest_gpu.pack_act_x(_dev(x))
+    wfull = zest_gpu.convert_weight(12, raw, 2 * F, K)
+    gu = zest_gpu.gemm(a, M, wfull, 2 * F, K)
+    h_ref = zest_gpu.glu(2, gu[:, :F], gu[:, F:], F)
+    wgu = zest_gpu.convert_weight_gu(12, raw[:F * rb], raw[F * rb:], F, K)
+    xo, h = zest_gpu.gemm_glu(2, a, M, wgu, F, K, h=True)
+    torch.cuda.synchronize()
+    assert torch.equal(h.view(torch.int32), h_ref.view(torch.int32))
+    assert torch.equal(xo, zest_gpu.pack_act_x(h_ref))
+
+
+def test_convert_weight_gu_is_the_interleaved_pair(zest_gpu):
+    # rows 64g..64g+31 of the pair are gate rows 32g.., rows 64g+32.. the up
+    # rows: each row's blocks are convert_weight's, and the padding is zero
+    for wtype, F, K in [(0, 96, 200), (8, 320, 512), (12, 224, 256)]:
+        gate, up = _weights(wtype, F, K, 23)
+        pair = zest_gpu.convert_weight_gu(wtype, gate, up, F, K).cpu().numpy()
+        bg = zest_gpu.tiles_to_blocks(zest_gpu.convert_weight(wtype, gate, F, K).cpu().numpy(), F, K)
+        bu = zest_gpu.tiles_to_blocks(zest_gpu.convert_weight(wtype, up, F, K).cpu().numpy(), F, K)
+        rows_pad = zest_gpu.rows_pad(2 * F)
+        bp = zest_gpu.tiles_to_blocks(pair, rows_pad, K)
+        r = np.arange(F)
+        dst = (r // 32) * 64 + r % 32
+        assert np.array_equal(bp[dst], bg), wtype
+        assert np.array_equal(bp[dst + 32], bu), wtype
+        rest = np.setdiff1d(np.arange(rows_pad), np.concatenate([dst, dst + 32]))
+        assert not bp[rest].any(), wtype
+
+
+def test_gemm_glu_nonfinite_flag(zest_gpu):
+    import torch
+    M, F, K = 64, 64, 128
+    x = Rng(29).normal(M * K).reshape(M, K)
+    x[3, 5] = np.inf
+    gate, up = _weights(0, F, K, 31)
+    a = zest_gpu.pack_act_x(_dev(x))
+    wgu = zest_gpu.convert_weight_gu(0, gate, up, F, K)
+    nf = torch.zeros(1, dtype=torch.int32, device="cuda")
+    zest_gpu.gemm_glu(2, a, M, wgu, F, K, nonfinite=nf)
+    torch.cuda.synchronize()
+    assert int(nf.item()) == 1
+
+
+def test_gemm_glu_rejects_bad_sizes(zest_gpu):
+    import torch
+    a = zest_gpu.empty_act(64, 64)
+    w = zest_gpu.empty_packed(128, 64)
+    with pytest.raises(RuntimeError):
+        zest_gpu.gemm_glu(2, a, 64, w, 48, 64)          # F % 32 != 0
+    with pytest.raises(RuntimeError):
+        zest_gpu.gemm_glu(9, a, 64, w, 64, 64)          # no such GLU kind
+    with pytest.raises(RuntimeError):
+        zest_gpu.gemm_glu(2, a, 64, w, 64, 64, xout=None)  # no output
+    torch.cuda.synchronize()
