@@ -50,6 +50,7 @@ SIGNATURES = {
     "zest_expand_act": (_c_i, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "zest_convert_weight": (_c_i, [_c_i, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "zest_gemm": (_c_i, [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p]),
+    "zest_gemm_group": (_c_i, [_c_p, _c_i64, _c_i64, _c_i, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p]),
     "zest_convert_weight_gu": (_c_i, [_c_i, _c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "zest_gemm_glu": (_c_i, [_c_i, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_p]),
     "zest_rms_norm": (_c_i, [_c_p, _c_i64, _c_i64, _c_f, _c_p, _c_p, _c_p, _c_p]),
@@ -215,6 +216,20 @@ def gemm(a_packed, m: int, w_packed, n: int, k: int, out=None, nonfinite=None):
     check(lib().zest_gemm(_ptr(a_packed), m, _ptr(w_packed), n, k, _ptr(out), out.stride(0), _ptr(nonfinite),
                           _stream()), "zest_gemm")
     return out
+
+
+def gemm_group(a_packed, m: int, weights, ns, k: int, outs=None, nonfinite=None):
+    """Several weights sharing one activation operand in one launch:
+    outs[i][m][ns[i]] = A . W_i^T. Returns the outputs."""
+    torch = _torch()
+    n = len(weights)
+    outs = [torch.empty((m, ni), dtype=torch.float32, device=a_packed.device) for ni in ns] if outs is None else outs
+    P, I64 = ctypes.c_void_p * n, ctypes.c_int64 * n
+    w = P(*[t.data_ptr() for t in weights])
+    c = P(*[t.data_ptr() for t in outs])
+    check(lib().zest_gemm_group(_ptr(a_packed), m, k, n, w, I64(*ns), c, I64(*[t.stride(0) for t in outs]),
+                                _ptr(nonfinite), _stream()), "zest_gemm_group")
+    return outs
 
 
 def convert_weight_gu(wtype: int, gate, up, f: int, k: int, out=None):

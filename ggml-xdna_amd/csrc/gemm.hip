@@ -20,6 +20,11 @@
 // ends. One barrier per K-step. The store is fp32 row-major, as the
 // reference's output mode 0 (kernels/bfp16_gemm/aie_kernels/aie2p/
 // mm_bfp_acc.cc:106-116, 258-278).
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "zest_common.h"
 #include "zest_device.h"
 
@@ -29,11 +34,15 @@
 #ifndef ZEST_GEMM_GROUP_M
 #define ZEST_GEMM_GROUP_M 4  // tile rows per group of the tile order
 #endif
+#ifndef ZEST_GEMM_XSTEP
+#define ZEST_GEMM_XSTEP 1  // consumers read a step's first fragments before the barrier that starts it
+#endif
 
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // BM x BN tile; CWM x CWN consumer waves, each a WM x WN block of 32x32 MFMA
 // tiles; as many producer waves.
@@ -98,6 +107,15 @@ typedef __attribute__((address_space(3))) void * lds_ptr_t;
 
 // s_waitcnt vmcnt(0) lgkmcnt(0): every load, DMA and LDS store of this wave done
 #define ZEST_WAIT_ALL() __builtin_amdgcn_s_waitcnt(7 << 4)
+
+// s_waitcnt vmcnt(VM) lgkmcnt(0): all but the last VM memory loads (LDS DMA
+// included; they complete in issue order) and every LDS store of this wave
+// done. (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8.)
+template <int VM>
+__device__ inline void wait_vm_lgkm0() {
+    static_assert(VM >= 0 && VM < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4));
+}
 
 // The producer side. Loads go through buffer resources: the slab's byte
 // offset is wave-uniform (a scalar offset), the lane's place in it a fixed
@@ -271,8 +289,9 @@ __device__ inline void store_glu(const f32x16 (&acc)[C::TI][C::TJ], uint8_t * sm
     // staged rows of 36 floats: the 16-lane groups of the row reads below
     // (rows r..r+15, one 16-byte column chunk) then hit distinct banks
     constexpr int P = 36;
-    static_assert((size_t) (C::NC / 64) * C::WM * P * 4 <= C::LDS_BYTES, "staging must fit the LDS ring");
-    float * st = reinterpret_cast<float *>(smem) + wave * (C::WM * P);
+    static_assert(P <= C::WN && (size_t) C::BM * C::BN * 4 <= C::LDS_BYTES, "staging must fit the LDS ring");
+    // the wave's LDS region, the one the split-K fixup uses: WM x WN floats
+    float * st = reinterpret_cast<float *>(smem + wave * (C::WM * C::WN * 4));
     const int64_t c0 = n0 / 2 + wn * 32, col = c0 + (lane & 31);
     bool bad = false;
 #pragma unroll
@@ -321,92 +340,249 @@ __device__ inline void store_glu(const f32x16 (&acc)[C::TI][C::TJ], uint8_t * sm
     if (nonfinite && __any(bad) && lane == 0) atomicOr(nonfinite, 1u);
 }
 
-// Where the consumers' accumulators go: C as fp32 (plain GEMM), or the fused
-// GLU's outputs.
-struct epilogue {
-    float * c;
-    int64_t ldc;
-    uint8_t * xout;
-    float * h;
-    int64_t ldh;
+// One weight of a launch. Weights that share the activation operand (a
+// group: q, k and v) run as one launch; their column tiles follow each other.
+struct gemm_weight {
+    const uint8_t * w;  // packed bfp16
+    float * c;          // fp32 output (plain epilogue)
+    int64_t n, ldc;
+    int w_kstride;      // bytes between K-steps of the packed weight
+    int tile0;          // its first column tile in the launch
 };
 
+struct gemm_params {
+    const uint8_t * a;  // expanded activations
+    int64_t M;
+    int a_kstride;      // bytes between K-steps of the activation operand
+    int nk;             // K-steps
+    int mt, nt;         // tile rows; column tiles of all weights
+    int nw;             // weights
+    gemm_weight wt[ZEST_GEMM_MAX_GROUP];
+    uint8_t * xout;     // fused GLU outputs (one weight)
+    float * h;
+    int64_t ldh;
+    uint32_t * nonfinite;
+    // Split-K: with splits S > 1, workgroup v takes unit v of the sequence
+    // (split 0 of every tile, split 1 of every tile, ...): split s of a tile is
+    // its K-steps [s*nk/S, (s+1)*nk/S). The workgroups running one split walk
+    // K side by side, as whole tiles do, so they keep sharing A and W slabs in
+    // L2. The splits of a tile are summed through `partial` (BM*BN floats per
+    // unit) and `counters` (one per tile and consumer wave, zero between
+    // launches).
+    int splits;
+    float * partial;
+    uint32_t * counters;
+};
+
+// Byte offset of a consumer wave's float4 (i, j, quad q) in a unit's partial
+// sums: [unit][wave][i][j][quad][lane], so each store and load instruction
+// covers 1 KB contiguous.
+template <class C>
+__device__ inline int partial_off(int unit, int wave, int i, int j, int q, int lane) {
+    return (((((unit * (C::NC / 64) + wave) * (C::TI * C::TJ) + i * C::TJ + j) * 4 + q) * 64) + lane) * 16;
+}
+
+// Cache policy of the partial sums' loads and stores: sc1, coherent at device
+// scope (the writer and the reader may sit on different XCDs, whose L2s are
+// not coherent with each other). No fence is used: a device-scope fence
+// writes back and invalidates the XCD's whole L2, which would take the A and
+// W slabs the other workgroups there are sharing.
+#define ZEST_SC1 16
+
+// Split-K fixup of one consumer wave's block of tile t, split `split` of
+// p.splits. Writes this wave's sums to its unit's partial (sc1 stores), waits
+// for them to be acknowledged, and counts itself in. The wave that arrives
+// last adds the splits' partials in order 0, 1, ... (its own read back like
+// the others), so the result does not depend on arrival order, and resets
+// the counter. Each partial comes into the wave's own LDS region by LDS DMA
+// (all of its loads in flight at once, no registers held), then is added
+// from there. LDS is free: the K loop is over, and this workgroup has no
+// other tile. Returns true for the last wave, whose acc then holds the
+// tile's sums. No wave waits for another.
+template <class C>
+__device__ inline bool fixup(f32x16 (&acc)[C::TI][C::TJ], const gemm_params & p, uint8_t * smem, int t, int split,
+                             int wave, int lane) {
+    constexpr int PARTS = C::TI * C::TJ * 4;  // 1 KB pieces of a wave's share
+    const int T = p.mt * p.nt, S = p.splits;
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+        p.partial, (short) 0, (int) ((int64_t) T * S * C::BM * C::BN * 4), 0x00020000);
+    const int me = split * T + t;
+#pragma unroll
+    for (int i = 0; i < C::TI; i++)
+#pragma unroll
+        for (int j = 0; j < C::TJ; j++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float4 x = make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                             acc[i][j][4 * q + 3]);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), rp,
+                                                       partial_off<C>(me, wave, i, j, q, lane), 0, ZEST_SC1);
+            }
+    // the stores have reached the coherent level before the count goes up
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    uint32_t * counter = p.counters + (int64_t) t * (C::NC / 64) + wave;
+    uint32_t old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __shfl(old, 0);
+    asm volatile("" ::: "memory");
+    if (old != (uint32_t) (S - 1)) return false;
+    uint8_t * region = smem + wave * (C::WM * C::WN * 4);
+    for (int u = 0; u < S; u++) {
+        const int base = partial_off<C>(u * T + t, wave, 0, 0, 0, 0);
+#pragma unroll
+        for (int x = 0; x < PARTS; x++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, (lds_ptr_t) (region + x * 1024), 16, lane * 16,
+                                                     base + x * 1024, 0, ZEST_SC1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < C::TI; i++)
+#pragma unroll
+            for (int j = 0; j < C::TJ; j++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float4 x =
+                        *reinterpret_cast<const float4 *>(region + ((i * C::TJ + j) * 4 + q) * 1024 + lane * 16);
+                    if (u == 0) {
+                        acc[i][j][4 * q] = x.x;
+                        acc[i][j][4 * q + 1] = x.y;
+                        acc[i][j][4 * q + 2] = x.z;
+                        acc[i][j][4 * q + 3] = x.w;
+                    } else {
+                        acc[i][j][4 * q] += x.x;
+                        acc[i][j][4 * q + 1] += x.y;
+                        acc[i][j][4 * q + 2] += x.z;
+                        acc[i][j][4 * q + 3] += x.w;
+                    }
+                }
+        // the reads are done before the next partial's DMA overwrites them
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    if (lane == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+}
+
+// The producer's barrier: no fence, so the compiler adds no wait of its own
+// (a workgroup fence would wait for every LDS DMA in flight); the waits it
+// needs are explicit before it.
+__device__ inline void producer_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// The producer's part of one tile over K-steps [k0, k0 + ns). During step k,
+// step k+2 goes into stage (k+2)%3: first its A slab by DMA, then step k+3's
+// W units are requested, then step k+2's W units (requested during step k+1)
+// are expanded and stored. Before the barrier that ends step k it waits only
+// for what the consumers need after it; loads issued in the step and not
+// needed yet stay in flight (they complete in issue order):
+//   ZEST_GEMM_XSTEP 1: the consumers read the first fragments of step k+1
+//     before that barrier, so stage (k+2)%3 is read during step k+1: the
+//     step's A DMA completes, its W loads (for step k+3) stay in flight;
+//   ZEST_GEMM_XSTEP 0: stage (k+1)%3, filled during step k-1, is the only one
+//     read next: the step's A DMA and W loads both stay in flight.
+// The steady state runs without conditions, so the compiler counts the
+// loads in flight exactly; the last steps take full waits. The barriers
+// match the consumer's, step for step.
+template <class C>
+__device__ inline void produce(const producer<C> & pr, uint8_t * smem, int a0, int w0, int a_kstride, int w_kstride,
+                               int ns) {
+    constexpr int AI = producer<C>::AI, WI = 2 * C::BU;  // VMEM instructions per step: A DMA, W loads
+    constexpr int FLY = ZEST_GEMM_XSTEP ? WI : AI + WI;
+    stage_regs<C> s0, s1;
+    pr.dma_a(smem, 0, a0);
+    pr.load_w(s0, w0);
+    if (ns > 1) {
+        pr.dma_a(smem, C::STAGE, a0 + a_kstride);
+        pr.load_w(s1, w0 + w_kstride);
+    }
+    pr.store_w(s0, smem, 0);
+    if (ns > 2) pr.load_w(s0, w0 + 2 * w_kstride);
+    if (ns > 1) pr.store_w(s1, smem, C::STAGE);
+    // stages 0 and 1 complete; step 2's W loads may stay in flight
+    if (ns > 2)
+        wait_vm_lgkm0<WI>();
+    else
+        ZEST_WAIT_ALL();
+    producer_barrier();
+    int stage = 2 * C::STAGE, k = 0;
+    for (; k + 4 < ns; k += 2) {
+        pr.dma_a(smem, stage, a0 + (k + 2) * a_kstride);
+        pr.load_w(s1, w0 + (k + 3) * w_kstride);
+        // every request of the step is out before waiting for last step's W
+        __builtin_amdgcn_sched_barrier(0);
+        pr.store_w(s0, smem, stage);
+        stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
+        wait_vm_lgkm0<FLY>();
+        producer_barrier();
+        pr.dma_a(smem, stage, a0 + (k + 3) * a_kstride);
+        pr.load_w(s0, w0 + (k + 4) * w_kstride);
+        __builtin_amdgcn_sched_barrier(0);
+        pr.store_w(s1, smem, stage);
+        stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
+        wait_vm_lgkm0<FLY>();
+        producer_barrier();
+    }
+    for (; k < ns; k += 2) {
+        if (k + 2 < ns) {
+            pr.dma_a(smem, stage, a0 + (k + 2) * a_kstride);
+            if (k + 3 < ns) pr.load_w(s1, w0 + (k + 3) * w_kstride);
+            pr.store_w(s0, smem, stage);
+        }
+        stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
+        ZEST_WAIT_ALL();
+        producer_barrier();
+        if (k + 1 < ns) {
+            if (k + 3 < ns) {
+                pr.dma_a(smem, stage, a0 + (k + 3) * a_kstride);
+                if (k + 4 < ns) pr.load_w(s0, w0 + (k + 4) * w_kstride);
+                pr.store_w(s1, smem, stage);
+            }
+            stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
+            ZEST_WAIT_ALL();
+            producer_barrier();
+        }
+    }
+}
+
 // EPI < 0: the plain GEMM's fp32 store; EPI >= 0: the fused GLU of that kind.
-template <class C, int EPI>
-__global__ __launch_bounds__(C::NT, 1) void gemm_kernel(const uint8_t * __restrict__ A, int64_t M_pad,
-                                                        const uint8_t * __restrict__ W, int64_t N_pad, int nk,
-                                                        epilogue ep, int64_t M, int64_t N, uint32_t * nonfinite) {
+// SPLIT: split-K (p.splits > 1), else one whole tile per workgroup.
+template <class C, int EPI, bool SPLIT>
+__global__ __launch_bounds__(C::NT, 1) void gemm_kernel(const gemm_params p) {
     extern __shared__ uint4 smem_u4[];
     uint8_t * smem = reinterpret_cast<uint8_t *>(smem_u4);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    int64_t m0, n0;
-    {
-        // Workgroups go to the 8 XCDs round-robin by linear id; give each XCD
-        // a contiguous run of tiles, and walk tiles in groups of GROUP_M tile
-        // rows (M-fastest inside a group), so the ~32 workgroups resident on
-        // one XCD cover a compact block of about 4 x 8 tiles and share their
-        // A and W slabs in its L2.
-        const int G = (int) gridDim.x, b = (int) blockIdx.x;
-        const int mt = (int) ((M + C::BM - 1) / C::BM), nt = (int) ((N + C::BN - 1) / C::BN);
+    const int nk = p.nk;
+    // Workgroups go to the 8 XCDs round-robin by linear id; v numbers them so
+    // that each XCD holds a contiguous run of v, i.e. of tiles.
+    const int G = (int) gridDim.x, b = (int) blockIdx.x;
 #if ZEST_GEMM_XCD
-        const int q = G / 8, r = G % 8, x = b % 8;
-        const int t = x * q + min(x, r) + b / 8;
+    const int v = (b % 8) * (G / 8) + min(b % 8, G % 8) + b / 8;
 #else
-        const int t = b;
+    const int v = b;
 #endif
-        const int per_group = ZEST_GEMM_GROUP_M * nt, first_m = t / per_group * ZEST_GEMM_GROUP_M;
-        const int gm = min(mt - first_m, ZEST_GEMM_GROUP_M), in = t % per_group;
-        m0 = (int64_t) (first_m + in % gm) * C::BM;
-        n0 = (int64_t) (in / gm) * C::BN;
-        (void) G;
-    }
-    // operands are < 2 GiB (checked by the host), so byte offsets fit an int
-    const int a_kstride = (int) ((M_pad / ZEST_TILE_ROWS) * ZEST_XTILE_BYTES);
-    const int w_kstride = (int) ((N_pad / ZEST_TILE_ROWS) * ZEST_TILE_BYTES);
+    const int T = p.mt * p.nt;
+    const int split = SPLIT ? v / T : 0, t = SPLIT ? v - split * T : v;
+    const int k0 = SPLIT ? split * nk / p.splits : 0, ns = SPLIT ? (split + 1) * nk / p.splits - k0 : nk;
+    // Tile t: tiles go in groups of GROUP_M tile rows, M-fastest inside a
+    // group, so the ~32 workgroups resident on one XCD cover a compact block
+    // of about 4 x 8 tiles and share their A and W slabs in its L2.
+    const int per_group = ZEST_GEMM_GROUP_M * p.nt, first_m = t / per_group * ZEST_GEMM_GROUP_M;
+    const int gm = min(p.mt - first_m, ZEST_GEMM_GROUP_M), in = t % per_group;
+    const int tm = first_m + in % gm, tn = in / gm;
+    int g = 0;
+#pragma unroll
+    for (int i = 1; i < ZEST_GEMM_MAX_GROUP; i++)
+        if (i < p.nw && tn >= p.wt[i].tile0) g = i;
+    g = __builtin_amdgcn_readfirstlane(g);
+    const gemm_weight W = p.wt[g];
+    const int64_t m0 = (int64_t) tm * C::BM, n0 = (int64_t) (tn - W.tile0) * C::BN;
 
     if (wave >= C::NC / 64) {
-        // Producer. During step k, step k+2 goes into stage (k+2)%3: first its
-        // A slab by DMA, then step k+3's W units are requested, then step
-        // k+2's W units (requested during step k+1) are expanded and stored.
-        // The barrier that ends the step waits for all of it. The barriers
-        // match the consumer loop's, step for step.
-        const int a0 = (int) ((m0 / ZEST_TILE_ROWS) * ZEST_XTILE_BYTES);
-        const int w0 = (int) ((n0 / ZEST_TILE_ROWS) * ZEST_TILE_BYTES);
-        const producer<C> pr(A, (int64_t) a_kstride * nk, W, (int64_t) w_kstride * nk, tid - C::NC);
-        stage_regs<C> s0, s1;
-        pr.dma_a(smem, 0, a0);
-        pr.load_w(s0, w0);
-        if (nk > 1) {
-            pr.dma_a(smem, C::STAGE, a0 + a_kstride);
-            pr.load_w(s1, w0 + w_kstride);
-        }
-        pr.store_w(s0, smem, 0);
-        if (nk > 2) pr.load_w(s0, w0 + 2 * w_kstride);
-        if (nk > 1) pr.store_w(s1, smem, C::STAGE);
-        ZEST_WAIT_ALL();
-        __syncthreads();
-        int stage = 2 * C::STAGE;
-        for (int k = 0; k < nk; k += 2) {
-            if (k + 2 < nk) {
-                pr.dma_a(smem, stage, a0 + (k + 2) * a_kstride);
-                if (k + 3 < nk) pr.load_w(s1, w0 + (k + 3) * w_kstride);
-                pr.store_w(s0, smem, stage);
-            }
-            stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
-            ZEST_WAIT_ALL();
-            __syncthreads();
-            if (k + 1 < nk) {
-                if (k + 3 < nk) {
-                    pr.dma_a(smem, stage, a0 + (k + 3) * a_kstride);
-                    if (k + 4 < nk) pr.load_w(s0, w0 + (k + 4) * w_kstride);
-                    pr.store_w(s1, smem, stage);
-                }
-                stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
-                ZEST_WAIT_ALL();
-                __syncthreads();
-            }
-        }
+        const producer<C> pr(p.a, (int64_t) p.a_kstride * nk, W.w, (int64_t) W.w_kstride * nk, tid - C::NC);
+        produce<C>(pr, smem, (int) ((m0 / ZEST_TILE_ROWS) * ZEST_XTILE_BYTES) + k0 * p.a_kstride,
+                   (int) ((n0 / ZEST_TILE_ROWS) * ZEST_TILE_BYTES) + k0 * W.w_kstride, p.a_kstride, W.w_kstride, ns);
         return;
     }
 
@@ -426,75 +602,230 @@ __global__ __launch_bounds__(C::NT, 1) void gemm_kernel(const uint8_t * __restri
         for (int j = 0; j < C::TJ; j++) acc[i][j] = f32x16{};
     bf16x8 af[2][C::TI], bw[2][C::TJ];
     __syncthreads();
-    read_frags<C>(af[0], bw[0], smem, fa[0], fw[0]);
+    if (ZEST_GEMM_XSTEP) read_frags<C>(af[0], bw[0], smem, fa[0], fw[0]);
     int cur = 0;
-    for (int k = 0; k < nk; k++) {
+    for (int k = 0; k < ns; k++) {
         const int nxt = cur == 2 * C::STAGE ? 0 : cur + C::STAGE;
-        consume<C>(acc, af, bw, smem, fa, fw, cur, nxt, k + 1 < nk);
+        if (!ZEST_GEMM_XSTEP) read_frags<C>(af[0], bw[0], smem, fa[0] + cur, fw[0] + cur);
+        consume<C>(acc, af, bw, smem, fa, fw, cur, nxt, ZEST_GEMM_XSTEP && k + 1 < ns);
         cur = nxt;
         __syncthreads();
     }
+    if (SPLIT && !fixup<C>(acc, p, smem, t, split, wave, lane)) return;
     if constexpr (EPI < 0)
-        store_tile<C>(acc, ep.c, M, N, ep.ldc, m0, n0, wm, wn, lane, nonfinite);
+        store_tile<C>(acc, W.c, p.M, W.n, W.ldc, m0, n0, wm, wn, lane, p.nonfinite);
     else
-        store_glu<C, EPI>(acc, smem, ep.xout, ep.h, ep.ldh, M, N / 2, m0, n0, wave, wm, wn, lane, nonfinite);
+        store_glu<C, EPI>(acc, smem, p.xout, p.h, p.ldh, p.M, W.n / 2, m0, n0, wave, wm, wn, lane, p.nonfinite);
 }
 
-template <class C, int EPI>
-int launch(const void * a, int64_t M, const void * w, int64_t N, int64_t K, const epilogue & ep, uint32_t * nf,
-           hipStream_t s, const char * name) {
-    static bool attr_set = false;
-    if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_kernel<C, EPI>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int) C::LDS_BYTES);
-        if (e != hipSuccess) return zest::fail(ZEST_E_HIP, "%s: LDS attribute: %s", name, hipGetErrorString(e));
-        attr_set = true;
-    }
-    const int64_t M_pad = zest_rows_padded(M), N_pad = zest_rows_padded(N), K_pad = zest_k_padded(K);
-    const dim3 grid((unsigned) (((N + C::BN - 1) / C::BN) * ((M + C::BM - 1) / C::BM)));
-    hipLaunchKernelGGL((gemm_kernel<C, EPI>), grid, dim3(C::NT), C::LDS_BYTES, s, (const uint8_t *) a, M_pad,
-                       (const uint8_t *) w, N_pad, (int) (K_pad / ZEST_TILE_K), ep, M, N, nf);
-    return zest::check_launch(name);
-}
-
-// 256x128 tiles (4 consumer waves of 128x64) wherever there are enough
-// tiles; 128x128 (64x64 each) for the narrow shapes.
+// 256x128 tiles (4 consumer waves of 128x64); 128x128 (64x64 each) when the
+// activations have at most 128 rows.
 #ifndef ZEST_GEMM_BIG
 #define ZEST_GEMM_BIG 256, 128, 2, 2
 #endif
 #ifndef ZEST_GEMM_SMALL
 #define ZEST_GEMM_SMALL 128, 128, 2, 2
 #endif
-#ifndef ZEST_GEMM_BIG_MIN_TILES
-#define ZEST_GEMM_BIG_MIN_TILES 160
+// Launch cost model, in K-steps of a 256x128 tile: T tiles on P CUs take
+// ceil(T/P) rounds of nk steps. S K-splits take ceil(T*S/P) rounds of nk/S
+// steps, plus the fixup: each split writes a fp32 tile and the last reads S
+// of them, about FIX steps per split (measured: 128 KB each way per split
+// through HBM). A 128x128 step costs SMALL_STEP of a 256x128 one (it does
+// half the MFMA work but not half the waiting). The cheapest plan wins.
+#ifndef ZEST_GEMM_MAX_SPLIT
+#define ZEST_GEMM_MAX_SPLIT 8
+#endif
+#ifndef ZEST_GEMM_FIX
+#define ZEST_GEMM_FIX 10.0
+#endif
+#ifndef ZEST_GEMM_SMALL_STEP
+#define ZEST_GEMM_SMALL_STEP 0.8
 #endif
 using cfg_big = gemm_cfg<ZEST_GEMM_BIG>;
 using cfg_small = gemm_cfg<ZEST_GEMM_SMALL>;
 
+// Per device and stream: the split-K workspace (grown as needed; counters
+// zeroed when allocated, and zero again after every launch).
+struct sk_space {
+    float * partial = nullptr;
+    size_t partial_bytes = 0;
+    uint32_t * counters = nullptr;
+    size_t n_counters = 0;
+};
+
+int cu_count(int dev) {
+    static std::mutex mu;
+    static std::map<int, int> cus;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cus.find(dev);
+    if (it != cus.end()) return it->second;
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+    return n;
+}
+
+int sk_reserve(hipStream_t s, size_t partial_bytes, size_t n_counters, sk_space & out, const char * name) {
+    static std::mutex mu;
+    static std::map<std::pair<int, hipStream_t>, sk_space> spaces;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return zest::fail(ZEST_E_HIP, "%s: hipGetDevice failed", name);
+    std::lock_guard<std::mutex> lock(mu);
+    sk_space & sp = spaces[{dev, s}];
+    // a launch still running on the stream may use the buffers being replaced
+    if ((sp.partial_bytes < partial_bytes || sp.n_counters < n_counters) && (sp.partial || sp.counters) &&
+        hipStreamSynchronize(s) != hipSuccess)
+        return zest::fail(ZEST_E_HIP, "%s: stream synchronize", name);
+    if (sp.partial_bytes < partial_bytes) {
+        if (sp.partial) (void) hipFree(sp.partial);
+        sp.partial = nullptr;
+        sp.partial_bytes = 0;
+        if (hipMalloc(&sp.partial, partial_bytes) != hipSuccess)
+            return zest::fail(ZEST_E_HIP, "%s: split-K workspace of %zu bytes", name, partial_bytes);
+        sp.partial_bytes = partial_bytes;
+    }
+    if (sp.n_counters < n_counters) {
+        if (sp.counters) (void) hipFree(sp.counters);
+        sp.counters = nullptr;
+        sp.n_counters = 0;
+        const size_t n = std::max(n_counters, (size_t) 4096);
+        if (hipMalloc(&sp.counters, n * 4) != hipSuccess || hipMemsetAsync(sp.counters, 0, n * 4, s) != hipSuccess)
+            return zest::fail(ZEST_E_HIP, "%s: split-K counters", name);
+        sp.n_counters = n;
+    }
+    out = sp;
+    return ZEST_OK;
+}
+
+template <class C, int EPI, bool SPLIT>
+int set_lds(const char * name) {
+    static bool attr_set = false;
+    if (!attr_set) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_kernel<C, EPI, SPLIT>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int) C::LDS_BYTES);
+        if (e != hipSuccess) return zest::fail(ZEST_E_HIP, "%s: LDS attribute: %s", name, hipGetErrorString(e));
+        attr_set = true;
+    }
+    return ZEST_OK;
+}
+
+struct gemm_plan {
+    int splits = 1;
+    double cost = 0;
+};
+
+// Tiles of a launch for one tile shape.
+int64_t tiles_of(const gemm_params & p, const int64_t * N, int BM, int BN) {
+    int64_t nt = 0;
+    for (int i = 0; i < p.nw; i++) nt += (N[i] + BN - 1) / BN;
+    return ((p.M + BM - 1) / BM) * nt;
+}
+
+// The cheapest number of K splits for T tiles of nk steps on P CUs.
+gemm_plan plan_splits(int64_t T, int nk, int64_t P, int max_split) {
+    gemm_plan best;
+    best.cost = (double) ((T + P - 1) / P) * nk;
+    for (int S = 2; S <= max_split && nk / S >= 4; S++) {
+        const double cost = (double) ((T * S + P - 1) / P) * nk / S + ZEST_GEMM_FIX * S;
+        if (cost < best.cost) {
+            best.splits = S;
+            best.cost = cost;
+        }
+    }
+    return best;
+}
+
+// Plans and launches one GEMM (a group of weights, or the fused GLU).
+template <class C, int EPI>
+int launch(gemm_params p, const int64_t * N, int splits, hipStream_t s, const char * name) {
+    p.mt = (int) ((p.M + C::BM - 1) / C::BM);
+    int nt = 0;
+    for (int i = 0; i < p.nw; i++) {
+        p.wt[i].tile0 = nt;
+        nt += (int) ((N[i] + C::BN - 1) / C::BN);
+    }
+    p.nt = nt;
+    const int64_t T = (int64_t) p.mt * nt;
+    p.splits = splits;
+    const int64_t grid = T * p.splits;
+    if (grid >= (1ll << 31) || (p.splits > 1 && grid * C::BM * C::BN * 4 >= (1ll << 31)))
+        return zest::fail(ZEST_E_ARG, "%s: %lld tiles is too many", name, (long long) T);
+    if (p.splits > 1) {
+        sk_space sp;
+        const int st = sk_reserve(s, (size_t) grid * C::BM * C::BN * 4, (size_t) T * (C::NC / 64), sp, name);
+        if (st != ZEST_OK) return st;
+        p.partial = sp.partial;
+        p.counters = sp.counters;
+    }
+    const int st = p.splits > 1 ? set_lds<C, EPI, true>(name) : set_lds<C, EPI, false>(name);
+    if (st != ZEST_OK) return st;
+    if (p.splits > 1)
+        hipLaunchKernelGGL((gemm_kernel<C, EPI, true>), dim3((unsigned) grid), dim3(C::NT), C::LDS_BYTES, s, p);
+    else
+        hipLaunchKernelGGL((gemm_kernel<C, EPI, false>), dim3((unsigned) grid), dim3(C::NT), C::LDS_BYTES, s, p);
+    return zest::check_launch(name);
+}
+
+// The tile shape and K splits of a launch (the cost model above).
+template <int EPI>
+int launch_any(gemm_params p, const int64_t * N, hipStream_t s, const char * name) {
+    int dev = 0;
+    (void) hipGetDevice(&dev);
+    const int64_t P = cu_count(dev);
+    const gemm_plan big = plan_splits(tiles_of(p, N, cfg_big::BM, cfg_big::BN), p.nk, P, ZEST_GEMM_MAX_SPLIT);
+    const int64_t T_small = tiles_of(p, N, cfg_small::BM, cfg_small::BN);
+    const double small_cost = (double) ((T_small + P - 1) / P) * p.nk * ZEST_GEMM_SMALL_STEP;
+    if (small_cost < big.cost) return launch<cfg_small, EPI>(p, N, 1, s, name);
+    return launch<cfg_big, EPI>(p, N, big.splits, s, name);
+}
+
+// The parts of a launch's parameters common to every kind.
+gemm_params base_params(const void * a, int64_t M, int64_t K, uint32_t * nonfinite) {
+    gemm_params p{};
+    p.a = (const uint8_t *) a;
+    p.M = M;
+    p.a_kstride = (int) ((zest_rows_padded(M) / ZEST_TILE_ROWS) * ZEST_XTILE_BYTES);
+    p.nk = (int) (zest_k_padded(K) / ZEST_TILE_K);
+    p.nonfinite = nonfinite;
+    return p;
+}
+
+gemm_weight weight_of(const void * w, int64_t N, float * c, int64_t ldc) {
+    gemm_weight g{};
+    g.w = (const uint8_t *) w;
+    g.c = c;
+    g.n = N;
+    g.ldc = ldc;
+    g.w_kstride = (int) ((zest_rows_padded(N) / ZEST_TILE_ROWS) * ZEST_TILE_BYTES);
+    return g;
+}
+
 } // namespace
 
-// The tile shape of a launch: 256x128 when there are enough tiles to fill
-// the GPU, else 128x128.
-template <int EPI>
-static int launch_any(const void * a, int64_t M, const void * w, int64_t N, int64_t K, const epilogue & ep,
-                      uint32_t * nf, hipStream_t s, const char * name) {
-    const int64_t big_tiles = ((M + cfg_big::BM - 1) / cfg_big::BM) * ((N + cfg_big::BN - 1) / cfg_big::BN);
-    if (big_tiles >= ZEST_GEMM_BIG_MIN_TILES) return launch<cfg_big, EPI>(a, M, w, N, K, ep, nf, s, name);
-    return launch<cfg_small, EPI>(a, M, w, N, K, ep, nf, s, name);
+extern "C" int zest_gemm_group(const void * a, int64_t M, int64_t K, int n, const void * const * w, const int64_t * N,
+                               float * const * c, const int64_t * ldc, uint32_t * nonfinite, void * stream) {
+    ZEST_REQUIRE(a && w && N && c && ldc, "zest_gemm_group: null pointer");
+    ZEST_REQUIRE(n >= 1 && n <= ZEST_GEMM_MAX_GROUP, "zest_gemm_group: %d weights (1..%d)", n, ZEST_GEMM_MAX_GROUP);
+    ZEST_REQUIRE(M > 0 && K > 0 && K % 8 == 0, "zest_gemm_group: M=%lld K=%lld", (long long) M, (long long) K);
+    ZEST_REQUIRE(zest_act_bytes(M, K) < (1ull << 31), "zest_gemm_group: activations must be under 2 GiB");
+    gemm_params p = base_params(a, M, K, nonfinite);
+    p.nw = n;
+    for (int i = 0; i < n; i++) {
+        ZEST_REQUIRE(w[i] && c[i], "zest_gemm_group: null weight or output %d", i);
+        ZEST_REQUIRE(N[i] > 0 && ldc[i] >= N[i], "zest_gemm_group: weight %d: N=%lld ldc=%lld", i, (long long) N[i],
+                     (long long) ldc[i]);
+        ZEST_REQUIRE(zest_bfp16_bytes(N[i], K) < (1ull << 31) &&
+                         (uint64_t) zest_rows_padded(M) * (uint64_t) ldc[i] * 4 < (1ull << 31),
+                     "zest_gemm_group: weight %d and its output must be under 2 GiB (N=%lld ldc=%lld)", i,
+                     (long long) N[i], (long long) ldc[i]);
+        p.wt[i] = weight_of(w[i], N[i], c[i], ldc[i]);
+    }
+    return launch_any<-1>(p, N, zest::as_stream(stream), "zest_gemm");
 }
 
 extern "C" int zest_gemm(const void * a, int64_t M, const void * w, int64_t N, int64_t K, float * c, int64_t ldc,
                          uint32_t * nonfinite, void * stream) {
-    ZEST_REQUIRE(a && w && c, "zest_gemm: null pointer");
-    ZEST_REQUIRE(M > 0 && N > 0 && K > 0 && K % 8 == 0, "zest_gemm: M=%lld N=%lld K=%lld", (long long) M,
-                 (long long) N, (long long) K);
-    ZEST_REQUIRE(ldc >= N, "zest_gemm: ldc %lld < N %lld", (long long) ldc, (long long) N);
-    ZEST_REQUIRE(zest_act_bytes(M, K) < (1ull << 31) && zest_bfp16_bytes(N, K) < (1ull << 31) &&
-                     (uint64_t) zest_rows_padded(M) * (uint64_t) ldc * 4 < (1ull << 31),
-                 "zest_gemm: operands and output must be under 2 GiB (M=%lld N=%lld K=%lld ldc=%lld)", (long long) M,
-                 (long long) N, (long long) K, (long long) ldc);
-    const epilogue ep{c, ldc, nullptr, nullptr, 0};
-    return launch_any<-1>(a, M, w, N, K, ep, nonfinite, zest::as_stream(stream), "zest_gemm");
+    return zest_gemm_group(a, M, K, 1, &w, &N, &c, &ldc, nonfinite, stream);
 }
 
 extern "C" int zest_gemm_glu(int kind, const void * a, int64_t M, const void * w_gu, int64_t F, int64_t K,
@@ -507,16 +838,21 @@ extern "C" int zest_gemm_glu(int kind, const void * a, int64_t M, const void * w
                      zest_act_bytes(M, F) < (1ull << 31),
                  "zest_gemm_glu: operands must be under 2 GiB (M=%lld F=%lld K=%lld)", (long long) M, (long long) F,
                  (long long) K);
-    const epilogue ep{nullptr, 0, (uint8_t *) xout, h, ldh};
-    hipStream_t s = zest::as_stream(stream);
+    gemm_params p = base_params(a, M, K, nonfinite);
     const int64_t N = 2 * F;
+    p.nw = 1;
+    p.wt[0] = weight_of(w_gu, N, nullptr, 0);
+    p.xout = (uint8_t *) xout;
+    p.h = h;
+    p.ldh = ldh;
+    hipStream_t s = zest::as_stream(stream);
     const char * name = "zest_gemm_glu";
     switch (kind) {
-        case ZEST_GLU_SWIGLU: return launch_any<ZEST_GLU_SWIGLU>(a, M, w_gu, N, K, ep, nonfinite, s, name);
-        case ZEST_GLU_GEGLU: return launch_any<ZEST_GLU_GEGLU>(a, M, w_gu, N, K, ep, nonfinite, s, name);
-        case ZEST_GLU_GEGLU_ERF: return launch_any<ZEST_GLU_GEGLU_ERF>(a, M, w_gu, N, K, ep, nonfinite, s, name);
-        case ZEST_GLU_GEGLU_QUICK: return launch_any<ZEST_GLU_GEGLU_QUICK>(a, M, w_gu, N, K, ep, nonfinite, s, name);
-        case ZEST_GLU_REGLU: return launch_any<ZEST_GLU_REGLU>(a, M, w_gu, N, K, ep, nonfinite, s, name);
+        case ZEST_GLU_SWIGLU: return launch_any<ZEST_GLU_SWIGLU>(p, &N, s, name);
+        case ZEST_GLU_GEGLU: return launch_any<ZEST_GLU_GEGLU>(p, &N, s, name);
+        case ZEST_GLU_GEGLU_ERF: return launch_any<ZEST_GLU_GEGLU_ERF>(p, &N, s, name);
+        case ZEST_GLU_GEGLU_QUICK: return launch_any<ZEST_GLU_GEGLU_QUICK>(p, &N, s, name);
+        case ZEST_GLU_REGLU: return launch_any<ZEST_GLU_REGLU>(p, &N, s, name);
         default: return zest::fail(ZEST_E_UNSUPPORTED, "zest_gemm_glu: GLU kind %d", kind);
     }
 }

@@ -3,7 +3,7 @@ BASELINE configurations), run through the C ABI on one GPU.
 
 A layer, for one chunk of M tokens with residual stream h [M][H] (fp32):
     RMS_NORM(h) * w_attn   -> packed (fused)        xdna-exec's norm -> q/k/v piece
-    Q, K, V = GEMM(packed, Wq / Wk / Wv)
+    Q, K, V = GEMM(packed, Wq / Wk / Wv)            one grouped launch
     (attention is excluded; the O projection's input is a stand-in: Q's output)
     pack(Q) ; O = GEMM(., Wo) ; h = h + O
     RMS_NORM(h) * w_ffn    -> packed (fused)
@@ -171,9 +171,10 @@ class Stack:
 
         for L in self.layers:
             z.rms_norm(self.h, eps, L.attn_norm, y=None, packed=self.pa)
-            gemm(self.pa, "attn_q", L, c.q, c.hidden, self.qo)
-            gemm(self.pa, "attn_k", L, c.kv, c.hidden, self.ko)
-            gemm(self.pa, "attn_v", L, c.kv, c.hidden, self.vo)
+            # q, k and v share their input: one launch (the reference's group)
+            timed(lambda: z.gemm_group(self.pa, m, [L.w["attn_q"], L.w["attn_k"], L.w["attn_v"]],
+                                       [c.q, c.kv, c.kv], c.hidden, outs=[self.qo, self.ko, self.vo]),
+                  2.0 * m * (c.q + 2 * c.kv) * c.hidden)
             z.pack_act_x(self.qo, out=self.po)
             gemm(self.po, "attn_output", L, c.hidden, c.q, self.oo)
             z.add(self.h, self.oo, y=self.h)

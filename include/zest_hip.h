@@ -101,6 +101,22 @@ ZEST_API int zest_convert_weight(int type, const void *raw, int64_t N, int64_t K
 ZEST_API int zest_gemm(const void *a, int64_t M, const void *w, int64_t N, int64_t K, float *c, int64_t ldc,
                        uint32_t *nonfinite, void *stream);
 
+/* Up to ZEST_GEMM_MAX_GROUP weights that share one activation operand, in one
+ * launch: c[i][M][N[i]] (row stride ldc[i]) = A . w[i]^T, as zest_gemm
+ * computes each (the same products; the launch's split of K among
+ * workgroups, and so the fp32 summation order, can differ). Replaces
+ * the reference's group of calls on one input (q, k and v): xdna_npu::begin /
+ * submit (src/xdna-npu.h:88-107) over the group built in xdna-exec.cpp
+ * (:509-547). A launch whose whole tiles would leave CUs idle splits each
+ * tile's K among workgroups (split-K) and sums the splits in a fixed order,
+ * through a workspace the library allocates per device and stream on first
+ * use (and grows, synchronizing the stream): calls that share a stream run
+ * in order and never share it concurrently. The same holds for zest_gemm
+ * and zest_gemm_glu, which run through the same launch. */
+#define ZEST_GEMM_MAX_GROUP 4
+ZEST_API int zest_gemm_group(const void *a, int64_t M, int64_t K, int n, const void *const *w, const int64_t *N,
+                             float *const *c, const int64_t *ldc, uint32_t *nonfinite, void *stream);
+
 /* A GLU's gate[F][K] and up[F][K] weights (GGUF rows of `type`, the same for
  * both; for a weight holding the gate and then the up, up = gate + F rows)
  * -> one packed weight of 2F rows for zest_gemm_glu (zest_bfp16_bytes(2F, K)
@@ -117,8 +133,10 @@ ZEST_API int zest_convert_weight_gu(int type, const void *gate, const void *up, 
  * h[M][F] = glu(g, u) of `kind` (zest_glu's arithmetic), written as the next
  * matmul's operand (xout, as zest_pack_act_x writes it, zest_act_bytes(M, F)
  * bytes) and/or as fp32 rows (h, row stride ldh floats); either may be NULL,
- * not both. xout is bit-exact with zest_pack_act_x of zest_glu(zest_gemm(gate),
- * zest_gemm(up)). `nonfinite` as for zest_gemm, over g, u and h. F % 32 == 0.
+ * not both. h is bit-exact with zest_glu over the gate and up columns of
+ * zest_gemm(a, w_gu) (2F columns, the same summation order), and xout with
+ * zest_pack_act_x of that. `nonfinite` as for zest_gemm, over g, u and h.
+ * F % 32 == 0.
  * Replaces the reference's fused SwiGLU matmul: find_fusions
  * (src/xdna-exec.cpp:399-431) and the NPU kernel's output mode 2
  * (kernels/bfp16_gemm/aie_kernels/aie2p/mm_bfp_acc.cc:258-278), which stores

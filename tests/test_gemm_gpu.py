@@ -153,3 +153,73 @@ def test_gemm_wide_exponent_data(zest_gpu, oracle):
     r64, ab = oracle.mul_mat_f64(wd, ad)
     worst, _ = gemm_check(c, r64, ab, k)
     assert worst <= 1.0
+
+
+def test_split_k_deterministic_and_reusable(zest_gpu, oracle):
+    # launches whose whole tiles would leave CUs idle split K over workgroups;
+    # a split tile is summed in split order by whichever workgroup finishes
+    # last. The sums must not depend on which one that is, and each launch
+    # must leave the per-tile counters at zero for the next: three rounds
+    # over three such shapes give the same bits every time.
+    import torch
+    shapes = [(2048, 2560, 9728), (1024, 2560, 16384), (600, 1000, 8192)]
+    runs = {}
+    for (M, N, K) in shapes:
+        x = Rng(M + 7).normal(M * K).reshape(M, K)
+        w = Rng(N + 7).normal(N * K, 0, 0.02).reshape(N, K)
+        c, nf, a, wp = run_gemm(zest_gpu, x, 0, w.view(np.uint8), N)
+        assert nf == 0
+        rows = np.array([0, 1, M // 2, M - 1])
+        r64, ab = oracle.mul_mat_f64(decoded(zest_gpu, oracle, wp, N, K), decoded_act(zest_gpu, oracle, a, M, K)[rows])
+        worst, maxrel = gemm_check(c[rows], r64, ab, K)
+        assert worst <= 1.0 and maxrel <= 1e-3, (M, N, K)
+        runs[(M, N, K)] = (a, wp, torch.from_numpy(c))
+    for _ in range(2):
+        for (M, N, K), (a, wp, c0) in runs.items():
+            c = zest_gpu.gemm(a, M, wp, N, K)
+            torch.cuda.synchronize()
+            assert torch.equal(c.cpu(), c0), (M, N, K)
+
+
+@pytest.mark.parametrize("M,K,ns,wtype", [
+    (2048, 2560, [4096, 1024, 1024], 12),   # config 2's q, k and v
+    (300, 200, [200, 96, 1000, 8], 0),      # ragged widths, four weights
+    (64, 512, [256], 8),
+])
+def test_gemm_group(zest_gpu, oracle, M, K, ns, wtype):
+    # one launch over weights sharing the activations, against the oracle and
+    # against each weight's own launch
+    import torch
+    quant = load_quant()
+    x = Rng(M + K).normal(M * K).reshape(M, K)
+    a = zest_gpu.pack_act_x(_dev(x))
+    ws, wds = [], []
+    for i, n in enumerate(ns):
+        w = Rng(100 + i).normal(n * K, 0, 0.02).reshape(n, K)
+        raw = quant.quantize(wtype, torch.from_numpy(w)).numpy() if wtype else w.view(np.uint8)
+        ws.append(zest_gpu.convert_weight(wtype, _dev(raw), n, K))
+    nf = torch.zeros(1, dtype=torch.int32, device="cuda")
+    outs = zest_gpu.gemm_group(a, M, ws, ns, K, nonfinite=nf)
+    torch.cuda.synchronize()
+    assert int(nf.item()) == 0
+    rows = np.unique(np.linspace(0, M - 1, min(M, 48)).astype(int))
+    ad = decoded_act(zest_gpu, oracle, a, M, K)[rows]
+    for i, n in enumerate(ns):
+        got = outs[i].cpu().numpy()
+        r64, ab = oracle.mul_mat_f64(decoded(zest_gpu, oracle, ws[i], n, K), ad)
+        worst, maxrel = gemm_check(got[rows], r64, ab, K)
+        assert worst <= 1.0 and maxrel <= 1e-3, i
+        alone = zest_gpu.gemm(a, M, ws[i], n, K).cpu().numpy()[rows]
+        worst, _ = gemm_check(got[rows], alone.astype(np.float64), ab, K)
+        assert worst <= 1.0, i
+
+
+def test_gemm_group_rejects_bad_counts(zest_gpu):
+    import torch
+    a = zest_gpu.empty_act(64, 64)
+    w = zest_gpu.empty_packed(128, 64)
+    with pytest.raises(RuntimeError):
+        zest_gpu.gemm_group(a, 64, [w] * 5, [128] * 5, 64)
+    with pytest.raises(RuntimeError):
+        zest_gpu.gemm_group(a, 64, [], [], 64)
+    torch.cuda.synchronize()
