@@ -155,10 +155,11 @@ struct producer {
         stw1 = C::A_BYTES + wrow * C::ROWB + ((2 * q + 1) ^ sw) * 16;
     }
 
-    // The A slab at byte a_off into the stage at byte `stage` of LDS.
-    __device__ void dma_a(uint8_t * smem, int stage, int a_off) const {
+    // The A slab at byte a_off into the stage at byte `stage` of LDS:
+    // instructions [i0, i0 + n) of its AI.
+    __device__ void dma_a(uint8_t * smem, int stage, int a_off, int i0 = 0, int n = AI) const {
 #pragma unroll
-        for (int i = 0; i < AI; i++)
+        for (int i = i0; i < i0 + n; i++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t) (smem + stage + (i * NPW + pw) * 1024), 16, va,
                                                      a_off + i * NPW * 1024, 0, 0);
     }
@@ -168,6 +169,29 @@ struct producer {
         for (int i = 0; i < C::BU; i++) {
             st.wm[i] = load16(rw, vwm, w_off + i * C::W_STEP);
             st.we[i] = __builtin_amdgcn_raw_buffer_load_b16(rw, vwe, w_off + i * C::W_STEP, 0);
+        }
+    }
+
+    // W unit i of a step, by the branch-free fast expansion, stored; true if
+    // the unit needs the general expansion (store_w_general) instead.
+    __device__ bool store_w_unit(const stage_regs<C> & st, int i, uint8_t * smem, int stage) const {
+        uint32_t b[8];
+        const bool slow = zest::expand16_fast(st.wm[i], st.we[i], b);
+        const int off = stage + i * (C::NP / 4) * C::ROWB;
+        lds_put_async(smem, stw0 + off, make_uint4(b[0], b[1], b[2], b[3]));
+        lds_put_async(smem, stw1 + off, make_uint4(b[4], b[5], b[6], b[7]));
+        return slow;
+    }
+
+    // Every unit of the step by the general expansion, stored.
+    __device__ void store_w_general(const stage_regs<C> & st, uint8_t * smem, int stage) const {
+#pragma unroll
+        for (int i = 0; i < C::BU; i++) {
+            uint32_t b[8];
+            zest::expand16(st.wm[i], st.we[i], b);
+            const int off = stage + i * (C::NP / 4) * C::ROWB;
+            lds_put_async(smem, stw0 + off, make_uint4(b[0], b[1], b[2], b[3]));
+            lds_put_async(smem, stw1 + off, make_uint4(b[4], b[5], b[6], b[7]));
         }
     }
 
@@ -470,6 +494,32 @@ __device__ inline void producer_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// One steady-state producer step: the A slab into `stage` by DMA, the W
+// units in `cur` (loaded a step ago) expanded and stored into it, and the
+// next step's W units loaded into `nxt`. The four producer waves of a CU
+// share its address unit, which takes about 16 cycles per load instruction
+// (a wave's A DMA alone is ~500 cycles of it), so the DMA instructions go
+// out in groups between the units' expansions: the address unit works
+// through one group while the wave expands. The scheduling barriers keep
+// that order. The W loads go last, so they are the loads the step may leave
+// in flight.
+template <class C>
+__device__ inline void steady_step(const producer<C> & pr, uint8_t * smem, int stage, int a_off,
+                                   const stage_regs<C> & cur, stage_regs<C> & nxt, int w_off_next) {
+    constexpr int AI = producer<C>::AI, PER = AI / C::BU;
+    static_assert(AI % C::BU == 0, "A instructions must split evenly between W units");
+    bool slow = false;
+#pragma unroll
+    for (int u = 0; u < C::BU; u++) {
+        pr.dma_a(smem, stage, a_off, u * PER, PER);
+        __builtin_amdgcn_sched_barrier(0);
+        slow |= pr.store_w_unit(cur, u, smem, stage);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    pr.load_w(nxt, w_off_next);
+    if (__builtin_expect(__any(slow), 0)) pr.store_w_general(cur, smem, stage);
+}
+
 // The producer's part of one tile over K-steps [k0, k0 + ns). During step k,
 // step k+2 goes into stage (k+2)%3: first its A slab by DMA, then step k+3's
 // W units are requested, then step k+2's W units (requested during step k+1)
@@ -507,18 +557,11 @@ __device__ inline void produce(const producer<C> & pr, uint8_t * smem, int a0, i
     producer_barrier();
     int stage = 2 * C::STAGE, k = 0;
     for (; k + 4 < ns; k += 2) {
-        pr.dma_a(smem, stage, a0 + (k + 2) * a_kstride);
-        pr.load_w(s1, w0 + (k + 3) * w_kstride);
-        // every request of the step is out before waiting for last step's W
-        __builtin_amdgcn_sched_barrier(0);
-        pr.store_w(s0, smem, stage);
+        steady_step<C>(pr, smem, stage, a0 + (k + 2) * a_kstride, s0, s1, w0 + (k + 3) * w_kstride);
         stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
         wait_vm_lgkm0<FLY>();
         producer_barrier();
-        pr.dma_a(smem, stage, a0 + (k + 3) * a_kstride);
-        pr.load_w(s0, w0 + (k + 4) * w_kstride);
-        __builtin_amdgcn_sched_barrier(0);
-        pr.store_w(s1, smem, stage);
+        steady_step<C>(pr, smem, stage, a0 + (k + 3) * a_kstride, s1, s0, w0 + (k + 4) * w_kstride);
         stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
         wait_vm_lgkm0<FLY>();
         producer_barrier();
