@@ -118,6 +118,24 @@ struct wkey_hash {
 };
 wkey key_of(const ggml_tensor * w) { return {w->buffer, w->data, (int) w->type, w->ne[0], w->ne[1]}; }
 
+// A GLU over matmuls that one fused gate/up GEMM replaces (the reference's
+// find_fusions, src/xdna-exec.cpp:399-431): gate and up matmuls on the same
+// input, or one matmul whose weight holds both halves (up == nullptr; then
+// `swapped` says the up rows come first), each read by nothing but the GLU.
+struct fusion {
+    const ggml_tensor * gate_mm, * up_mm;
+    ggml_tensor * glu;
+    bool swapped;
+    int64_t F, K;
+};
+
+// The cache key of a fused pair: the gate weight's, type + 1000, 2F rows (as
+// xdna_npu::fused_key, src/xdna-npu.h:65).
+wkey fused_key(const fusion & f) {
+    const ggml_tensor * w = f.gate_mm->src[0];
+    return {w->buffer, w->data, 1000 + (int) w->type, f.K, 2 * f.F};
+}
+
 // GGML_XDNA_FAIL_AFTER=n: every GEMM submission after the n-th fails;
 // GGML_XDNA_NAN_AFTER=n: every GEMM result after the n-th comes back as NaN
 // (src/xdna-npu.cpp:89-112). Both forced from the host: kernels run normally.
@@ -239,6 +257,64 @@ struct context {
         weights.emplace(key, e);
         return true;
     }
+
+    // The same for a fused gate/up pair: both weights' rows, interleaved into
+    // one entry (zest_convert_weight_gu).
+    bool ensure_fused(const fusion & f, hipStream_t on_stream, bool at_load, std::string & err) {
+        const wkey key = fused_key(f);
+        auto it = weights.find(key);
+        if (it != weights.end()) {
+            if (!at_load && it->second.ready && hipStreamWaitEvent(stream, it->second.ready, 0) != hipSuccess) {
+                err = "waiting for a weight conversion failed";
+                return false;
+            }
+            return true;
+        }
+        const ggml_tensor * gw = f.gate_mm->src[0], * uw = f.up_mm ? f.up_mm->src[0] : nullptr;
+        weight_entry e;
+        if (hipMalloc(&e.packed, zest_bfp16_bytes(2 * f.F, f.K)) != hipSuccess) {
+            err = "cannot allocate a weight-cache entry";
+            return false;
+        }
+        // each weight's raw rows in device memory (host weights go up first)
+        std::vector<void *> tmps;
+        auto dev = [&](const ggml_tensor * w) -> const uint8_t * {
+            if (!buffer_is_host(w->buffer)) return (const uint8_t *) w->data;
+            void * t = nullptr;
+            if (hipMalloc(&t, nbytes(w)) != hipSuccess ||
+                hipMemcpyAsync(t, w->data, nbytes(w), hipMemcpyHostToDevice, on_stream) != hipSuccess)
+                return nullptr;
+            tmps.push_back(t);
+            return (const uint8_t *) t;
+        };
+        const uint8_t * g = dev(gw), * u = uw ? dev(uw) : nullptr;
+        int st = ZEST_E_HIP;
+        if (g && (!uw || u)) {
+            if (!uw) {
+                // one weight: the gate's F rows, then the up's (or the reverse)
+                const uint8_t * second = g + f.F * gw->nb[1];
+                u = f.swapped ? g : second;
+                g = f.swapped ? second : g;
+            }
+            st = zest_convert_weight_gu(gw->type, g, u, f.F, f.K, e.packed, on_stream);
+        }
+        if (!tmps.empty()) (void) hipStreamSynchronize(on_stream);
+        for (void * t : tmps) (void) hipFree(t);
+        if (st != ZEST_OK) {
+            err = std::string(gw->name) + " (fused gate/up): " + (st == ZEST_E_HIP ? "upload failed" : zest_last_error());
+            (void) hipFree(e.packed);
+            return false;
+        }
+        if (at_load) {
+            (void) hipEventCreateWithFlags(&e.ready, hipEventDisableTiming);
+            (void) hipEventRecord(e.ready, on_stream);
+            built_at_load++;
+        } else {
+            built_in_graph++;
+        }
+        weights.emplace(key, e);
+        return true;
+    }
 };
 
 // Live contexts, so that freeing one of our buffers drops the cache entries of
@@ -315,6 +391,59 @@ void rope_corr_dims(int n_dims, int n_ctx_orig, float base, float beta_fast, flo
     dims[1] = std::min((float) (n_dims - 1), ceilf(dim(beta_slow)));
 }
 
+// The tensor whose packed copy a matmul input x can use: its owner when x
+// reads the owner's rows exactly (itself, or a reshape of the same rows),
+// else x itself (no packed copy is ever made for a partial view).
+const ggml_tensor * packed_key(const ggml_tensor * x) {
+    const ggml_tensor * o = owner(x);
+    if (x == o) return x;
+    return x->data == o->data && x->ne[0] == o->ne[0] && nrows(x) == nrows(o) && is_contiguous(x) ? o : x;
+}
+
+// A matmul this backend runs as a GEMM: a weight (K % 8 == 0) times F32 rows.
+bool gemm_matmul(const ggml_tensor * n) {
+    return n->op == GGML_OP_MUL_MAT && is_weight(n->src[0]) && n->src[1]->type == GGML_TYPE_F32 &&
+           is_contiguous(n->src[1]) && n->src[0]->ne[0] % 8 == 0;
+}
+
+// The fusions of a piece (src/xdna-exec.cpp:399-431): a GLU whose gate and up
+// are matmuls of the piece on the same input, with weights of one type and
+// shape, read by nothing but the GLU, inside the piece or out; or a GLU over
+// the halves of one such matmul's output. F % 32 == 0 (the fused GEMM's
+// interleave). The reference fuses SwiGLU only; every GLU kind is fused here,
+// the epilogue computing the same GLU the GLU kernel does.
+std::vector<fusion> find_fusions(const std::vector<ggml_tensor *> & nodes,
+                                 const std::unordered_set<const ggml_tensor *> & in_piece) {
+    std::vector<fusion> out;
+    for (ggml_tensor * n : nodes) {
+        if (n->op != GGML_OP_GLU || glu_kind_of(param_i32(n, 0)) < 0 || !is_contiguous(n)) continue;
+        const ggml_tensor * gm = n->src[0], * um = n->src[1];
+        if (!gemm_matmul(gm) || !in_piece.count(gm) || read_outside(gm, in_piece) || !is_contiguous(gm)) continue;
+        const ggml_tensor * gw = gm->src[0];
+        fusion f{gm, nullptr, n, false, 0, gw->ne[0]};
+        if (um) {
+            if (param_i32(n, 1) != 0 || !gemm_matmul(um) || !in_piece.count(um) || read_outside(um, in_piece) ||
+                !is_contiguous(um) || packed_key(gm->src[1]) != packed_key(um->src[1]))
+                continue;
+            const ggml_tensor * uw = um->src[0];
+            if (uw->type != gw->type || uw->ne[0] != gw->ne[0] || uw->ne[1] != gw->ne[1]) continue;
+            f.up_mm = um;
+            f.F = gw->ne[1];
+        } else {
+            if (gw->ne[1] % 2) continue;
+            f.F = gw->ne[1] / 2;
+            f.swapped = param_i32(n, 1) != 0;
+        }
+        if (f.F % 32 || n->ne[0] != f.F || nrows(n) != gm->src[1]->ne[1]) continue;
+        bool other = false;  // another reader of the gate's or up's result
+        for (const ggml_tensor * m : nodes)
+            for (int j = 0; j < GGML_MAX_SRC && m != n; j++)
+                if (m->src[j] && (owner(m->src[j]) == gm || (um && owner(m->src[j]) == um))) other = true;
+        if (!other) out.push_back(f);
+    }
+    return out;
+}
+
 struct piece {
     context & ctx;
     const ggml_cgraph * g;
@@ -329,10 +458,21 @@ struct piece {
     std::vector<pending_out> host_outs;  // results of nodes whose memory is on the host
     std::string err;
 
+    std::vector<fusion> fusions;
+    int launches = 0, fused_launches = 0, grouped_launches = 0;  // GEMM launches of the piece
+    std::unordered_map<const ggml_tensor *, const fusion *> fused_mm;   // gate/up matmul -> its fusion
+    std::unordered_map<const ggml_tensor *, const fusion *> fused_glu;  // GLU -> its fusion
+
     piece(context & c, const ggml_cgraph * graph) : ctx(c), g(graph) {
         for (int i = 0; i < g->n_nodes; i++) {
             nodes.push_back(g->nodes[i]);
             in_piece.insert(g->nodes[i]);
+        }
+        fusions = find_fusions(nodes, in_piece);
+        for (const fusion & f : fusions) {
+            fused_mm[f.gate_mm] = &f;
+            if (f.up_mm) fused_mm[f.up_mm] = &f;
+            fused_glu[f.glu] = &f;
         }
     }
 
@@ -363,14 +503,6 @@ struct piece {
         return p;
     }
 
-    // The tensor whose packed copy a matmul input x can use: its owner when x
-    // reads the owner's rows exactly (itself, or a reshape of the same rows),
-    // else x itself (no packed copy is ever made for a partial view).
-    static const ggml_tensor * packed_key(const ggml_tensor * x) {
-        const ggml_tensor * o = owner(x);
-        if (x == o) return x;
-        return x->data == o->data && x->ne[0] == o->ne[0] && nrows(x) == nrows(o) && is_contiguous(x) ? o : x;
-    }
     // whether some MUL_MAT of this piece reads t's rows as its input
     bool feeds_matmul(const ggml_tensor * t) const {
         for (const ggml_tensor * n : nodes)
@@ -413,35 +545,98 @@ struct piece {
         return fail(std::string(what) + ": " + zest_last_error());
     }
 
-    bool mul_mat(ggml_tensor * n) {
-        const ggml_tensor * w = n->src[0], * x = n->src[1];
-        const int64_t K = w->ne[0], N = w->ne[1], M = x->ne[1];
-        if (!is_weight(w) || x->type != GGML_TYPE_F32 || !is_contiguous(x) || K % 8) return fail("a matmul this backend does not take");
-        if (!ctx.ensure_weight(w, ctx.stream, false, err)) return false;
-        const void * wp = ctx.weights.at(key_of(w)).packed;
-        void * ap = nullptr;
+    // The expanded bfp16 operand of matmul input x: the packed copy made with
+    // x (a fused norm or GLU), or packed here, once per piece.
+    const void * packed_input(const ggml_tensor * x) {
         auto it = packed.find(packed_key(x));
-        if (it != packed.end()) {
-            ap = it->second;
-        } else {
-            const void * xd = in(x);
-            ap = ctx.ws_alloc(zest_act_bytes(M, K));
-            if (!xd || !ap) return fail("out of device memory for a matmul input");
-            if (!check(zest_pack_act_x((const float *) xd, M, K, (int64_t) (x->nb[1] / 4), ap, ctx.stream), "pack"))
-                return false;
-            packed[packed_key(x)] = ap;
+        if (it != packed.end()) return it->second;
+        const int64_t M = x->ne[1], K = x->ne[0];
+        const void * xd = in(x);
+        void * ap = ctx.ws_alloc(zest_act_bytes(M, K));
+        if (!xd || !ap) {
+            fail("out of device memory for a matmul input");
+            return nullptr;
         }
-        float * y = (float *) out(n);
-        if (!y) return fail("out of device memory for a matmul result");
-        const int64_t ldc = (int64_t) (n->nb[1] / 4);
-        const int64_t s = ++g_submissions;
+        if (!check(zest_pack_act_x((const float *) xd, M, K, (int64_t) (x->nb[1] / 4), ap, ctx.stream), "pack"))
+            return nullptr;
+        packed[packed_key(x)] = ap;
+        return ap;
+    }
+
+    // One GEMM submission: GGML_XDNA_FAIL_AFTER fails it; GGML_XDNA_NAN_AFTER
+    // then turns its results into NaN (src/xdna-npu.cpp:89-112).
+    bool injected_failure(int64_t & s) {
+        s = ++g_submissions;
         if (fail_after() >= 0 && s > fail_after()) return fail("an injected failure (GGML_XDNA_FAIL_AFTER)");
-        if (!check(zest_gemm(ap, M, wp, N, K, y, ldc, ctx.nonfinite, ctx.stream), "gemm")) return false;
-        if (nan_after() >= 0 && s > nan_after()) {
+        return true;
+    }
+    bool inject_nan(int64_t s, float * y, int64_t M, int64_t N, int64_t ldc) {
+        if (nan_after() < 0 || s <= nan_after()) return true;
+        if (y) {
             (void) hipMemsetAsync(y, 0xff, (size_t) ((M - 1) * ldc + N) * 4, ctx.stream);
-            if (!check(zest_check_finite(y, M, N, ldc, ctx.nonfinite, ctx.stream), "finite check")) return false;
+            return check(zest_check_finite(y, M, N, ldc, ctx.nonfinite, ctx.stream), "finite check");
         }
-        ctx.matmuls++;
+        return hipMemsetAsync(ctx.nonfinite, 0x01, sizeof(uint32_t), ctx.stream) == hipSuccess ||
+               fail("flagging an injected NaN failed");
+    }
+
+    // Matmuls on one input, consecutive in the piece: one launch (the
+    // reference's group of calls on one input, src/xdna-exec.cpp:509-547).
+    bool mul_mats(const std::vector<ggml_tensor *> & ms) {
+        const ggml_tensor * x = ms[0]->src[1];
+        const int64_t K = x->ne[0], M = x->ne[1];
+        for (ggml_tensor * n : ms)
+            if (!gemm_matmul(n)) return fail("a matmul this backend does not take");
+        const void * ap = packed_input(x);
+        if (!ap) return false;
+        const void * w[ZEST_GEMM_MAX_GROUP];
+        int64_t N[ZEST_GEMM_MAX_GROUP], ldc[ZEST_GEMM_MAX_GROUP];
+        float * y[ZEST_GEMM_MAX_GROUP];
+        for (size_t i = 0; i < ms.size(); i++) {
+            const ggml_tensor * wt = ms[i]->src[0];
+            if (!ctx.ensure_weight(wt, ctx.stream, false, err)) return false;
+            w[i] = ctx.weights.at(key_of(wt)).packed;
+            N[i] = wt->ne[1];
+            ldc[i] = (int64_t) (ms[i]->nb[1] / 4);
+            y[i] = (float *) out(ms[i]);
+            if (!y[i]) return fail("out of device memory for a matmul result");
+        }
+        int64_t s = 0;
+        if (!injected_failure(s)) return false;
+        if (!check(zest_gemm_group(ap, M, K, (int) ms.size(), w, N, y, ldc, ctx.nonfinite, ctx.stream), "gemm"))
+            return false;
+        for (size_t i = 0; i < ms.size(); i++)
+            if (!inject_nan(s, y[i], M, N[i], ldc[i])) return false;
+        ctx.matmuls += (int64_t) ms.size();
+        launches++;
+        if (ms.size() > 1) grouped_launches++;
+        return true;
+    }
+
+    // A fused gate/up GEMM, run where its GLU stands: the GLU's fp32 rows
+    // where something other than a matmul reads them, and its packed copy
+    // where a matmul of the piece does.
+    bool fused_glu_gemm(const fusion & f) {
+        const ggml_tensor * x = f.gate_mm->src[1];
+        const int64_t M = x->ne[1];
+        const void * ap = packed_input(x);
+        if (!ap) return false;
+        if (!ctx.ensure_fused(f, ctx.stream, false, err)) return false;
+        const void * wp = ctx.weights.at(fused_key(f)).packed;
+        ggml_tensor * n = f.glu;
+        void * pk = packed_for(n, M, f.F);
+        float * y = pk && only_matmuls_read(n) ? nullptr : (float *) out(n);
+        if (!y && !pk) return fail("out of device memory for a fused GLU result");
+        int64_t s = 0;
+        if (!injected_failure(s)) return false;
+        if (!check(zest_gemm_glu(glu_kind_of(param_i32(n, 0)), ap, M, wp, f.F, f.K, pk, y, y ? (int64_t) (n->nb[1] / 4) : 0,
+                                 ctx.nonfinite, ctx.stream),
+                   "fused gate/up gemm"))
+            return false;
+        if (!inject_nan(s, y, M, f.F, y ? (int64_t) (n->nb[1] / 4) : 0)) return false;
+        ctx.matmuls += f.up_mm ? 2 : 1;
+        launches++;
+        fused_launches++;
         return true;
     }
 
@@ -512,9 +707,34 @@ struct piece {
             if (is_noop(n)) continue;
             bool ok = true;
             switch (n->op) {
-                case GGML_OP_MUL_MAT: ok = mul_mat(n); break;
+                case GGML_OP_MUL_MAT: {
+                    if (fused_mm.count(n)) {
+                        // runs with its GLU; its input is packed now, while it is sure to be intact
+                        ok = packed_input(n->src[1]) != nullptr;
+                        break;
+                    }
+                    // the run of matmuls on the same input that follows
+                    std::vector<ggml_tensor *> ms{n};
+                    size_t last = i;
+                    for (size_t j = i + 1; j < nodes.size() && ms.size() < ZEST_GEMM_MAX_GROUP; j++) {
+                        ggml_tensor * m = nodes[j];
+                        if (is_noop(m)) continue;
+                        if (m->op != GGML_OP_MUL_MAT || fused_mm.count(m) ||
+                            packed_key(m->src[1]) != packed_key(n->src[1]))
+                            break;
+                        ms.push_back(m);
+                        last = j;
+                    }
+                    ok = mul_mats(ms);
+                    i = last;
+                    break;
+                }
                 case GGML_OP_RMS_NORM: ok = rms_norm(n, i); break;
-                case GGML_OP_GLU: ok = glu(n); break;
+                case GGML_OP_GLU: {
+                    auto f = fused_glu.find(n);
+                    ok = f != fused_glu.end() ? fused_glu_gemm(*f->second) : glu(n);
+                    break;
+                }
                 case GGML_OP_ROPE: ok = rope(n); break;
                 case GGML_OP_MUL: {
                     const void * xd = in(n->src[0]), * wd = in(n->src[1]);
@@ -590,6 +810,10 @@ ggml_status graph_compute(ggml_backend_t backend, ggml_cgraph * cgraph) {
     }
     ctx.compute_ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     ctx.pieces++;
+    static const int64_t trace_level = env_int("GGML_XDNA_TRACE", 0);
+    if (trace_level >= 2)
+        fprintf(stderr, "xdna piece: %d GEMM launches (%d fused gate/up, %d grouped)\n", p.launches, p.fused_launches,
+                p.grouped_launches);
     if (trace() && ctx.matmuls >= 196) {
         fprintf(stderr, "xdna times, %lld matmuls in %lld pieces: all %.1f ms; weight copies %lld at load, %lld in pieces\n",
                 (long long) ctx.matmuls, (long long) ctx.pieces, ctx.compute_ms, (long long) ctx.built_at_load,
@@ -613,12 +837,25 @@ void graph_optimize(ggml_backend_t backend, ggml_cgraph * cgraph, ggml_backend_g
     if (!at_load || mode() != run_mode::gpu || broken()) return;
     context & ctx = *(context *) backend->context;
     if (!ctx.loader) return;
-    for (int i = 0; i < cgraph->n_nodes; i++) {
-        const ggml_tensor * n = cgraph->nodes[i];
-        if (n->op != GGML_OP_MUL_MAT) continue;
+    // the fusions graph_compute will make: their interleaved entries instead
+    std::vector<ggml_tensor *> nodes(cgraph->nodes, cgraph->nodes + cgraph->n_nodes);
+    const std::unordered_set<const ggml_tensor *> in_piece(nodes.begin(), nodes.end());
+    std::unordered_set<const ggml_tensor *> fused;
+    std::string err;
+    for (const fusion & f : find_fusions(nodes, in_piece)) {
+        const ggml_tensor * gw = f.gate_mm->src[0], * uw = f.up_mm ? f.up_mm->src[0] : nullptr;
+        if (!gw->data || !in_weight_buffer(gw) || (uw && (!uw->data || !in_weight_buffer(uw)))) continue;
+        if (!ctx.ensure_fused(f, ctx.loader, true, err)) {
+            mark_broken("building a weight-cache entry at load: " + err);
+            return;
+        }
+        fused.insert(f.gate_mm);
+        if (f.up_mm) fused.insert(f.up_mm);
+    }
+    for (const ggml_tensor * n : nodes) {
+        if (n->op != GGML_OP_MUL_MAT || fused.count(n)) continue;
         const ggml_tensor * w = n->src[0];
         if (!w->data || !in_weight_buffer(w) || !is_weight(w) || w->ne[0] % 8) continue;
-        std::string err;
         if (!ctx.ensure_weight(w, ctx.loader, true, err)) {
             mark_broken("building a weight-cache entry at load: " + err);
             return;

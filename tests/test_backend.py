@@ -87,7 +87,10 @@ def test_mul_mat_gpu_conversion_in_graph():
 
 @pytest.mark.gpu
 def test_host_ops_gpu():
-    run("test_host_ops")
+    out = run("test_host_ops", GGML_XDNA_TRACE="2")
+    # the FFN block's gate and up ran as one fused launch with the SwiGLU,
+    # and q, k and v as one grouped launch
+    assert "1 fused gate/up, 1 grouped" in out
 
 
 @pytest.mark.gpu
