@@ -11,11 +11,24 @@ one whole prompt (4 chunks x 36 layers); inputs resident in HBM.
 
 Prints one JSON line: value = MUL_MAT TFLOP/s of the whole step (matmul FLOPs
 over wall time, packs and fused host ops included), with tok/s, the GEMM
-kernel's roofline from HIP events around every GEMM launch of the timed
-steps, and the reference's CPU path (the xdna-ref loop restated in
-oracle/, built with the reference's flags) on a bounded sample.
+kernel's roofline (the step's GEMM launches run back to back between two HIP
+events: the same shapes, tiles and K splits), and the reference's CPU path
+(the xdna-ref loop restated in oracle/, built with the reference's flags) on
+a bounded sample.
 
-    python bench.py [--steps K] [--warmup W] [--workload qwen3-4b] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--workload qwen3-4b] [--chunk M] [--no-cpu]
+
+The roofline's `traffic` (HBM bytes per GEMM launch) comes from two
+rocprofv3 counter runs of this script's probe mode, summarised into
+profiles/gemm_traffic_<workload>.json:
+
+    rocprofv3 --pmc FETCH_SIZE --output-format csv -d <dir_f> -o run -- python3 bench.py --traffic-probe
+    rocprofv3 --pmc WRITE_SIZE --output-format csv -d <dir_w> -o run -- python3 bench.py --traffic-probe
+    python3 bench.py --traffic-summary <dir_f> <dir_w> > profiles/gemm_traffic_qwen3-4b.json
+
+The probe runs one prompt step, then a calibration kernel of known traffic
+(zest_scale over 64 Mi floats: 256 MiB read, 256 MiB written); each counter
+is scaled by what it reads for that kernel.
 """
 from __future__ import annotations
 
@@ -131,6 +144,62 @@ def convert_bandwidth(z, wtype: int, n: int, k: int, reps: int = 10) -> dict:
             "frac": round(gbs / HBM_PEAK, 3)}
 
 
+CALIB_FLOATS = 64 << 20  # the calibration kernel's floats: 256 MiB each way
+
+
+def traffic_probe(args) -> int:
+    """One prompt step of the workload, then the calibration kernel."""
+    import torch
+    z = load_pkg()
+    from ggml_xdna_amd.stack import CONFIGS, Stack
+    torch.cuda.set_device(0)
+    z.init(0)
+    cfg = CONFIGS[args.workload]
+    stack = Stack(cfg, seed=0, chunk=args.chunk)
+    stack.run_prompt()
+    torch.cuda.synchronize()
+    x = torch.randn(CALIB_FLOATS, device="cuda")
+    y = torch.empty_like(x)
+    z.scale(x, 1.0, 0.0, y=y)
+    torch.cuda.synchronize()
+    print(f"[probe] {cfg.name}: one step and the calibration kernel done", flush=True)
+    return 0
+
+
+def _counter_rows(d: str):
+    import csv
+    import glob
+    for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+        yield from csv.DictReader(open(f))
+
+
+def traffic_summary(fetch_dir: str, write_dir: str) -> int:
+    """Average FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of the GEMM
+    launches, each scaled by the calibration kernel's reading."""
+    res = {}
+    for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        gemm, calib = [], []
+        for r in _counter_rows(d):
+            if r.get("Counter_Name") != counter:
+                continue
+            v = float(r["Counter_Value"]) * 1024.0  # KiB -> bytes
+            if "gemm_kernel" in r["Kernel_Name"]:
+                gemm.append(v)
+            elif "scale_kernel" in r["Kernel_Name"]:
+                calib.append(v)
+        if not gemm or not calib:
+            print(f"no {counter} rows for the GEMM or the calibration kernel under {d}", file=sys.stderr)
+            return 1
+        factor = CALIB_FLOATS * 4.0 / max(calib)
+        res[counter] = {"raw_bytes_per_launch": sum(gemm) / len(gemm), "launches": len(gemm),
+                        "calibration_raw_bytes": max(calib), "factor": factor,
+                        "bytes_per_launch": sum(gemm) / len(gemm) * factor}
+    line = {"kernel": "gemm_kernel", "fetch": res["FETCH_SIZE"], "write": res["WRITE_SIZE"],
+            "traffic_bytes_per_launch": res["FETCH_SIZE"]["bytes_per_launch"] + res["WRITE_SIZE"]["bytes_per_launch"]}
+    print(json.dumps(line, indent=1))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -140,7 +209,14 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=2048)
     ap.add_argument("--unfused", action="store_true", help="gate and up as two GEMMs plus a SwiGLU kernel")
+    ap.add_argument("--chunk", type=int, default=None, help="tokens per chunk (default: the workload's)")
+    ap.add_argument("--traffic-probe", action="store_true", help="one step and the calibration kernel, for rocprofv3")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
     args = ap.parse_args()
+    if args.traffic_summary:
+        return traffic_summary(*args.traffic_summary)
+    if args.traffic_probe:
+        return traffic_probe(args)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
               file=sys.stderr)
@@ -155,7 +231,7 @@ def main() -> int:
     z.self_test()
     cfg = CONFIGS[args.workload]
     t_build = time.perf_counter()
-    stack = Stack(cfg, seed=0, fused=not args.unfused)
+    stack = Stack(cfg, seed=0, fused=not args.unfused, chunk=args.chunk)
     torch.cuda.synchronize()
     print(f"[bench] {cfg.name}: weights converted in {time.perf_counter() - t_build:.1f} s "
           f"(kernel time {stack.convert_ms:.1f} ms)", file=sys.stderr, flush=True)
@@ -164,23 +240,40 @@ def main() -> int:
         stack.run_prompt()
     torch.cuda.synchronize()
 
-    events: list = []
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        stack.run_prompt(gemm_events=events)
+        stack.run_prompt()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms_step = (t1 - t0) * 1e3 / args.steps
 
     flops_step = cfg.flops_per_token() * cfg.tokens
     value = flops_step / (ms_step * 1e-3) / 1e12
-    gemm_ms = sum(a.elapsed_time(b) for a, b, _ in events)
-    gemm_flops = sum(f for _, _, f in events)
+    # The GEMM kernel's roofline: the same launches back to back, timed with
+    # HIP events on the stream they run on (the host ops between them are
+    # what the step adds)
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    launches, gemm_flops = 0, 0.0
+    for _ in range(args.steps):
+        n, f = stack.run_gemms()
+        launches += n
+        gemm_flops += f
+    e1.record(stream)
+    e1.synchronize()
+    gemm_ms = e0.elapsed_time(e1)
     achieved = gemm_flops / (gemm_ms * 1e-3) / 1e12
-    print(f"[bench] {args.steps} steps: {ms_step:.2f} ms/step, GEMM {gemm_ms / args.steps:.2f} ms/step over "
-          f"{len(events) // args.steps} launches", file=sys.stderr, flush=True)
+    print(f"[bench] {args.steps} steps: {ms_step:.2f} ms/step; the GEMMs alone {gemm_ms / args.steps:.2f} ms/step over "
+          f"{launches // args.steps} launches", file=sys.stderr, flush=True)
 
-    pack = pack_bandwidth(z, cfg.chunk, cfg.q)
+    pack = pack_bandwidth(z, stack.chunk, cfg.q)
+    # HBM bytes per GEMM launch, from the committed counter runs of this workload
+    traffic, traffic_src = None, None
+    tf = ROOT / "profiles" / f"gemm_traffic_{cfg.name}.json"
+    if tf.exists() and stack.chunk == cfg.chunk and not args.unfused:
+        traffic = round(json.loads(tf.read_text())["traffic_bytes_per_launch"])
+        traffic_src = str(tf.relative_to(ROOT))
     convert = [convert_bandwidth(z, cfg.ffn_type, cfg.ffn, cfg.hidden),
                convert_bandwidth(z, cfg.down_type, cfg.hidden, cfg.ffn)]
     line = {
@@ -197,8 +290,8 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": f"{cfg.name} stack: {cfg.layers} layers, hidden {cfg.hidden}, {cfg.tokens}-token "
-                               f"prompt in {cfg.chunk}-token chunks, random-init GGUF weights, attention excluded",
-                   "tokens": cfg.tokens, "chunk": cfg.chunk, "layers": cfg.layers,
+                               f"prompt in {stack.chunk}-token chunks, random-init GGUF weights, attention excluded",
+                   "tokens": cfg.tokens, "chunk": stack.chunk, "layers": cfg.layers,
                    "gate_up": "two GEMMs + SwiGLU kernel" if args.unfused else
                               "one fused GEMM, SwiGLU and pack in its epilogue",
                    "operands": "bfp16 (8-value blocks, shared exponent, int8 mantissas) expanded to bf16 for "
@@ -206,8 +299,10 @@ def main() -> int:
         "pct_bf16_peak": round(100 * value / BF16_PEAK, 2),
         "tok_per_s": round(cfg.tokens / (ms_step * 1e-3), 1),
         "roofline": {"bound": "mfma", "kernel": "gemm_kernel", "achieved": round(achieved, 2), "peak": BF16_PEAK,
-                     "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK, 4), "traffic": None,
-                     "launches": len(events), "avg_launch_us": round(gemm_ms * 1e3 / len(events), 2)},
+                     "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK, 4), "traffic": traffic,
+                     "traffic_source": traffic_src,
+                     "launches": launches, "avg_launch_us": round(gemm_ms * 1e3 / launches, 2),
+                     "timed": "the step's GEMM launches back to back between two HIP events"},
         "convert": convert,
         "pack": pack,
     }

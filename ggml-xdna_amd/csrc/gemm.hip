@@ -669,17 +669,21 @@ __global__ __launch_bounds__(C::NT, 1) void gemm_kernel(const gemm_params p) {
 #ifndef ZEST_GEMM_SMALL
 #define ZEST_GEMM_SMALL 128, 128, 2, 2
 #endif
-// Launch cost model, in K-steps of a 256x128 tile: T tiles on P CUs take
-// ceil(T/P) rounds of nk steps. S K-splits take ceil(T*S/P) rounds of nk/S
-// steps, plus the fixup: each split writes a fp32 tile and the last reads S
-// of them, about FIX steps per split (measured: 128 KB each way per split
-// through HBM). A 128x128 step costs SMALL_STEP of a 256x128 one (it does
-// half the MFMA work but not half the waiting). The cheapest plan wins.
+// Launch cost model, in K-steps of a 256x128 tile at full occupancy (about
+// 0.85 us): T tiles on P CUs take ceil(T/P) rounds of nk steps, plus PROLOGUE
+// steps per round to fill the pipeline. S K-splits take ceil(T*S/P) rounds of
+// nk/S steps, plus the fixup: every split writes its fp32 tile and the last
+// reads all S back through HBM, 2*T*S*BM*BN*4 bytes at about FIX_BW bytes
+// per step. A 128x128 step costs SMALL_STEP of a 256x128 one (half the MFMA
+// work, not half the waiting). The cheapest plan wins.
 #ifndef ZEST_GEMM_MAX_SPLIT
-#define ZEST_GEMM_MAX_SPLIT 8
+#define ZEST_GEMM_MAX_SPLIT 16
 #endif
-#ifndef ZEST_GEMM_FIX
-#define ZEST_GEMM_FIX 10.0
+#ifndef ZEST_GEMM_PROLOGUE
+#define ZEST_GEMM_PROLOGUE 2.0
+#endif
+#ifndef ZEST_GEMM_FIX_BW
+#define ZEST_GEMM_FIX_BW 4.25e6  // bytes per step: ~5 TB/s x 0.85 us
 #endif
 #ifndef ZEST_GEMM_SMALL_STEP
 #define ZEST_GEMM_SMALL_STEP 0.8
@@ -764,12 +768,14 @@ int64_t tiles_of(const gemm_params & p, const int64_t * N, int BM, int BN) {
     return ((p.M + BM - 1) / BM) * nt;
 }
 
-// The cheapest number of K splits for T tiles of nk steps on P CUs.
-gemm_plan plan_splits(int64_t T, int nk, int64_t P, int max_split) {
+// The cheapest number of K splits for T tiles of nk steps on P CUs, with
+// tiles of tile_bytes fp32 and steps of `step` 256x128-steps.
+gemm_plan plan_splits(int64_t T, int nk, int64_t P, double tile_bytes, double step) {
     gemm_plan best;
-    best.cost = (double) ((T + P - 1) / P) * nk;
-    for (int S = 2; S <= max_split && nk / S >= 4; S++) {
-        const double cost = (double) ((T * S + P - 1) / P) * nk / S + ZEST_GEMM_FIX * S;
+    best.cost = (double) ((T + P - 1) / P) * (nk + ZEST_GEMM_PROLOGUE) * step;
+    for (int S = 2; S <= ZEST_GEMM_MAX_SPLIT && nk / S >= 4; S++) {
+        const double cost = (double) ((T * S + P - 1) / P) * ((double) nk / S + ZEST_GEMM_PROLOGUE) * step +
+                            2.0 * T * S * tile_bytes / ZEST_GEMM_FIX_BW;
         if (cost < best.cost) {
             best.splits = S;
             best.cost = cost;
@@ -815,10 +821,11 @@ int launch_any(gemm_params p, const int64_t * N, hipStream_t s, const char * nam
     int dev = 0;
     (void) hipGetDevice(&dev);
     const int64_t P = cu_count(dev);
-    const gemm_plan big = plan_splits(tiles_of(p, N, cfg_big::BM, cfg_big::BN), p.nk, P, ZEST_GEMM_MAX_SPLIT);
-    const int64_t T_small = tiles_of(p, N, cfg_small::BM, cfg_small::BN);
-    const double small_cost = (double) ((T_small + P - 1) / P) * p.nk * ZEST_GEMM_SMALL_STEP;
-    if (small_cost < big.cost) return launch<cfg_small, EPI>(p, N, 1, s, name);
+    const gemm_plan big = plan_splits(tiles_of(p, N, cfg_big::BM, cfg_big::BN), p.nk, P,
+                                      (double) cfg_big::BM * cfg_big::BN * 4, 1.0);
+    const gemm_plan small = plan_splits(tiles_of(p, N, cfg_small::BM, cfg_small::BN), p.nk, P,
+                                        (double) cfg_small::BM * cfg_small::BN * 4, ZEST_GEMM_SMALL_STEP);
+    if (small.cost < big.cost) return launch<cfg_small, EPI>(p, N, small.splits, s, name);
     return launch<cfg_big, EPI>(p, N, big.splits, s, name);
 }
 

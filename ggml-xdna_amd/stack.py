@@ -78,7 +78,7 @@ class Layer:
 class Stack:
     """Weights resident in HBM plus per-chunk work buffers."""
 
-    def __init__(self, cfg: StackConfig, seed: int = 0, device: str = "cuda", fused: bool = True):
+    def __init__(self, cfg: StackConfig, seed: int = 0, device: str = "cuda", fused: bool = True, chunk=None):
         import torch
         self.cfg, self.device, self.fused = cfg, device, fused
         g = torch.Generator(device=device)
@@ -121,8 +121,8 @@ class Stack:
             L.ffn_norm = 1.0 + 0.1 * torch.randn(cfg.hidden, generator=g, device=device)
             self.layers.append(L)
         del raw_by_shape
-        self.chunk = cfg.chunk
-        self._alloc(cfg.chunk)
+        self.chunk = chunk or cfg.chunk
+        self._alloc(self.chunk)
         x = torch.randn((cfg.tokens, cfg.hidden), generator=g, device=device)
         if cfg.outlier_frac > 0:
             nout = max(1, int(cfg.hidden * cfg.outlier_frac))
@@ -154,7 +154,11 @@ class Stack:
         import torch
         c, m = self.cfg, x_chunk.shape[0]
         eps = 1e-6
-        self.h.copy_(x_chunk)
+        # a short last chunk uses the first m rows of every buffer (the
+        # packed operands are laid out for m rows by their writer and reader)
+        h, qo, ko, vo, oo, do = (t[:m] for t in (self.h, self.qo, self.ko, self.vo, self.oo, self.do))
+        go, uo = (self.go[:m], self.uo[:m]) if not self.fused else (None, None)
+        h.copy_(x_chunk)
 
         def timed(fn, flops):
             if gemm_events is None:
@@ -170,25 +174,52 @@ class Stack:
             timed(lambda: z.gemm(a, m, L.w[wname], n, k, out=out), 2.0 * m * n * k)
 
         for L in self.layers:
-            z.rms_norm(self.h, eps, L.attn_norm, y=None, packed=self.pa)
+            z.rms_norm(h, eps, L.attn_norm, y=None, packed=self.pa)
             # q, k and v share their input: one launch (the reference's group)
             timed(lambda: z.gemm_group(self.pa, m, [L.w["attn_q"], L.w["attn_k"], L.w["attn_v"]],
-                                       [c.q, c.kv, c.kv], c.hidden, outs=[self.qo, self.ko, self.vo]),
+                                       [c.q, c.kv, c.kv], c.hidden, outs=[qo, ko, vo]),
                   2.0 * m * (c.q + 2 * c.kv) * c.hidden)
-            z.pack_act_x(self.qo, out=self.po)
-            gemm(self.po, "attn_output", L, c.hidden, c.q, self.oo)
-            z.add(self.h, self.oo, y=self.h)
-            z.rms_norm(self.h, eps, L.ffn_norm, y=None, packed=self.pa)
+            z.pack_act_x(qo, out=self.po)
+            gemm(self.po, "attn_output", L, c.hidden, c.q, oo)
+            z.add(h, oo, y=h)
+            z.rms_norm(h, eps, L.ffn_norm, y=None, packed=self.pa)
             if self.fused:
                 timed(lambda: z.gemm_glu(z.GLU_SWIGLU, self.pa, m, L.w["ffn_gate_up"], c.ffn, c.hidden,
                                          xout=self.pd), 4.0 * m * c.ffn * c.hidden)
             else:
-                gemm(self.pa, "ffn_gate", L, c.ffn, c.hidden, self.go)
-                gemm(self.pa, "ffn_up", L, c.ffn, c.hidden, self.uo)
-                z.glu(z.GLU_SWIGLU, self.go, self.uo, c.ffn, y=None, packed=self.pd)
-            gemm(self.pd, "ffn_down", L, c.hidden, c.ffn, self.do)
-            z.add(self.h, self.do, y=self.h)
-        return self.h
+                gemm(self.pa, "ffn_gate", L, c.ffn, c.hidden, go)
+                gemm(self.pa, "ffn_up", L, c.ffn, c.hidden, uo)
+                z.glu(z.GLU_SWIGLU, go, uo, c.ffn, y=None, packed=self.pd)
+            gemm(self.pd, "ffn_down", L, c.hidden, c.ffn, do)
+            z.add(h, do, y=h)
+        return h
+
+    def run_gemms(self):
+        """The GEMM launches of one prompt step, back to back and on the
+        operands the last step left (the same shapes, tiles and splits): the
+        GEMM kernel's own time, without the host ops between launches.
+        Returns (launches, flops)."""
+        c = self.cfg
+        n, flops = 0, 0.0
+        for t0 in range(0, c.tokens, self.chunk):
+            m = min(self.chunk, c.tokens - t0)
+            qo, ko, vo, oo, do = (t[:m] for t in (self.qo, self.ko, self.vo, self.oo, self.do))
+            for L in self.layers:
+                z.gemm_group(self.pa, m, [L.w["attn_q"], L.w["attn_k"], L.w["attn_v"]], [c.q, c.kv, c.kv],
+                             c.hidden, outs=[qo, ko, vo])
+                z.gemm(self.po, m, L.w["attn_output"], c.hidden, c.q, out=oo)
+                if self.fused:
+                    z.gemm_glu(z.GLU_SWIGLU, self.pa, m, L.w["ffn_gate_up"], c.ffn, c.hidden, xout=self.pd)
+                    n += 3
+                else:
+                    z.gemm(self.pa, m, L.w["ffn_gate"], c.ffn, c.hidden, out=self.go[:m])
+                    z.gemm(self.pa, m, L.w["ffn_up"], c.ffn, c.hidden, out=self.uo[:m])
+                    n += 4
+                z.gemm(self.pd, m, L.w["ffn_down"], c.hidden, c.ffn, out=do)
+                n += 1
+                flops += 2.0 * m * ((c.q + 2 * c.kv) * c.hidden + c.hidden * c.q + 2 * c.ffn * c.hidden +
+                                    c.hidden * c.ffn)
+        return n, flops
 
     def run_prompt(self, gemm_events=None):
         for t0 in range(0, self.cfg.tokens, self.chunk):
