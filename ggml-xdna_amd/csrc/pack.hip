@@ -21,47 +21,79 @@ using zest::encode8;
 // holds a gate value and its up value in the same lane.
 __device__ inline int64_t dst_row(int64_t r, int gu) { return gu < 0 ? r : (r >> 5) * 64 + gu * 32 + (r & 31); }
 
-// One thread encodes two blocks (16 values) of one row: 64 bytes of fp32 in,
-// a 16-byte mantissa store and a 2-byte exponent store out. A workgroup is one
-// 16-row tile row by 256 columns (4 tiles): thread t takes row t/16 and the
-// 16-column quarter t%16. Rows past M and columns past K become zero blocks.
-// XOUT: write the expanded operand (two 16-byte bf16 stores) instead.
+// One workgroup packs a 16-row band of 256 columns (four tiles). Load i reads
+// columns 64i..64i+63 of the band (a column past K reads as zero): thread t
+// takes row t/16 and the 4 floats
+// at column 64i + 4(t%16), so the 16 threads of a row read 256 contiguous
+// bytes. A bfp16 block is 8 columns, two threads: the pair's exponent is the
+// larger of their two maxima (one lane exchange); each thread then encodes
+// its 4 values exactly as encode8 does, into one mantissa dword at tile i,
+// row t/16, byte 4(t%16), so a wave's store covers 4 whole tile rows (256
+// contiguous bytes). The 8 exponent bytes of a tile row come from threads
+// t%16 = 0 and 8, which gather 4 each and store a dword. Rows past M and
+// columns past K become zero blocks.
+// XOUT: write the expanded operand instead (the 4 decoded values as bf16,
+// 8 bytes, at row t/16 of the 2048-byte tile).
 template <bool XOUT>
 __global__ __launch_bounds__(256) void pack_act_kernel(const float * __restrict__ x, int64_t M, int64_t K, int64_t ldx,
                                                        uint8_t * __restrict__ dst, int64_t R_pad, int64_t K_pad, int gu) {
-    const int t = threadIdx.x;
-    const int64_t r = (int64_t) blockIdx.y * ZEST_TILE_ROWS + (t >> 4);
+    const int t = threadIdx.x, j = t & 15, rr = t >> 4;
+    const int64_t r = (int64_t) blockIdx.y * ZEST_TILE_ROWS + rr;
     const int64_t rt = dst_row((int64_t) blockIdx.y * ZEST_TILE_ROWS, gu) / ZEST_TILE_ROWS;  // 16-row groups stay whole
-    const int64_t col = (int64_t) blockIdx.x * 256 + (t & 15) * 16;
-    if (col >= K_pad) return;
-    float v[16];
-    const bool row_ok = r < M;
-    if (row_ok && col + 16 <= K && (ldx & 3) == 0) {
-        typedef float f32x4 __attribute__((ext_vector_type(4)));
-        const f32x4 * p = reinterpret_cast<const f32x4 *>(x + r * ldx + col);
+    const bool row_ok = r < M, vec = (ldx & 3) == 0;
+    // all four loads first, then the encodes: 64 bytes in flight per thread
+    float va[4][4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const f32x4 q = __builtin_nontemporal_load(p + i);
-            v[4 * i] = q.x;
-            v[4 * i + 1] = q.y;
-            v[4 * i + 2] = q.z;
-            v[4 * i + 3] = q.w;
+    for (int i = 0; i < 4; i++) {
+        const int64_t col = (int64_t) blockIdx.x * 256 + i * 64 + j * 4;
+        if (row_ok && col + 4 <= K && vec) {
+            typedef float f32x4 __attribute__((ext_vector_type(4)));
+            const f32x4 q = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(x + r * ldx + col));
+            va[i][0] = q.x;
+            va[i][1] = q.y;
+            va[i][2] = q.z;
+            va[i][3] = q.w;
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; q++) va[i][q] = (row_ok && col + q < K) ? x[r * ldx + col + q] : 0.0f;
         }
-    } else {
+    }
 #pragma unroll
-        for (int i = 0; i < 16; i++) v[i] = (row_ok && col + i < K) ? x[r * ldx + col + i] : 0.0f;
+    for (int i = 0; i < 4; i++) {
+        const int64_t c0 = (int64_t) blockIdx.x * 256 + i * 64;  // the tile's first column
+        if (c0 >= K_pad) break;
+        const float * v = va[i];
+        uint32_t e = 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) e = max(e, (__float_as_uint(v[q]) >> 23) & 0xffu);
+        e = max(e, (uint32_t) __shfl_xor((int) e, 1));
+        const int sh = 133 - (int) e;
+        int32_t qi[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            qi[q] = (int32_t) __builtin_amdgcn_fmed3f(__builtin_rintf(__builtin_ldexpf(v[q], sh)), -128.0f, 127.0f);
+        const int64_t kc = c0 / ZEST_TILE_K;
+        if (XOUT) {
+            // q * 2^(e-133) is exact in fp32 and in bf16 (at most 8 significant bits)
+            const float sc = zest::block_scale(e);
+            uint32_t b[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) b[q] = __float_as_uint((float) qi[q] * sc) >> 16;
+            *reinterpret_cast<uint2 *>(dst + zest_xtile_offset(rt, kc, R_pad) + rr * 128 + j * 8) =
+                make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
+        } else {
+            uint8_t * tile = dst + zest_tile_offset(rt, kc, R_pad);
+            *reinterpret_cast<uint32_t *>(tile + rr * ZEST_TILE_K + j * 4) =
+                ((uint32_t) qi[0] & 0xffu) | (((uint32_t) qi[1] & 0xffu) << 8) | (((uint32_t) qi[2] & 0xffu) << 16) |
+                (((uint32_t) qi[3] & 0xffu) << 24);
+            // blocks j/2, j/2+1, j/2+2, j/2+3 of the row, from threads j, j+2, j+4, j+6
+            const uint32_t e1 = (uint32_t) __shfl_down((int) e, 2), e2 = (uint32_t) __shfl_down((int) e, 4),
+                           e3 = (uint32_t) __shfl_down((int) e, 6);
+            if ((j & 7) == 0)
+                *reinterpret_cast<uint32_t *>(tile + ZEST_TILE_MANT + rr * 8 + (j >> 3) * 4) =
+                    e | (e1 << 8) | (e2 << 16) | (e3 << 24);
+        }
     }
-    if (XOUT) {
-        zest::store_expanded16(dst, R_pad, rt * ZEST_TILE_ROWS + (t >> 4), col, v);
-        return;
-    }
-    uint4 m;
-    const uint32_t e0 = encode8(v, m.x, m.y);
-    const uint32_t e1 = encode8(v + 8, m.z, m.w);
-    uint8_t * tile = dst + zest_tile_offset(rt, col / ZEST_TILE_K, R_pad);
-    const int rr = t >> 4, q = (t & 15) & 3;
-    *reinterpret_cast<uint4 *>(tile + rr * ZEST_TILE_K + q * 16) = m;
-    *reinterpret_cast<uint16_t *>(tile + ZEST_TILE_MANT + rr * 8 + q * 2) = (uint16_t) (e0 | (e1 << 8));
 }
 
 // One thread per 16-value unit of a packed operand: its mantissas and two
@@ -123,61 +155,75 @@ __global__ __launch_bounds__(256) void convert_q8_0_kernel(const uint8_t * __res
     *reinterpret_cast<uint32_t *>(tile + ZEST_TILE_MANT + rr * 8 + half * 4) = ex;
 }
 
+// Encodes 64 consecutive values of one row (a tile row: 8 blocks) and stores
+// them at row dr of tile column kc: 64 mantissa bytes (four 16-byte stores)
+// and the 8 exponent bytes (one 8-byte store).
+__device__ inline void store_tile_row(uint8_t * dst, int64_t R_pad, int64_t dr, int64_t kc, const float v[64]) {
+    uint4 m[4];
+    uint32_t e[8];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        e[2 * u] = encode8(v + 16 * u, m[u].x, m[u].y);
+        e[2 * u + 1] = encode8(v + 16 * u + 8, m[u].z, m[u].w);
+    }
+    uint8_t * tile = dst + zest_tile_offset(dr / ZEST_TILE_ROWS, kc, R_pad);
+    const int64_t rr = dr % ZEST_TILE_ROWS;
+    uint4 * mp = reinterpret_cast<uint4 *>(tile + rr * ZEST_TILE_K);
+#pragma unroll
+    for (int u = 0; u < 4; u++) mp[u] = m[u];
+    *reinterpret_cast<uint2 *>(tile + ZEST_TILE_MANT + rr * 8) =
+        make_uint2(e[0] | (e[1] << 8) | (e[2] << 16) | (e[3] << 24), e[4] | (e[5] << 8) | (e[6] << 16) | (e[7] << 24));
+}
+
 // Q4_K: 144-byte super-blocks of 256: fp16 d, fp16 dmin, 12 bytes of 6-bit
 // (scale, min) pairs, 128 bytes of nibbles. Sub-block s (0..7) is 32 values:
 // the low (s even) or high (s odd) nibbles of qs[32*(s/2) ..+32), with pair s:
 // y = (d*sc)*q - dmin*m. The products are exact in fp32, so the one rounding
-// is the subtraction's and fma gives the same float. One thread per
-// sub-block; workgroup 8 rows x 32 sub-blocks (4 super-blocks).
+// is the subtraction's and fma gives the same float. One thread per quarter
+// super-block: sub-blocks 2p and 2p+1, the two nibbles of the same 32 bytes,
+// i.e. 64 consecutive values, one tile row. Three aligned 16-byte loads (the
+// 16-byte header; the 32 nibble bytes). Workgroup: 16 rows x 4 super-blocks.
 __global__ __launch_bounds__(256) void convert_q4_k_kernel(const uint8_t * __restrict__ raw, int64_t N, int64_t K,
                                                            uint8_t * __restrict__ dst, int64_t R_pad, int64_t K_pad,
                                                            int64_t R_src, int gu) {
-    const int t = threadIdx.x;
-    const int64_t r = (int64_t) blockIdx.y * 8 + (t >> 5);
-    const int64_t sb = (int64_t) blockIdx.x * 32 + (t & 31);  // 32-column sub-block
-    const int64_t col = sb * 32;
+    const int t = threadIdx.x, p = t & 3;
+    const int64_t r = (int64_t) blockIdx.y * ZEST_TILE_ROWS + (t >> 4);
+    const int64_t sb = (int64_t) blockIdx.x * 4 + ((t >> 2) & 3);
+    const int64_t col = sb * 256 + p * 64;
     if (col >= K_pad || r >= R_src) return;
-    uint4 m0 = make_uint4(0, 0, 0, 0), m1 = make_uint4(0, 0, 0, 0);
-    uint32_t ex = 0;
+    float v[64];
     if (r < N && col < K) {
-        const uint8_t * blk = raw + r * (K / 256 * 144) + (sb / 8) * 144;
-        const int s = (int) (sb & 7);
-        const uint32_t dd = *reinterpret_cast<const uint32_t *>(blk);
-        const float d = half_to_float((uint16_t) (dd & 0xffff)), dmin = half_to_float((uint16_t) (dd >> 16));
-        const uint8_t * sc = blk + 4;
-        uint32_t scv, mv;
-        if (s < 4) {
-            scv = sc[s] & 63;
-            mv = sc[s + 4] & 63;
-        } else {
-            scv = (sc[s + 4] & 0xF) | ((sc[s - 4] >> 6) << 4);
-            mv = (sc[s + 4] >> 4) | ((sc[s] >> 6) << 4);
-        }
-        const float d1 = d * (float) scv, m1f = dmin * (float) mv;
-        const uint4 * qp = reinterpret_cast<const uint4 *>(blk + 16 + 32 * (s >> 1));
-        const uint4 qa = qp[0], qb = qp[1];
+        const uint8_t * blk = raw + r * (K / 256 * 144) + sb * 144;
+        const uint4 hdr = *reinterpret_cast<const uint4 *>(blk);
+        const uint4 qa = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * p);
+        const uint4 qb = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * p);
+        const float d = half_to_float((uint16_t) (hdr.x & 0xffff)), dmin = half_to_float((uint16_t) (hdr.x >> 16));
+        const uint32_t scw[3] = {hdr.y, hdr.z, hdr.w};
+        auto sc = [&](int i) { return (scw[i >> 2] >> ((i & 3) * 8)) & 0xffu; };
         const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-        const int shift = (s & 1) * 4;
-        float v[32];
 #pragma unroll
-        for (int i = 0; i < 32; i++) {
-            const uint32_t nib = (w[i >> 2] >> ((i & 3) * 8 + shift)) & 0xF;
-            v[i] = fmaf(d1, (float) nib, -m1f);
+        for (int h = 0; h < 2; h++) {
+            const int s = 2 * p + h;
+            uint32_t scv, mv;
+            if (s < 4) {
+                scv = sc(s) & 63;
+                mv = sc(s + 4) & 63;
+            } else {
+                scv = (sc(s + 4) & 0xF) | ((sc(s - 4) >> 6) << 4);
+                mv = (sc(s + 4) >> 4) | ((sc(s) >> 6) << 4);
+            }
+            const float d1 = d * (float) scv, m1f = dmin * (float) mv;
+#pragma unroll
+            for (int i = 0; i < 32; i++) {
+                const uint32_t nib = (w[i >> 2] >> ((i & 3) * 8 + h * 4)) & 0xF;
+                v[32 * h + i] = fmaf(d1, (float) nib, -m1f);
+            }
         }
-        uint32_t e[4];
-        e[0] = encode8(v, m0.x, m0.y);
-        e[1] = encode8(v + 8, m0.z, m0.w);
-        e[2] = encode8(v + 16, m1.x, m1.y);
-        e[3] = encode8(v + 24, m1.z, m1.w);
-        ex = e[0] | (e[1] << 8) | (e[2] << 16) | (e[3] << 24);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 64; i++) v[i] = 0.0f;
     }
-    const int64_t dr = dst_row(r, gu);
-    uint8_t * tile = dst + zest_tile_offset(dr / ZEST_TILE_ROWS, col / ZEST_TILE_K, R_pad);
-    const int64_t rr = dr % ZEST_TILE_ROWS, half = (col % ZEST_TILE_K) / 32;
-    uint4 * mp = reinterpret_cast<uint4 *>(tile + rr * ZEST_TILE_K + half * 32);
-    mp[0] = m0;
-    mp[1] = m1;
-    *reinterpret_cast<uint32_t *>(tile + ZEST_TILE_MANT + rr * 8 + half * 4) = ex;
+    store_tile_row(dst, R_pad, dst_row(r, gu), col / ZEST_TILE_K, v);
 }
 
 bool aligned(const void * p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
@@ -264,7 +310,7 @@ static int convert(int type, const void * raw, int64_t N, int64_t K, void * dst,
         case ZEST_TYPE_Q4_K: {
             ZEST_REQUIRE(K % 256 == 0, "%s: Q4_K needs K %% 256 == 0 (K=%lld)", name, (long long) K);
             ZEST_REQUIRE(aligned(raw, 16), "%s: Q4_K rows must be 16-byte aligned", name);
-            const dim3 grid((unsigned) ((K_pad / 32 + 31) / 32), (unsigned) (R_src / 8));
+            const dim3 grid((unsigned) ((K_pad / 256 + 3) / 4), (unsigned) (R_src / ZEST_TILE_ROWS));
             hipLaunchKernelGGL(convert_q4_k_kernel, grid, dim3(256), 0, s, (const uint8_t *) raw, N, K, (uint8_t *) dst,
                                R_pad, K_pad, R_src, gu);
             return zest::check_launch(name);
