@@ -45,71 +45,128 @@ __device__ inline void store16(float * p, const float v[16], int64_t valid) {
     }
 }
 
-constexpr int NORM_THREADS = 256;
-constexpr int NORM_UNITS = 4;  // 16-column units per thread: rows up to 16384 wide
+constexpr int NORM_ROWS = 4;  // rows per workgroup, one wave each
 
-// One workgroup per row: sum of squares (fp32), sc = 1/sqrt(ss/d + eps),
-// y = x * sc (* w). Units of 16 columns stay in registers between the two
-// passes. Writes y and/or the packed row, including the zero blocks of the
-// K padding when d % 64 != 0.
-__global__ __launch_bounds__(NORM_THREADS) void rms_norm_kernel(const float * __restrict__ x, int64_t d, float eps,
-                                                                const float * __restrict__ w, float * __restrict__ y,
-                                                                uint8_t * __restrict__ packed, int64_t R_pad) {
-    const int64_t r = blockIdx.x;
-    const float * xr = x + r * d;
-    const int64_t units = (d + 15) / 16, d_pad = zest_k_padded(d);
-    float v[NORM_UNITS][16];
-    float ss = 0.0f;
+// Writes 4 values of row r at columns [c, c+4) (c % 4 == 0) of the next
+// matmul's input, the bfp16 pack stored expanded: the 8-column block is this
+// lane's 4 and its neighbour's (lane ^ 1), whose largest exponent field one
+// lane exchange finds; the 4 values are encoded as encode8 does and stored as
+// the bf16 they stand for (8 bytes). Both lanes of a pair must call it.
+__device__ inline void pack4_expanded(uint8_t * packed, int64_t R_pad, int64_t r, int64_t c, const float v[4]) {
+    uint32_t e = 0;
 #pragma unroll
-    for (int k = 0; k < NORM_UNITS; k++) {
-        const int64_t u = threadIdx.x + (int64_t) k * NORM_THREADS;
-        if (u < units) {
-            load16(xr + u * 16, v[k], d - u * 16);
+    for (int q = 0; q < 4; q++) e = max(e, (__float_as_uint(v[q]) >> 23) & 0xffu);
+    e = max(e, (uint32_t) __shfl_xor((int) e, 1));
+    const int sh = 133 - (int) e;
+    const float sc = zest::block_scale(e);
+    uint32_t b[4];
 #pragma unroll
-            for (int i = 0; i < 16; i++) ss += v[k][i] * v[k][i];
-        }
+    for (int q = 0; q < 4; q++) {
+        const int32_t qi =
+            (int32_t) __builtin_amdgcn_fmed3f(__builtin_rintf(__builtin_ldexpf(v[q], sh)), -128.0f, 127.0f);
+        b[q] = __float_as_uint((float) qi * sc) >> 16;  // exact: at most 8 significant bits
     }
-    __shared__ float part[NORM_THREADS / 64];
+    *reinterpret_cast<uint2 *>(packed + zest_xtile_offset(r / ZEST_TILE_ROWS, c / ZEST_TILE_K, R_pad) +
+                               (r % ZEST_TILE_ROWS) * 128 + (c % ZEST_TILE_K) * 2) =
+        make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
+}
+
+// Zeroes row r of an expanded operand (d_pad columns): a padding row past the
+// last real row, which the GEMM reads as zero.
+__device__ inline void zero_row_expanded(uint8_t * packed, int64_t R_pad, int64_t r, int64_t d_pad, int lane) {
+    for (int64_t c = lane * 4; c < d_pad; c += 256)
+        *reinterpret_cast<uint2 *>(packed + zest_xtile_offset(r / ZEST_TILE_ROWS, c / ZEST_TILE_K, R_pad) +
+                                   (r % ZEST_TILE_ROWS) * 128 + (c % ZEST_TILE_K) * 2) = make_uint2(0, 0);
+}
+
+// One wave per row: sum of squares (fp32), sc = 1/sqrt(ss/d + eps),
+// y = x * sc (* w). Lane l takes the 4 floats at columns 4l + 256i, so a
+// wave's load covers 1 KB of the row; the sum is a wave reduction, no LDS.
+// The second pass re-reads the row (from L2) and writes y and/or the packed
+// row, including the zero blocks of the K padding when d % 64 != 0; waves
+// past the last row zero the packed operand's padding rows.
+__global__ __launch_bounds__(NORM_ROWS * 64) void rms_norm_kernel(const float * __restrict__ x, int64_t rows,
+                                                                  int64_t d, float eps, const float * __restrict__ w,
+                                                                  float * __restrict__ y, uint8_t * __restrict__ packed,
+                                                                  int64_t R_pad) {
+    const int lane = threadIdx.x & 63;
+    const int64_t r = (int64_t) blockIdx.x * NORM_ROWS + (threadIdx.x >> 6);
+    const int64_t d_pad = zest_k_padded(d);
+    if (r >= rows) {
+        if (packed && r < R_pad) zero_row_expanded(packed, R_pad, r, d_pad, lane);
+        return;
+    }
+    const float * xr = x + r * d;
+    const bool vec = (d & 3) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+    auto load4 = [&](const float * p, int64_t c, float v[4]) {
+        if (vec && c + 4 <= d) {
+            const float4 q = *reinterpret_cast<const float4 *>(p + c);
+            v[0] = q.x;
+            v[1] = q.y;
+            v[2] = q.z;
+            v[3] = q.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = c + i < d ? p[c + i] : 0.0f;
+        }
+    };
+    float ss = 0.0f;
+    for (int64_t c = lane * 4; c < d; c += 256) {
+        float v[4];
+        load4(xr, c, v);
+#pragma unroll
+        for (int i = 0; i < 4; i++) ss += v[i] * v[i];
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    float tot = 0.0f;
+    const float sc = 1.0f / sqrtf(ss / (float) d + eps);
+    const bool wvec = w && vec && (reinterpret_cast<uintptr_t>(w) & 15) == 0;
+    for (int64_t c = lane * 4; c < (packed ? d_pad : d); c += 256) {
+        float o[4];
+        load4(xr, c, o);
 #pragma unroll
-    for (int i = 0; i < NORM_THREADS / 64; i++) tot += part[i];
-    const float sc = 1.0f / sqrtf(tot / (float) d + eps);
+        for (int i = 0; i < 4; i++) o[i] *= sc;
+        if (w) {
+            float wv[4];
+            if (wvec && c + 4 <= d) {
+                const float4 q = *reinterpret_cast<const float4 *>(w + c);
+                wv[0] = q.x;
+                wv[1] = q.y;
+                wv[2] = q.z;
+                wv[3] = q.w;
+            } else {
 #pragma unroll
-    for (int k = 0; k < NORM_UNITS; k++) {
-        const int64_t u = threadIdx.x + (int64_t) k * NORM_THREADS;
-        if (u < units) {
-            float o[16];
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int64_t j = u * 16 + i;
-                o[i] = j < d ? v[k][i] * sc : 0.0f;
-                if (w && j < d) o[i] *= w[j];
+                for (int i = 0; i < 4; i++) wv[i] = c + i < d ? w[c + i] : 0.0f;
             }
-            if (y) store16(y + r * d + u * 16, o, d - u * 16);
-            if (packed) pack16(packed, R_pad, r, u * 16, o);
-        } else if (packed && u * 16 < d_pad) {
-            float z[16] = {};
-            pack16(packed, R_pad, r, u * 16, z);
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[i] *= wv[i];
         }
+        if (y && c < d) {
+            float * yr = y + r * d;
+            if (vec && c + 4 <= d) {
+                *reinterpret_cast<float4 *>(yr + c) = make_float4(o[0], o[1], o[2], o[3]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (c + i < d) yr[c + i] = o[i];
+            }
+        }
+        if (packed) pack4_expanded(packed, R_pad, r, c, o);
     }
 }
 
-
 // One thread per 16 outputs of one row: y = act(g) * u (REGLU as g > 0 ? g*u : 0).
+// With a packed output the grid also covers its padding rows, written as zeros.
 template <int KIND>
 __global__ __launch_bounds__(256) void glu_kernel(const float * __restrict__ g, int64_t sg, const float * __restrict__ u,
                                                   int64_t su, int64_t rows, int64_t f, float * __restrict__ y,
-                                                  uint8_t * __restrict__ packed, int64_t R_pad) {
+                                                  uint8_t * __restrict__ packed, int64_t R_pad, int64_t grid_rows) {
     const int64_t units = zest_k_padded(f) / 16;
     const int64_t idx = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= rows * units) return;
+    if (idx >= grid_rows * units) return;
     const int64_t r = idx / units, c = (idx % units) * 16;
     float o[16];
-    if (c < f) {
+    if (r < rows && c < f) {
         float gv[16], uv[16];
         load16(g + r * sg + c, gv, f - c);
         load16(u + r * su + c, uv, f - c);
@@ -201,11 +258,12 @@ int zest_rms_norm(const float * x, int64_t rows, int64_t d, float eps, const flo
                   void * stream) {
     ZEST_REQUIRE(x && (y || packed), "zest_rms_norm: null pointer");
     ZEST_REQUIRE(rows > 0 && d > 0, "zest_rms_norm: rows=%lld d=%lld", (long long) rows, (long long) d);
-    ZEST_REQUIRE((d + 15) / 16 <= (int64_t) NORM_UNITS * NORM_THREADS, "zest_rms_norm: rows of %lld are too wide",
-                 (long long) d);
     ZEST_REQUIRE(!packed || d % 8 == 0, "zest_rms_norm: packing needs d %% 8 == 0");
-    hipLaunchKernelGGL(rms_norm_kernel, dim3((unsigned) rows), dim3(NORM_THREADS), 0, zest::as_stream(stream), x, d,
-                       eps, w, y, (uint8_t *) packed, zest_rows_padded(rows));
+    // with a packed output, the grid also covers its padding rows (zeroed)
+    const int64_t R_pad = zest_rows_padded(rows), grid_rows = packed ? R_pad : rows;
+    hipLaunchKernelGGL(rms_norm_kernel, dim3((unsigned) ((grid_rows + NORM_ROWS - 1) / NORM_ROWS)),
+                       dim3(NORM_ROWS * 64), 0, zest::as_stream(stream), x, rows, d, eps, w, y, (uint8_t *) packed,
+                       R_pad);
     return zest::check_launch("zest_rms_norm");
 }
 
@@ -214,17 +272,17 @@ int zest_glu(int kind, const float * g, int64_t sg, const float * u, int64_t su,
     ZEST_REQUIRE(g && u && (y || packed), "zest_glu: null pointer");
     ZEST_REQUIRE(rows > 0 && f > 0 && sg >= f && su >= f, "zest_glu: bad shape");
     ZEST_REQUIRE(!packed || f % 8 == 0, "zest_glu: packing needs f %% 8 == 0");
-    const int64_t n = rows * (zest_k_padded(f) / 16);
+    const int64_t R_pad = zest_rows_padded(rows), gr = packed ? R_pad : rows;
+    const int64_t n = gr * (zest_k_padded(f) / 16);
     const dim3 grid(blocks_for(n, 256));
     hipStream_t s = zest::as_stream(stream);
-    const int64_t R_pad = zest_rows_padded(rows);
     uint8_t * p = (uint8_t *) packed;
     switch (kind) {
-        case ZEST_GLU_SWIGLU: hipLaunchKernelGGL(glu_kernel<ZEST_GLU_SWIGLU>, grid, dim3(256), 0, s, g, sg, u, su, rows, f, y, p, R_pad); break;
-        case ZEST_GLU_GEGLU: hipLaunchKernelGGL(glu_kernel<ZEST_GLU_GEGLU>, grid, dim3(256), 0, s, g, sg, u, su, rows, f, y, p, R_pad); break;
-        case ZEST_GLU_GEGLU_ERF: hipLaunchKernelGGL(glu_kernel<ZEST_GLU_GEGLU_ERF>, grid, dim3(256), 0, s, g, sg, u, su, rows, f, y, p, R_pad); break;
-        case ZEST_GLU_GEGLU_QUICK: hipLaunchKernelGGL(glu_kernel<ZEST_GLU_GEGLU_QUICK>, grid, dim3(256), 0, s, g, sg, u, su, rows, f, y, p, R_pad); break;
-        case ZEST_GLU_REGLU: hipLaunchKernelGGL(glu_kernel<ZEST_GLU_REGLU>, grid, dim3(256), 0, s, g, sg, u, su, rows, f, y, p, R_pad); break;
+        case ZEST_GLU_SWIGLU: hipLaunchKernelGGL(glu_kernel<ZEST_GLU_SWIGLU>, grid, dim3(256), 0, s, g, sg, u, su, rows, f, y, p, R_pad, gr); break;
+        case ZEST_GLU_GEGLU: hipLaunchKernelGGL(glu_kernel<ZEST_GLU_GEGLU>, grid, dim3(256), 0, s, g, sg, u, su, rows, f, y, p, R_pad, gr); break;
+        case ZEST_GLU_GEGLU_ERF: hipLaunchKernelGGL(glu_kernel<ZEST_GLU_GEGLU_ERF>, grid, dim3(256), 0, s, g, sg, u, su, rows, f, y, p, R_pad, gr); break;
+        case ZEST_GLU_GEGLU_QUICK: hipLaunchKernelGGL(glu_kernel<ZEST_GLU_GEGLU_QUICK>, grid, dim3(256), 0, s, g, sg, u, su, rows, f, y, p, R_pad, gr); break;
+        case ZEST_GLU_REGLU: hipLaunchKernelGGL(glu_kernel<ZEST_GLU_REGLU>, grid, dim3(256), 0, s, g, sg, u, su, rows, f, y, p, R_pad, gr); break;
         default: return zest::fail(ZEST_E_UNSUPPORTED, "zest_glu: GLU kind %d", kind);
     }
     return zest::check_launch("zest_glu");

@@ -91,7 +91,9 @@ ZEST_API int zest_expand_act(const void *src, int64_t M, int64_t K, void *dst, v
 ZEST_API int zest_convert_weight(int type, const void *raw, int64_t N, int64_t K, void *dst, void *stream);
 
 /* c[M][N] (row stride ldc floats) = A . W^T, a the expanded activation
- * operand (M rows, zest_pack_act_x) and w a packed bfp16 weight (N rows), K
+ * operand (M rows, as zest_pack_act_x, the fused norm and GLU packs and
+ * zest_gemm_glu write it: its padding rows and columns zero, so they add
+ * nothing) and w a packed bfp16 weight (N rows), K
  * columns each: the weight's bfp16 tiles expanded to bf16 in LDS, bf16 MFMA,
  * fp32 accumulation, fp32 store. If `nonfinite` (a device word) is non-NULL,
  * it is OR-ed with 1 when any stored value is NaN or infinite. Replaces

@@ -98,3 +98,35 @@ def test_rope(zest_gpu, oracle, n_dims, mode, n_ctx, fs, ext, factors):
     got = zest_gpu.rope(_dev(x), _dev(pos), None if ff is None else _dev(ff), n_dims, mode, 10000.0, fs, ext, 1.0,
                         corr)
     assert nrmse(_host(got), want) <= EXACT
+
+
+def _padding_is_zero(z, buf, rows, d):
+    """The expanded operand's rows past `rows` and columns past d are zero."""
+    full = z.expanded_to_rows(buf, z.rows_pad(rows), z.k_pad(d))
+    return not full[rows:].any() and not full[:, d:].any()
+
+
+@pytest.mark.parametrize("rows,d", [(5, 200), (300, 2560)])
+def test_fused_packs_zero_their_padding(zest_gpu, oracle, rows, d):
+    # the GEMM reads the operand up to its padded row count: the norm and GLU
+    # packs write those rows (and the K padding) as zeros, whatever the
+    # buffer held before
+    import torch
+    x = Rng(rows * 3 + d).normal(rows * d, 0, 1.5).reshape(rows, d)
+    packed = zest_gpu.empty_act(rows, d)
+    packed.fill_(0xFF)
+    y = zest_gpu.rms_norm(_dev(x), 1e-6, packed=packed)
+    host = _host(packed)
+    assert _padding_is_zero(zest_gpu, host, rows, d)
+    got = _host(y)
+    assert np.array_equal(zest_gpu.expanded_to_rows(host, rows, d).view(np.uint32),
+                          oracle.decode_rows(oracle.encode_rows(got)).view(np.uint32))
+    g = Rng(rows + 1).normal(rows * d, 0, 1.5).reshape(rows, d)
+    u = Rng(rows + 2).normal(rows * d, 0, 1.5).reshape(rows, d)
+    packed.fill_(0xFF)
+    h = zest_gpu.glu(2, _dev(g), _dev(u), d, packed=packed)
+    host = _host(packed)
+    assert _padding_is_zero(zest_gpu, host, rows, d)
+    assert np.array_equal(zest_gpu.expanded_to_rows(host, rows, d).view(np.uint32),
+                          oracle.decode_rows(oracle.encode_rows(_host(h))).view(np.uint32))
+    del torch
