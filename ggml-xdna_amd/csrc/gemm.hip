@@ -62,7 +62,6 @@ struct gemm_cfg {
     static constexpr int STAGES = 3;
     static constexpr size_t LDS_BYTES = (size_t) STAGES * STAGE;
     static constexpr int A_STEP = NP * 16;                     // bytes between a thread's A chunks
-    static constexpr int W_STEP = NP / 64 * ZEST_TILE_BYTES;  // bytes between a thread's W units
     static_assert(BM * 8 % NP == 0 && BN * 4 % NP == 0, "work must divide evenly");
     static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be whole 32x32 MFMA tiles");
 };
@@ -100,7 +99,7 @@ __device__ inline uint4 load16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
 template <class C>
 struct stage_regs {
     uint4 wm[C::BU];
-    uint32_t we[C::BU];
+    uint32_t we;  // both units' exponent bytes: unit 0 in bits 0-15, unit 1 in bits 16-31
 };
 
 typedef __attribute__((address_space(3))) void * lds_ptr_t;
@@ -126,18 +125,22 @@ __device__ inline void wait_vm_lgkm0() {
 //      8j..8j+7, lane l writing the 16 bytes at 16*l, i.e. row 8j + l/8,
 //      position l%8. The swizzle is applied on the source side: lane l reads
 //      the chunk that belongs at that position, (l%8) ^ swz(row).
-//   W: unit p + i*NP of the W slab is tile (p + i*NP)/64, and in it lane
-//      l = p%64 takes row l%16, column quarter l/16%4 (16 consecutive lanes
-//      = 16 consecutive rows, for the swizzled stores), through registers:
-//      loaded a step ahead, expanded, stored.
+//   W: thread p takes two adjacent units of tile p/32 of the W slab: row
+//      p%16, column quarters 2h and 2h+1 with h = p/16%2, i.e. 32 contiguous
+//      mantissa bytes (two 16-byte loads) and 4 contiguous exponent bytes
+//      (one 4-byte load: the address unit costs the same per instruction
+//      whatever its width). 16 consecutive lanes are 16 consecutive rows,
+//      for the swizzled stores. Loaded a step ahead, expanded, stored.
 template <class C>
 struct producer {
     static constexpr int NPW = C::NP / 64;          // producer waves
     static constexpr int AI = C::BM / 8 / NPW;      // A instructions per producer wave per K-step
+    static constexpr int WI = 3;                    // W load instructions per K-step (load_w)
+    static_assert(C::BU == 2 && C::NP / 32 == C::BN / 16, "two W units per producer thread, 32 threads a tile");
     __amdgpu_buffer_rsrc_t ra, rw;
     int pw;                // producer wave
     int va, vwm, vwe;      // lane offsets: A chunk, W mantissas, W exponents
-    int stw0, stw1;        // LDS offsets of the first W unit's two chunks
+    int stw[2][2];         // LDS offsets of the two W units' two chunks each
 
     __device__ producer(const uint8_t * A, int64_t a_bytes, const uint8_t * W, int64_t w_bytes, int p) {
         ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(A), (short) 0, (int) a_bytes, 0x00020000);
@@ -147,12 +150,15 @@ struct producer {
         // instruction j = i*NPW + pw: j and pw have the same parity, so
         // swz(8j + l/8) is the same for every i
         va = pw * 1024 + (l >> 3) * 128 + ((l & 7) ^ swz(8 * (pw & 1) + (l >> 3))) * 16;
-        const int u = (l & 15) * 4 + ((l >> 4) & 3);
-        vwm = (p >> 6) * ZEST_TILE_BYTES + u * 16;
-        vwe = (p >> 6) * ZEST_TILE_BYTES + ZEST_TILE_MANT + u * 2;
-        const int wrow = (p >> 6) * 16 + (l & 15), q = (l >> 4) & 3, sw = swz(wrow);
-        stw0 = C::A_BYTES + wrow * C::ROWB + ((2 * q) ^ sw) * 16;
-        stw1 = C::A_BYTES + wrow * C::ROWB + ((2 * q + 1) ^ sw) * 16;
+        const int t = p >> 5, row = p & 15, h = (p >> 4) & 1;
+        vwm = t * ZEST_TILE_BYTES + row * ZEST_TILE_K + h * 32;
+        vwe = t * ZEST_TILE_BYTES + ZEST_TILE_MANT + row * 8 + h * 4;
+        const int wrow = t * 16 + row, sw = swz(wrow);
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            stw[i][0] = C::A_BYTES + wrow * C::ROWB + ((4 * h + 2 * i) ^ sw) * 16;
+            stw[i][1] = C::A_BYTES + wrow * C::ROWB + ((4 * h + 2 * i + 1) ^ sw) * 16;
+        }
     }
 
     // The A slab at byte a_off into the stage at byte `stage` of LDS:
@@ -165,21 +171,18 @@ struct producer {
     }
 
     __device__ void load_w(stage_regs<C> & st, int w_off) const {
-#pragma unroll
-        for (int i = 0; i < C::BU; i++) {
-            st.wm[i] = load16(rw, vwm, w_off + i * C::W_STEP);
-            st.we[i] = __builtin_amdgcn_raw_buffer_load_b16(rw, vwe, w_off + i * C::W_STEP, 0);
-        }
+        st.wm[0] = load16(rw, vwm, w_off);
+        st.wm[1] = load16(rw, vwm + 16, w_off);
+        st.we = __builtin_amdgcn_raw_buffer_load_b32(rw, vwe, w_off, 0);
     }
 
     // W unit i of a step, by the branch-free fast expansion, stored; true if
     // the unit needs the general expansion (store_w_general) instead.
     __device__ bool store_w_unit(const stage_regs<C> & st, int i, uint8_t * smem, int stage) const {
         uint32_t b[8];
-        const bool slow = zest::expand16_fast(st.wm[i], st.we[i], b);
-        const int off = stage + i * (C::NP / 4) * C::ROWB;
-        lds_put_async(smem, stw0 + off, make_uint4(b[0], b[1], b[2], b[3]));
-        lds_put_async(smem, stw1 + off, make_uint4(b[4], b[5], b[6], b[7]));
+        const bool slow = zest::expand16_fast(st.wm[i], i ? st.we >> 16 : st.we & 0xffffu, b);
+        lds_put_async(smem, stw[i][0] + stage, make_uint4(b[0], b[1], b[2], b[3]));
+        lds_put_async(smem, stw[i][1] + stage, make_uint4(b[4], b[5], b[6], b[7]));
         return slow;
     }
 
@@ -188,10 +191,9 @@ struct producer {
 #pragma unroll
         for (int i = 0; i < C::BU; i++) {
             uint32_t b[8];
-            zest::expand16(st.wm[i], st.we[i], b);
-            const int off = stage + i * (C::NP / 4) * C::ROWB;
-            lds_put_async(smem, stw0 + off, make_uint4(b[0], b[1], b[2], b[3]));
-            lds_put_async(smem, stw1 + off, make_uint4(b[4], b[5], b[6], b[7]));
+            zest::expand16(st.wm[i], i ? st.we >> 16 : st.we & 0xffffu, b);
+            lds_put_async(smem, stw[i][0] + stage, make_uint4(b[0], b[1], b[2], b[3]));
+            lds_put_async(smem, stw[i][1] + stage, make_uint4(b[4], b[5], b[6], b[7]));
         }
     }
 
@@ -202,23 +204,8 @@ struct producer {
     __device__ void store_w(const stage_regs<C> & st, uint8_t * smem, int stage) const {
         bool slow = false;
 #pragma unroll
-        for (int i = 0; i < C::BU; i++) {
-            uint32_t b[8];
-            slow |= zest::expand16_fast(st.wm[i], st.we[i], b);
-            const int off = stage + i * (C::NP / 4) * C::ROWB;
-            lds_put_async(smem, stw0 + off, make_uint4(b[0], b[1], b[2], b[3]));
-            lds_put_async(smem, stw1 + off, make_uint4(b[4], b[5], b[6], b[7]));
-        }
-        if (__builtin_expect(__any(slow), 0)) {
-#pragma unroll
-            for (int i = 0; i < C::BU; i++) {
-                uint32_t b[8];
-                zest::expand16(st.wm[i], st.we[i], b);
-                const int off = stage + i * (C::NP / 4) * C::ROWB;
-                lds_put_async(smem, stw0 + off, make_uint4(b[0], b[1], b[2], b[3]));
-                lds_put_async(smem, stw1 + off, make_uint4(b[4], b[5], b[6], b[7]));
-            }
-        }
+        for (int i = 0; i < C::BU; i++) slow |= store_w_unit(st, i, smem, stage);
+        if (__builtin_expect(__any(slow), 0)) store_w_general(st, smem, stage);
     }
 };
 
@@ -537,7 +524,7 @@ __device__ inline void steady_step(const producer<C> & pr, uint8_t * smem, int s
 template <class C>
 __device__ inline void produce(const producer<C> & pr, uint8_t * smem, int a0, int w0, int a_kstride, int w_kstride,
                                int ns) {
-    constexpr int AI = producer<C>::AI, WI = 2 * C::BU;  // VMEM instructions per step: A DMA, W loads
+    constexpr int AI = producer<C>::AI, WI = producer<C>::WI;  // VMEM instructions per step: A DMA, W loads
     constexpr int FLY = ZEST_GEMM_XSTEP ? WI : AI + WI;
     stage_regs<C> s0, s1;
     pr.dma_a(smem, 0, a0);
