@@ -50,6 +50,7 @@ SIGNATURES = {
     "zest_expand_act": (_c_i, [_c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "zest_convert_weight": (_c_i, [_c_i, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "zest_gemm": (_c_i, [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p]),
+    "zest_gemm_residual": (_c_i, [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p]),
     "zest_gemm_group": (_c_i, [_c_p, _c_i64, _c_i64, _c_i, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p]),
     "zest_convert_weight_gu": (_c_i, [_c_i, _c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "zest_gemm_glu": (_c_i, [_c_i, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_p]),
@@ -215,6 +216,15 @@ def gemm(a_packed, m: int, w_packed, n: int, k: int, out=None, nonfinite=None):
     out = torch.empty((m, n), dtype=torch.float32, device=a_packed.device) if out is None else out
     check(lib().zest_gemm(_ptr(a_packed), m, _ptr(w_packed), n, k, _ptr(out), out.stride(0), _ptr(nonfinite),
                           _stream()), "zest_gemm")
+    return out
+
+
+def gemm_residual(a_packed, m: int, w_packed, n: int, k: int, res, out=None, nonfinite=None):
+    """c[m][n] = A . W^T + res (res may be out itself: an in-place residual add)."""
+    torch = _torch()
+    out = torch.empty((m, n), dtype=torch.float32, device=a_packed.device) if out is None else out
+    check(lib().zest_gemm_residual(_ptr(a_packed), m, _ptr(w_packed), n, k, _ptr(res), res.stride(0), _ptr(out),
+                                   out.stride(0), _ptr(nonfinite), _stream()), "zest_gemm_residual")
     return out
 
 

@@ -444,6 +444,34 @@ std::vector<fusion> find_fusions(const std::vector<ggml_tensor *> & nodes,
     return out;
 }
 
+// Residual adds: an ADD of a matmul's result and a same-shape F32 tensor whose
+// rows are 16-byte aligned, the matmul read by nothing else, inside the piece
+// or out, runs as one GEMM with the add in its store (zest_gemm_residual).
+// Returns ADD -> its matmul.
+std::unordered_map<const ggml_tensor *, const ggml_tensor *> find_residuals(
+    const std::vector<ggml_tensor *> & nodes, const std::unordered_set<const ggml_tensor *> & in_piece,
+    const std::unordered_set<const ggml_tensor *> & fused) {
+    std::unordered_map<const ggml_tensor *, const ggml_tensor *> out;
+    for (ggml_tensor * a : nodes) {
+        if (a->op != GGML_OP_ADD || !is_contiguous(a) || a->type != GGML_TYPE_F32) continue;
+        for (int side = 0; side < 2; side++) {
+            const ggml_tensor * n = a->src[side], * r = a->src[1 - side];
+            if (!n || !r || !gemm_matmul(n) || fused.count(n) || !in_piece.count(n) || read_outside(n, in_piece) ||
+                !same_shape(a, n) || !same_shape(a, r) || r->type != GGML_TYPE_F32 || r->nb[0] != 4 ||
+                r->nb[1] % 16 != 0 || nrows(a) != a->ne[1])
+                continue;
+            bool other = false;  // another reader of the matmul's result
+            for (const ggml_tensor * m : nodes)
+                for (int j = 0; j < GGML_MAX_SRC && m != a; j++)
+                    if (m->src[j] && owner(m->src[j]) == n) other = true;
+            if (other) continue;
+            out[a] = n;
+            break;
+        }
+    }
+    return out;
+}
+
 struct piece {
     context & ctx;
     const ggml_cgraph * g;
@@ -462,6 +490,9 @@ struct piece {
     int launches = 0, fused_launches = 0, grouped_launches = 0;  // GEMM launches of the piece
     std::unordered_map<const ggml_tensor *, const fusion *> fused_mm;   // gate/up matmul -> its fusion
     std::unordered_map<const ggml_tensor *, const fusion *> fused_glu;  // GLU -> its fusion
+    std::unordered_map<const ggml_tensor *, const ggml_tensor *> res_add;  // ADD -> its matmul
+    std::unordered_set<const ggml_tensor *> res_mm;                       // matmuls run by their ADD
+    int residual_launches = 0;
 
     piece(context & c, const ggml_cgraph * graph) : ctx(c), g(graph) {
         for (int i = 0; i < g->n_nodes; i++) {
@@ -469,11 +500,16 @@ struct piece {
             in_piece.insert(g->nodes[i]);
         }
         fusions = find_fusions(nodes, in_piece);
+        std::unordered_set<const ggml_tensor *> fused;
         for (const fusion & f : fusions) {
             fused_mm[f.gate_mm] = &f;
             if (f.up_mm) fused_mm[f.up_mm] = &f;
             fused_glu[f.glu] = &f;
+            fused.insert(f.gate_mm);
+            if (f.up_mm) fused.insert(f.up_mm);
         }
+        res_add = find_residuals(nodes, in_piece, fused);
+        for (const auto & kv : res_add) res_mm.insert(kv.second);
     }
 
     bool fail(const std::string & e) {
@@ -613,6 +649,34 @@ struct piece {
         return true;
     }
 
+    // A matmul and the ADD of its result, run where the ADD stands: one GEMM
+    // storing acc + the other operand into the ADD's output.
+    bool residual_gemm(ggml_tensor * a, const ggml_tensor * n) {
+        const ggml_tensor * r = a->src[0] == n ? a->src[1] : a->src[0];
+        const ggml_tensor * wt = n->src[0], * x = n->src[1];
+        const int64_t K = wt->ne[0], N = wt->ne[1], M = x->ne[1];
+        const void * ap = packed_input(x);
+        if (!ap) return false;
+        if (!ctx.ensure_weight(wt, ctx.stream, false, err)) return false;
+        const void * wp = ctx.weights.at(key_of(wt)).packed;
+        const float * rd = (const float *) in(r);
+        float * y = (float *) out(a);
+        if (!rd || !y) return fail("out of device memory for a residual add");
+        if ((reinterpret_cast<uintptr_t>(rd) & 15) != 0) return fail("a residual whose rows are not 16-byte aligned");
+        int64_t s = 0;
+        if (!injected_failure(s)) return false;
+        const int64_t ldc = (int64_t) (a->nb[1] / 4);
+        if (!check(zest_gemm_residual(ap, M, wp, N, K, rd, (int64_t) (r->nb[1] / 4), y, ldc, ctx.nonfinite,
+                                      ctx.stream),
+                   "gemm+add"))
+            return false;
+        if (!inject_nan(s, y, M, N, ldc)) return false;
+        ctx.matmuls++;
+        launches++;
+        residual_launches++;
+        return true;
+    }
+
     // A fused gate/up GEMM, run where its GLU stands: the GLU's fp32 rows
     // where something other than a matmul reads them, and its packed copy
     // where a matmul of the piece does.
@@ -708,7 +772,7 @@ struct piece {
             bool ok = true;
             switch (n->op) {
                 case GGML_OP_MUL_MAT: {
-                    if (fused_mm.count(n)) {
+                    if (fused_mm.count(n) || res_mm.count(n)) {
                         // runs with its GLU; its input is packed now, while it is sure to be intact
                         ok = packed_input(n->src[1]) != nullptr;
                         break;
@@ -719,7 +783,7 @@ struct piece {
                     for (size_t j = i + 1; j < nodes.size() && ms.size() < ZEST_GEMM_MAX_GROUP; j++) {
                         ggml_tensor * m = nodes[j];
                         if (is_noop(m)) continue;
-                        if (m->op != GGML_OP_MUL_MAT || fused_mm.count(m) ||
+                        if (m->op != GGML_OP_MUL_MAT || fused_mm.count(m) || res_mm.count(m) ||
                             packed_key(m->src[1]) != packed_key(n->src[1]))
                             break;
                         ms.push_back(m);
@@ -745,6 +809,10 @@ struct piece {
                     break;
                 }
                 case GGML_OP_ADD: {
+                    if (auto rm = res_add.find(n); rm != res_add.end()) {
+                        ok = residual_gemm(n, rm->second);
+                        break;
+                    }
                     const ggml_tensor * a = n->src[0], * b = n->src[1];
                     const void * ad = in(a), * bd = in(b);
                     float * y = (float *) out(n);
@@ -812,8 +880,8 @@ ggml_status graph_compute(ggml_backend_t backend, ggml_cgraph * cgraph) {
     ctx.pieces++;
     static const int64_t trace_level = env_int("GGML_XDNA_TRACE", 0);
     if (trace_level >= 2)
-        fprintf(stderr, "xdna piece: %d GEMM launches (%d fused gate/up, %d grouped)\n", p.launches, p.fused_launches,
-                p.grouped_launches);
+        fprintf(stderr, "xdna piece: %d GEMM launches (%d fused gate/up, %d grouped, %d with a residual add)\n",
+                p.launches, p.fused_launches, p.grouped_launches, p.residual_launches);
     if (trace() && ctx.matmuls >= 196) {
         fprintf(stderr, "xdna times, %lld matmuls in %lld pieces: all %.1f ms; weight copies %lld at load, %lld in pieces\n",
                 (long long) ctx.matmuls, (long long) ctx.pieces, ctx.compute_ms, (long long) ctx.built_at_load,

@@ -40,6 +40,9 @@
 
 namespace {
 
+// Epilogues other than the GLU kinds (which are >= 0)
+constexpr int EPI_PLAIN = -1, EPI_RESIDUAL = -2;
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -252,13 +255,35 @@ __device__ inline void consume(f32x16 (&acc)[C::TI][C::TJ], bf16x8 (&af)[2][C::T
 // dropped by the hardware range check on the vector offset (the whole byte
 // offset is kept there); columns past N are masked per lane. Also ORs 1 into
 // *nonfinite if any stored value is NaN or infinite.
-template <class C>
+// With `res` (RES), the consumer wave's WM x WN block of the residual comes
+// into the wave's own LDS region first (LDS DMA, every load in flight at
+// once: the ring is free after the K loop), and each output is acc + res
+// (res may be Cout itself: every element is read before it is written, by
+// the lane that writes it).
+template <class C, bool RES = false>
 __device__ inline void store_tile(const f32x16 (&acc)[C::TI][C::TJ], float * Cout, int64_t M, int64_t N, int64_t ldc,
-                                  int64_t m0, int64_t n0, int wm, int wn, int lane, uint32_t * nonfinite) {
+                                  int64_t m0, int64_t n0, int wm, int wn, int lane, uint32_t * nonfinite,
+                                  const float * res = nullptr, int64_t ldr = 0, uint8_t * smem = nullptr,
+                                  int wave = 0) {
     const __amdgpu_buffer_rsrc_t rc =
         __builtin_amdgcn_make_buffer_rsrc(Cout, (short) 0, (int) (M * ldc * 4), 0x00020000);
     const int khalf = lane >> 5;
     const int row0 = (int) m0 + wm * C::WM;
+    const float * rl = nullptr;  // the residual block in LDS: WM rows of WN floats
+    if constexpr (RES) {
+        static_assert(C::WN == 64, "a residual row segment is 16 lanes of 16 bytes");
+        uint8_t * region = smem + wave * (C::WM * C::WN * 4);
+        const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float *>(res), (short) 0, (int) (M * ldr * 4), 0x00020000);
+        // instruction q: rows 4q..4q+3 of the block, lane l taking row 4q + l/16, bytes 16(l%16)
+        const int voff = (int) ((row0 + (lane >> 4)) * ldr * 4 + (n0 + wn * C::WN) * 4 + (lane & 15) * 16);
+#pragma unroll
+        for (int q = 0; q < C::WM / 4; q++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_ptr_t) (region + q * 1024), 16, voff,
+                                                     (int) (4 * q * ldr * 4), 0, 0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        rl = reinterpret_cast<const float *>(region);
+    }
     bool bad = false;
 #pragma unroll
     for (int j = 0; j < C::TJ; j++) {
@@ -269,7 +294,9 @@ __device__ inline void store_tile(const f32x16 (&acc)[C::TI][C::TJ], float * Cou
             for (int i = 0; i < C::TI; i++)
 #pragma unroll
                 for (int v = 0; v < 16; v++) {
-                    const float x = acc[i][j][v];
+                    float x = acc[i][j][v];
+                    if constexpr (RES)
+                        x += rl[(i * 32 + (v >> 2) * 8 + khalf * 4 + (v & 3)) * C::WN + j * 32 + (lane & 31)];
                     bad |= !(__builtin_fabsf(x) <= 3.402823466e38f);
                     const int roff = (row0 + i * 32 + (v >> 2) * 8 + (v & 3)) * (int) ldc * 4;
                     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), rc, voff + roff, 0, 0);
@@ -372,6 +399,8 @@ struct gemm_params {
     uint8_t * xout;     // fused GLU outputs (one weight)
     float * h;
     int64_t ldh;
+    const float * res;  // residual added by the EPI_RESIDUAL epilogue (one weight)
+    int64_t ldr;
     uint32_t * nonfinite;
     // Split-K: with splits S > 1, workgroup v takes unit v of the sequence
     // (split 0 of every tile, split 1 of every tile, ...): split s of a tile is
@@ -575,7 +604,8 @@ __device__ inline void produce(const producer<C> & pr, uint8_t * smem, int a0, i
     }
 }
 
-// EPI < 0: the plain GEMM's fp32 store; EPI >= 0: the fused GLU of that kind.
+// EPI: EPI_PLAIN the fp32 store, EPI_RESIDUAL the fp32 store of acc + res,
+// >= 0 the fused GLU of that kind.
 // SPLIT: split-K (p.splits > 1), else one whole tile per workgroup.
 template <class C, int EPI, bool SPLIT>
 __global__ __launch_bounds__(C::NT, 1) void gemm_kernel(const gemm_params p) {
@@ -642,7 +672,9 @@ __global__ __launch_bounds__(C::NT, 1) void gemm_kernel(const gemm_params p) {
         __syncthreads();
     }
     if (SPLIT && !fixup<C>(acc, p, smem, t, split, wave, lane)) return;
-    if constexpr (EPI < 0)
+    if constexpr (EPI == EPI_RESIDUAL)
+        store_tile<C, true>(acc, W.c, p.M, W.n, W.ldc, m0, n0, wm, wn, lane, p.nonfinite, p.res, p.ldr, smem, wave);
+    else if constexpr (EPI < 0)
         store_tile<C>(acc, W.c, p.M, W.n, W.ldc, m0, n0, wm, wn, lane, p.nonfinite);
     else
         store_glu<C, EPI>(acc, smem, p.xout, p.h, p.ldh, p.M, W.n / 2, m0, n0, wave, wm, wn, lane, p.nonfinite);
@@ -857,12 +889,32 @@ extern "C" int zest_gemm_group(const void * a, int64_t M, int64_t K, int n, cons
                      (long long) N[i], (long long) ldc[i]);
         p.wt[i] = weight_of(w[i], N[i], c[i], ldc[i]);
     }
-    return launch_any<-1>(p, N, zest::as_stream(stream), "zest_gemm");
+    return launch_any<EPI_PLAIN>(p, N, zest::as_stream(stream), "zest_gemm");
 }
 
 extern "C" int zest_gemm(const void * a, int64_t M, const void * w, int64_t N, int64_t K, float * c, int64_t ldc,
                          uint32_t * nonfinite, void * stream) {
     return zest_gemm_group(a, M, K, 1, &w, &N, &c, &ldc, nonfinite, stream);
+}
+
+extern "C" int zest_gemm_residual(const void * a, int64_t M, const void * w, int64_t N, int64_t K, const float * res,
+                                  int64_t ldr, float * c, int64_t ldc, uint32_t * nonfinite, void * stream) {
+    ZEST_REQUIRE(a && w && c && res, "zest_gemm_residual: null pointer");
+    ZEST_REQUIRE(M > 0 && N > 0 && K > 0 && K % 8 == 0, "zest_gemm_residual: M=%lld N=%lld K=%lld", (long long) M,
+                 (long long) N, (long long) K);
+    ZEST_REQUIRE(ldc >= N && ldr >= N, "zest_gemm_residual: ldc %lld / ldr %lld < N %lld", (long long) ldc,
+                 (long long) ldr, (long long) N);
+    ZEST_REQUIRE((reinterpret_cast<uintptr_t>(res) & 15) == 0 && ldr % 4 == 0,
+                 "zest_gemm_residual: the residual's rows must be 16-byte aligned");
+    ZEST_REQUIRE(zest_act_bytes(M, K) < (1ull << 31) && zest_bfp16_bytes(N, K) < (1ull << 31) &&
+                     (uint64_t) zest_rows_padded(M) * (uint64_t) std::max(ldc, ldr) * 4 < (1ull << 31),
+                 "zest_gemm_residual: operands and output must be under 2 GiB");
+    gemm_params p = base_params(a, M, K, nonfinite);
+    p.nw = 1;
+    p.wt[0] = weight_of(w, N, c, ldc);
+    p.res = res;
+    p.ldr = ldr;
+    return launch_any<EPI_RESIDUAL>(p, &N, zest::as_stream(stream), "zest_gemm_residual");
 }
 
 extern "C" int zest_gemm_glu(int kind, const void * a, int64_t M, const void * w_gu, int64_t F, int64_t K,

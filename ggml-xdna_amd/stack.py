@@ -5,11 +5,11 @@ A layer, for one chunk of M tokens with residual stream h [M][H] (fp32):
     RMS_NORM(h) * w_attn   -> packed (fused)        xdna-exec's norm -> q/k/v piece
     Q, K, V = GEMM(packed, Wq / Wk / Wv)            one grouped launch
     (attention is excluded; the O projection's input is a stand-in: Q's output)
-    pack(Q) ; O = GEMM(., Wo) ; h = h + O
+    pack(Q) ; h = h + GEMM(., Wo)                   the residual add in the GEMM's store
     RMS_NORM(h) * w_ffn    -> packed (fused)
     SiLU(packed . Wgate) * (packed . Wup) -> packed  one fused gate/up GEMM
                                                     (xdna-exec's find_fusions)
-    D = GEMM(., Wdown) ; h = h + D
+    h = h + GEMM(., Wdown)
 With fused=False the gate and up are two GEMMs and the SwiGLU its own kernel,
 as for a GLU that cannot be fused.
 Weights are random-init N(0, 0.02), quantised to GGUF on the GPU, converted
@@ -138,11 +138,9 @@ class Stack:
         self.qo = torch.empty((m, c.q), **f32)
         self.ko = torch.empty((m, c.kv), **f32)
         self.vo = torch.empty((m, c.kv), **f32)
-        self.oo = torch.empty((m, c.hidden), **f32)
         if not self.fused:
             self.go = torch.empty((m, c.ffn), **f32)
             self.uo = torch.empty((m, c.ffn), **f32)
-        self.do = torch.empty((m, c.hidden), **f32)
         # the matmuls' activation operands (the bfp16 pack, expanded)
         self.pa = z.empty_act(m, c.hidden, dev)
         self.po = z.empty_act(m, c.q, dev)
@@ -156,7 +154,7 @@ class Stack:
         eps = 1e-6
         # a short last chunk uses the first m rows of every buffer (the
         # packed operands are laid out for m rows by their writer and reader)
-        h, qo, ko, vo, oo, do = (t[:m] for t in (self.h, self.qo, self.ko, self.vo, self.oo, self.do))
+        h, qo, ko, vo = (t[:m] for t in (self.h, self.qo, self.ko, self.vo))
         go, uo = (self.go[:m], self.uo[:m]) if not self.fused else (None, None)
         h.copy_(x_chunk)
 
@@ -180,8 +178,8 @@ class Stack:
                                        [c.q, c.kv, c.kv], c.hidden, outs=[qo, ko, vo]),
                   2.0 * m * (c.q + 2 * c.kv) * c.hidden)
             z.pack_act_x(qo, out=self.po)
-            gemm(self.po, "attn_output", L, c.hidden, c.q, oo)
-            z.add(h, oo, y=h)
+            timed(lambda: z.gemm_residual(self.po, m, L.w["attn_output"], c.hidden, c.q, h, out=h),
+                  2.0 * m * c.hidden * c.q)
             z.rms_norm(h, eps, L.ffn_norm, y=None, packed=self.pa)
             if self.fused:
                 timed(lambda: z.gemm_glu(z.GLU_SWIGLU, self.pa, m, L.w["ffn_gate_up"], c.ffn, c.hidden,
@@ -190,8 +188,8 @@ class Stack:
                 gemm(self.pa, "ffn_gate", L, c.ffn, c.hidden, go)
                 gemm(self.pa, "ffn_up", L, c.ffn, c.hidden, uo)
                 z.glu(z.GLU_SWIGLU, go, uo, c.ffn, y=None, packed=self.pd)
-            gemm(self.pd, "ffn_down", L, c.hidden, c.ffn, do)
-            z.add(h, do, y=h)
+            timed(lambda: z.gemm_residual(self.pd, m, L.w["ffn_down"], c.hidden, c.ffn, h, out=h),
+                  2.0 * m * c.hidden * c.ffn)
         return h
 
     def run_gemms(self):
@@ -203,11 +201,11 @@ class Stack:
         n, flops = 0, 0.0
         for t0 in range(0, c.tokens, self.chunk):
             m = min(self.chunk, c.tokens - t0)
-            qo, ko, vo, oo, do = (t[:m] for t in (self.qo, self.ko, self.vo, self.oo, self.do))
+            h, qo, ko, vo = (t[:m] for t in (self.h, self.qo, self.ko, self.vo))
             for L in self.layers:
                 z.gemm_group(self.pa, m, [L.w["attn_q"], L.w["attn_k"], L.w["attn_v"]], [c.q, c.kv, c.kv],
                              c.hidden, outs=[qo, ko, vo])
-                z.gemm(self.po, m, L.w["attn_output"], c.hidden, c.q, out=oo)
+                z.gemm_residual(self.po, m, L.w["attn_output"], c.hidden, c.q, h, out=h)
                 if self.fused:
                     z.gemm_glu(z.GLU_SWIGLU, self.pa, m, L.w["ffn_gate_up"], c.ffn, c.hidden, xout=self.pd)
                     n += 3
@@ -215,7 +213,7 @@ class Stack:
                     z.gemm(self.pa, m, L.w["ffn_gate"], c.ffn, c.hidden, out=self.go[:m])
                     z.gemm(self.pa, m, L.w["ffn_up"], c.ffn, c.hidden, out=self.uo[:m])
                     n += 4
-                z.gemm(self.pd, m, L.w["ffn_down"], c.hidden, c.ffn, out=do)
+                z.gemm_residual(self.pd, m, L.w["ffn_down"], c.hidden, c.ffn, h, out=h)
                 n += 1
                 flops += 2.0 * m * ((c.q + 2 * c.kv) * c.hidden + c.hidden * c.q + 2 * c.ffn * c.hidden +
                                     c.hidden * c.ffn)

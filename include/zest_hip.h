@@ -103,6 +103,14 @@ ZEST_API int zest_convert_weight(int type, const void *raw, int64_t N, int64_t K
 ZEST_API int zest_gemm(const void *a, int64_t M, const void *w, int64_t N, int64_t K, float *c, int64_t ldc,
                        uint32_t *nonfinite, void *stream);
 
+/* c[M][N] = A . W^T + res[M][N] (row stride ldr floats, 16-byte aligned
+ * rows; res may be c itself, for an in-place residual add): zest_gemm with
+ * the ADD that follows a matmul fused into its store, bit-exact with zest_gemm
+ * then zest_add. Replaces the matmul + ADD of the reference's row pass
+ * (src/xdna-exec.cpp:278-289 after xdna_npu::mul_mat). */
+ZEST_API int zest_gemm_residual(const void *a, int64_t M, const void *w, int64_t N, int64_t K, const float *res,
+                                int64_t ldr, float *c, int64_t ldc, uint32_t *nonfinite, void *stream);
+
 /* Up to ZEST_GEMM_MAX_GROUP weights that share one activation operand, in one
  * launch: c[i][M][N[i]] (row stride ldc[i]) = A . w[i]^T, as zest_gemm
  * computes each (the same products; the launch's split of K among

@@ -89,8 +89,9 @@ def test_mul_mat_gpu_conversion_in_graph():
 def test_host_ops_gpu():
     out = run("test_host_ops", GGML_XDNA_TRACE="2")
     # the FFN block's gate and up ran as one fused launch with the SwiGLU,
-    # and q, k and v as one grouped launch
-    assert "1 fused gate/up, 1 grouped" in out
+    # q, k and v as one grouped launch, and the down projection with the
+    # residual ADD in its store
+    assert "1 fused gate/up, 1 grouped, 1 with a residual add" in out
 
 
 @pytest.mark.gpu

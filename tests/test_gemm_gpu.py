@@ -223,3 +223,29 @@ def test_gemm_group_rejects_bad_counts(zest_gpu):
     with pytest.raises(RuntimeError):
         zest_gpu.gemm_group(a, 64, [], [], 64)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("M,N,K", [
+    (2048, 2560, 4096),   # config 3's O projection: h += O
+    (2048, 2560, 9728),   # its down projection (split K)
+    (300, 200, 256),      # ragged rows, 128x128 tiles
+    (1024, 1000, 512),    # a width that is not a tile multiple
+])
+def test_gemm_residual_is_gemm_then_add(zest_gpu, M, N, K):
+    # the residual epilogue adds in the store: the same floats as the GEMM
+    # followed by the ADD kernel, in place (res is the output) or not
+    import torch
+    x = Rng(M + 11).normal(M * K).reshape(M, K)
+    w = Rng(N + 11).normal(N * K, 0, 0.02).reshape(N, K)
+    a = zest_gpu.pack_act_x(_dev(x))
+    wp = zest_gpu.convert_weight(0, _dev(w.view(np.uint8)), N, K)
+    h0 = torch.from_numpy(Rng(M + N).normal(M * N).reshape(M, N)).cuda()
+    want = zest_gpu.add(zest_gpu.gemm(a, M, wp, N, K), h0)
+    out = zest_gpu.gemm_residual(a, M, wp, N, K, h0)
+    h = h0.clone()
+    nf = torch.zeros(1, dtype=torch.int32, device="cuda")
+    zest_gpu.gemm_residual(a, M, wp, N, K, h, out=h, nonfinite=nf)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int32), want.view(torch.int32))
+    assert torch.equal(h.view(torch.int32), want.view(torch.int32))
+    assert int(nf.item()) == 0
