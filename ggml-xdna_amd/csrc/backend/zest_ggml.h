@@ -58,9 +58,26 @@ inline type_traits traits_of(int type) {
     }
 }
 
-// weight types the converter turns into bfp16 (zest_convert_weight)
+// weight types the converter turns into bfp16 (zest_convert_weight): the
+// reference takes any type with a to_float (src/ggml-zest.cpp:1066-1072);
+// these are GGUF's float and block types (not the IQ family, Q8_1 or Q8_K)
 inline bool convertible(int type) {
-    return type == GGML_TYPE_F32 || type == GGML_TYPE_Q8_0 || type == GGML_TYPE_Q4_K;
+    switch (type) {
+        case GGML_TYPE_F32:
+        case GGML_TYPE_F16:
+        case GGML_TYPE_BF16:
+        case GGML_TYPE_Q4_0:
+        case GGML_TYPE_Q4_1:
+        case GGML_TYPE_Q5_0:
+        case GGML_TYPE_Q5_1:
+        case GGML_TYPE_Q8_0:
+        case GGML_TYPE_Q2_K:
+        case GGML_TYPE_Q3_K:
+        case GGML_TYPE_Q4_K:
+        case GGML_TYPE_Q5_K:
+        case GGML_TYPE_Q6_K: return true;
+        default: return false;
+    }
 }
 
 inline int64_t nelements(const ggml_tensor * t) { return t->ne[0] * t->ne[1] * t->ne[2] * t->ne[3]; }

@@ -3,8 +3,8 @@
 //   zest_pack_act_x      fp32 activations -> the GEMM's expanded operand: the
 //                        same bfp16 blocks, stored decoded as bf16
 //   zest_expand_act      packed bfp16 -> expanded operand
-//   zest_convert_weight  GGUF F32 / Q8_0 / Q4_K weights -> packed bfp16 (once,
-//                        into the resident weight cache)
+//   zest_convert_weight  GGUF weights (F32, F16, BF16, Q4_0..Q8_0, Q2_K..Q6_K)
+//                        -> packed bfp16 (once, into the resident weight cache)
 // All write the layouts of zest_layout.h with 16-byte stores.
 #include "zest_common.h"
 #include "zest_device.h"
@@ -226,6 +226,231 @@ __global__ __launch_bounds__(256) void convert_q4_k_kernel(const uint8_t * __res
     store_tile_row(dst, R_pad, dst_row(r, gu), col / ZEST_TILE_K, v);
 }
 
+// ---- the other GGUF types ------------------------------------------------------
+// One thread per 64 consecutive values of a row (one tile row of one tile
+// column), dequantised as ggml's to_float does: every product below is exact
+// in fp32 (fp16 scale x small integers), so where the format adds an offset
+// the one rounding is the addition's and fmaf gives the same float.
+
+__device__ inline uint32_t ld16(const uint8_t * p) { return *reinterpret_cast<const uint16_t *>(p); }  // 2-aligned
+__device__ inline uint32_t ld32(const uint8_t * p) { return *reinterpret_cast<const uint32_t *>(p); }  // 4-aligned
+__device__ inline uint32_t ld32h(const uint8_t * p) { return ld16(p) | (ld16(p + 2) << 16); }          // 2-aligned
+__device__ inline uint32_t byte_of(const uint32_t * w, int i) { return (w[i >> 2] >> ((i & 3) * 8)) & 0xffu; }
+
+// 32-value blocks: byte j of qs holds value j (low nibble) and j + 16 (high);
+// bit j of the 32-bit qh is value j's fifth bit. SIGNED: q - 2^(bits-1)
+// times d; else q*d + m.
+template <int BITS, bool SIGNED>
+__device__ inline void dq_block32(float d, float m, uint32_t qh, const uint32_t qs[4], float * v) {
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const uint32_t b = byte_of(qs, j);
+        int lo = (int) (b & 0xF), hi = (int) (b >> 4);
+        if (BITS == 5) {
+            lo |= (int) ((qh >> j) & 1u) << 4;
+            hi |= (int) ((qh >> (j + 16)) & 1u) << 4;
+        }
+        if (SIGNED) {
+            v[j] = (float) (lo - (1 << (BITS - 1))) * d;
+            v[j + 16] = (float) (hi - (1 << (BITS - 1))) * d;
+        } else {
+            v[j] = fmaf((float) lo, d, m);
+            v[j + 16] = fmaf((float) hi, d, m);
+        }
+    }
+}
+
+template <int TYPE>
+__device__ inline void dq_32(const uint8_t * p, float * v) {
+    uint32_t qs[4];
+    if (TYPE == ZEST_TYPE_Q4_0) {  // d, qs[16]: 18 bytes
+#pragma unroll
+        for (int i = 0; i < 4; i++) qs[i] = ld32h(p + 2 + 4 * i);
+        dq_block32<4, true>(half_to_float((uint16_t) ld16(p)), 0.0f, 0, qs, v);
+    } else if (TYPE == ZEST_TYPE_Q4_1) {  // d, m, qs[16]: 20 bytes
+        const uint32_t h = ld32(p);
+#pragma unroll
+        for (int i = 0; i < 4; i++) qs[i] = ld32(p + 4 + 4 * i);
+        dq_block32<4, false>(half_to_float((uint16_t) (h & 0xffff)), half_to_float((uint16_t) (h >> 16)), 0, qs, v);
+    } else if (TYPE == ZEST_TYPE_Q5_0) {  // d, qh[4], qs[16]: 22 bytes
+#pragma unroll
+        for (int i = 0; i < 4; i++) qs[i] = ld32h(p + 6 + 4 * i);
+        dq_block32<5, true>(half_to_float((uint16_t) ld16(p)), 0.0f, ld32h(p + 2), qs, v);
+    } else {  // Q5_1: d, m, qh[4], qs[16]: 24 bytes
+        const uint32_t h = ld32(p);
+#pragma unroll
+        for (int i = 0; i < 4; i++) qs[i] = ld32(p + 8 + 4 * i);
+        dq_block32<5, false>(half_to_float((uint16_t) (h & 0xffff)), half_to_float((uint16_t) (h >> 16)), ld32(p + 4),
+                             qs, v);
+    }
+}
+
+// Values [col, col + 64) of one row (col % 64 == 0, col < K).
+template <int TYPE>
+__device__ inline void dq_64(const uint8_t * row, int64_t col, int64_t K, float v[64]) {
+    if (TYPE == ZEST_TYPE_F16 || TYPE == ZEST_TYPE_BF16) {
+        // K % 8 == 0 but maybe not % 64: 8-value chunks past K read as zero
+        const uint4 * p = reinterpret_cast<const uint4 *>(row + col * 2);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint4 q = col + 8 * i < K ? p[i] : make_uint4(0, 0, 0, 0);
+            const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t lo = w[k] & 0xffff, hi = w[k] >> 16;
+                if (TYPE == ZEST_TYPE_F16) {
+                    v[8 * i + 2 * k] = half_to_float((uint16_t) lo);
+                    v[8 * i + 2 * k + 1] = half_to_float((uint16_t) hi);
+                } else {
+                    v[8 * i + 2 * k] = __uint_as_float(lo << 16);
+                    v[8 * i + 2 * k + 1] = __uint_as_float(hi << 16);
+                }
+            }
+        }
+    } else if (TYPE == ZEST_TYPE_Q4_0 || TYPE == ZEST_TYPE_Q4_1 || TYPE == ZEST_TYPE_Q5_0 ||
+               TYPE == ZEST_TYPE_Q5_1) {
+        constexpr int B = TYPE == ZEST_TYPE_Q4_0 ? 18 : TYPE == ZEST_TYPE_Q4_1 ? 20 : TYPE == ZEST_TYPE_Q5_0 ? 22 : 24;
+        const uint8_t * p = row + (col / 32) * B;
+        dq_32<TYPE>(p, v);
+        if (col + 32 < K) {
+            dq_32<TYPE>(p + B, v + 32);
+        } else {
+#pragma unroll
+            for (int i = 32; i < 64; i++) v[i] = 0.0f;
+        }
+    } else if (TYPE == ZEST_TYPE_Q2_K) {
+        // scales[16], qs[64], d, dmin: 84 bytes. Quarter c4 = half h, groups
+        // 4c..4c+3 of 16 (c = c4 % 2); group g takes 2-bit field g/2 of
+        // qs[32h + 16(g%2) + l], scale byte 8h + g: y = (d*(s&15))*q - dmin*(s>>4)
+        const int64_t sb = col / 256;
+        const int c4 = (int) ((col % 256) / 64), h = c4 >> 1, c = c4 & 1;
+        const uint8_t * p = row + sb * 84;
+        const uint32_t dd = ld32(p + 80), sw = ld32(p + 8 * h + 4 * c);
+        const float d = half_to_float((uint16_t) (dd & 0xffff)), dmin = half_to_float((uint16_t) (dd >> 16));
+        uint32_t q[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) q[i] = ld32(p + 16 + 32 * h + 4 * i);
+#pragma unroll
+        for (int gi = 0; gi < 4; gi++) {
+            const int g = 4 * c + gi, sh = 2 * (g >> 1);
+            const uint32_t s = (sw >> (8 * gi)) & 0xffu;
+            const float dl = d * (float) (s & 0xF), ml = dmin * (float) (s >> 4);
+#pragma unroll
+            for (int l = 0; l < 16; l++)
+                v[16 * gi + l] = fmaf(dl, (float) ((byte_of(q, 16 * (gi & 1) + l) >> sh) & 3u), -ml);
+        }
+    } else if (TYPE == ZEST_TYPE_Q3_K) {
+        // hmask[32], qs[64], scales[12], d: 110 bytes. As Q2_K's fields, with
+        // q = field - 4 where bit 4h + g/2 of hmask[16(g%2) + l] is clear, and
+        // 6-bit signed scales: y = (d*scale)*q, exact.
+        const int64_t sb = col / 256;
+        const int c4 = (int) ((col % 256) / 64), h = c4 >> 1, c = c4 & 1;
+        const uint8_t * p = row + sb * 110;
+        const float d = half_to_float((uint16_t) ld16(p + 108));
+        uint32_t hm[8], q[8], sc[3];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            hm[i] = ld32h(p + 4 * i);
+            q[i] = ld32h(p + 32 + 32 * h + 4 * i);
+        }
+#pragma unroll
+        for (int i = 0; i < 3; i++) sc[i] = ld32h(p + 96 + 4 * i);
+#pragma unroll
+        for (int gi = 0; gi < 4; gi++) {
+            const int g = 4 * c + gi, j = g >> 1, si = 8 * h + g;
+            const int lo = si < 8 ? (int) (byte_of(sc, si) & 0xF) : (int) (byte_of(sc, si - 8) >> 4);
+            const int hi = (int) ((byte_of(sc, 8 + (si & 3)) >> (2 * (si >> 2))) & 3u);
+            const float dl = d * (float) ((lo | (hi << 4)) - 32);
+#pragma unroll
+            for (int l = 0; l < 16; l++) {
+                const int o = 16 * (gi & 1) + l;
+                const int f = (int) ((byte_of(q, o) >> (2 * j)) & 3u) - ((byte_of(hm, o) >> (4 * h + j)) & 1u ? 0 : 4);
+                v[16 * gi + l] = dl * (float) f;
+            }
+        }
+    } else if (TYPE == ZEST_TYPE_Q5_K) {
+        // d, dmin, scales[12], qh[32], qs[128]: 176 bytes. Group j of 64:
+        // Q4_K's nibbles of qs[32j..32j+32) and pairs 2j, 2j+1, fifth bits
+        // 2j (low nibbles) and 2j + 1 (high) of qh[l].
+        const int64_t sb = col / 256;
+        const int jq = (int) ((col % 256) / 64);
+        const uint8_t * p = row + sb * 176;
+        const uint4 hdr = *reinterpret_cast<const uint4 *>(p);
+        const uint4 h0 = *reinterpret_cast<const uint4 *>(p + 16), h1 = *reinterpret_cast<const uint4 *>(p + 32);
+        const uint4 qa = *reinterpret_cast<const uint4 *>(p + 48 + 32 * jq);
+        const uint4 qb = *reinterpret_cast<const uint4 *>(p + 64 + 32 * jq);
+        const float d = half_to_float((uint16_t) (hdr.x & 0xffff)), dmin = half_to_float((uint16_t) (hdr.x >> 16));
+        const uint32_t scw[3] = {hdr.y, hdr.z, hdr.w};
+        const uint32_t qh[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+        const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const int s = 2 * jq + e;
+            uint32_t scv, mv;
+            if (s < 4) {
+                scv = byte_of(scw, s) & 63;
+                mv = byte_of(scw, s + 4) & 63;
+            } else {
+                scv = (byte_of(scw, s + 4) & 0xF) | ((byte_of(scw, s - 4) >> 6) << 4);
+                mv = (byte_of(scw, s + 4) >> 4) | ((byte_of(scw, s) >> 6) << 4);
+            }
+            const float d1 = d * (float) scv, m1 = dmin * (float) mv;
+#pragma unroll
+            for (int l = 0; l < 32; l++) {
+                const uint32_t qv = ((byte_of(w, l) >> (4 * e)) & 0xF) | (((byte_of(qh, l) >> s) & 1u) << 4);
+                v[32 * e + l] = fmaf(d1, (float) qv, -m1);
+            }
+        }
+    } else {  // Q6_K
+        // ql[128], qh[64], int8 scales[16], d: 210 bytes. Half h, quarters
+        // c = 2c2 + e: value l's low 4 bits are nibble c2 of
+        // ql[64h + 32e + l], its high 2 bits bits 2c of qh[32h + l]; minus
+        // 32, times d*scales[8h + 2c + l/16] (products exact in fp32).
+        const int64_t sb = col / 256;
+        const int c4 = (int) ((col % 256) / 64), h = c4 >> 1, c2 = c4 & 1;
+        const uint8_t * p = row + sb * 210;
+        const float d = half_to_float((uint16_t) ld16(p + 208));
+        const uint32_t sw = ld32h(p + 192 + 8 * h + 4 * c2);
+        uint32_t ql[16], qh[8];
+#pragma unroll
+        for (int i = 0; i < 16; i++) ql[i] = ld32h(p + 64 * h + 4 * i);
+#pragma unroll
+        for (int i = 0; i < 8; i++) qh[i] = ld32h(p + 128 + 32 * h + 4 * i);
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const int cq = 2 * c2 + e;
+#pragma unroll
+            for (int l = 0; l < 32; l++) {
+                const int lo = (int) ((byte_of(ql, 32 * e + l) >> (4 * c2)) & 0xF);
+                const int hi = (int) ((byte_of(qh, l) >> (2 * cq)) & 3u);
+                const int8_t s = (int8_t) ((sw >> (8 * (2 * e + l / 16))) & 0xffu);
+                v[32 * e + l] = (d * (float) s) * (float) ((lo | (hi << 4)) - 32);
+            }
+        }
+    }
+}
+
+// Workgroup: 16 rows x 16 tile columns (1024 values of each row); lane t
+// takes row t/16 and tile column t%16, so the 16 lanes of a row read one
+// contiguous run of its GGUF bytes.
+template <int TYPE>
+__global__ __launch_bounds__(256) void convert_kernel(const uint8_t * __restrict__ raw, size_t row_bytes, int64_t N,
+                                                      int64_t K, uint8_t * __restrict__ dst, int64_t R_pad,
+                                                      int64_t K_pad, int64_t R_src, int gu) {
+    const int t = threadIdx.x;
+    const int64_t r = (int64_t) blockIdx.y * ZEST_TILE_ROWS + (t >> 4);
+    const int64_t kc = (int64_t) blockIdx.x * 16 + (t & 15), col = kc * ZEST_TILE_K;
+    if (col >= K_pad || r >= R_src) return;
+    float v[64];
+    if (r < N && col < K) {
+        dq_64<TYPE>(raw + r * (int64_t) row_bytes, col, K, v);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 64; i++) v[i] = 0.0f;
+    }
+    store_tile_row(dst, R_pad, dst_row(r, gu), kc, v);
+}
+
 bool aligned(const void * p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 } // namespace
@@ -241,9 +466,34 @@ size_t zest_bfp16_bytes(int64_t rows, int64_t K) {
 size_t zest_raw_row_bytes(int type, int64_t K) {
     switch (type) {
         case ZEST_TYPE_F32: return (size_t) K * 4;
+        case ZEST_TYPE_F16:
+        case ZEST_TYPE_BF16: return (size_t) K * 2;
+        case ZEST_TYPE_Q4_0: return K % 32 ? 0 : (size_t) (K / 32) * 18;
+        case ZEST_TYPE_Q4_1: return K % 32 ? 0 : (size_t) (K / 32) * 20;
+        case ZEST_TYPE_Q5_0: return K % 32 ? 0 : (size_t) (K / 32) * 22;
+        case ZEST_TYPE_Q5_1: return K % 32 ? 0 : (size_t) (K / 32) * 24;
         case ZEST_TYPE_Q8_0: return K % 32 ? 0 : (size_t) (K / 32) * 34;
+        case ZEST_TYPE_Q2_K: return K % 256 ? 0 : (size_t) (K / 256) * 84;
+        case ZEST_TYPE_Q3_K: return K % 256 ? 0 : (size_t) (K / 256) * 110;
         case ZEST_TYPE_Q4_K: return K % 256 ? 0 : (size_t) (K / 256) * 144;
+        case ZEST_TYPE_Q5_K: return K % 256 ? 0 : (size_t) (K / 256) * 176;
+        case ZEST_TYPE_Q6_K: return K % 256 ? 0 : (size_t) (K / 256) * 210;
         default: return 0;
+    }
+}
+
+// required alignment of a weight's rows, by the widest load its converter makes
+static size_t row_align(int type) {
+    switch (type) {
+        case ZEST_TYPE_F32:
+        case ZEST_TYPE_F16:
+        case ZEST_TYPE_BF16:
+        case ZEST_TYPE_Q4_K:
+        case ZEST_TYPE_Q5_K: return 16;
+        case ZEST_TYPE_Q4_1:
+        case ZEST_TYPE_Q5_1:
+        case ZEST_TYPE_Q2_K: return 4;
+        default: return 2;
     }
 }
 
@@ -315,9 +565,38 @@ static int convert(int type, const void * raw, int64_t N, int64_t K, void * dst,
                                R_pad, K_pad, R_src, gu);
             return zest::check_launch(name);
         }
-        default:
-            return zest::fail(ZEST_E_UNSUPPORTED, "%s: weight type %d has no converter", name, type);
+        default: break;
     }
+    const size_t rb = zest_raw_row_bytes(type, K);
+    if (rb == 0) {
+        if (zest_raw_row_bytes(type, 256) == 0)
+            return zest::fail(ZEST_E_UNSUPPORTED, "%s: weight type %d has no converter", name, type);
+        return zest::fail(ZEST_E_ARG, "%s: K=%lld is not a multiple of type %d's block", name, (long long) K,
+                          type);
+    }
+    ZEST_REQUIRE(aligned(raw, row_align(type)), "%s: type %d rows must be %zu-byte aligned", name, type,
+                 row_align(type));
+    const dim3 grid((unsigned) ((K_pad / ZEST_TILE_K + 15) / 16), (unsigned) (R_src / ZEST_TILE_ROWS));
+    const uint8_t * r8 = (const uint8_t *) raw;
+    uint8_t * d8 = (uint8_t *) dst;
+#define ZEST_CONVERT(T)                                                                                         \
+    case T: hipLaunchKernelGGL(convert_kernel<T>, grid, dim3(256), 0, s, r8, rb, N, K, d8, R_pad, K_pad, R_src, gu); \
+        break
+    switch (type) {
+        ZEST_CONVERT(ZEST_TYPE_F16);
+        ZEST_CONVERT(ZEST_TYPE_BF16);
+        ZEST_CONVERT(ZEST_TYPE_Q4_0);
+        ZEST_CONVERT(ZEST_TYPE_Q4_1);
+        ZEST_CONVERT(ZEST_TYPE_Q5_0);
+        ZEST_CONVERT(ZEST_TYPE_Q5_1);
+        ZEST_CONVERT(ZEST_TYPE_Q2_K);
+        ZEST_CONVERT(ZEST_TYPE_Q3_K);
+        ZEST_CONVERT(ZEST_TYPE_Q5_K);
+        ZEST_CONVERT(ZEST_TYPE_Q6_K);
+        default: return zest::fail(ZEST_E_UNSUPPORTED, "%s: weight type %d has no converter", name, type);
+    }
+#undef ZEST_CONVERT
+    return zest::check_launch(name);
 }
 
 int zest_convert_weight(int type, const void * raw, int64_t N, int64_t K, void * dst, void * stream) {

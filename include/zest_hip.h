@@ -32,7 +32,21 @@ enum zest_status {
 };
 
 /* Weight types, numbered as ggml's enum ggml_type. */
-enum zest_type { ZEST_TYPE_F32 = 0, ZEST_TYPE_Q8_0 = 8, ZEST_TYPE_Q4_K = 12 };
+enum zest_type {
+    ZEST_TYPE_F32 = 0,
+    ZEST_TYPE_F16 = 1,
+    ZEST_TYPE_Q4_0 = 2,
+    ZEST_TYPE_Q4_1 = 3,
+    ZEST_TYPE_Q5_0 = 6,
+    ZEST_TYPE_Q5_1 = 7,
+    ZEST_TYPE_Q8_0 = 8,
+    ZEST_TYPE_Q2_K = 10,
+    ZEST_TYPE_Q3_K = 11,
+    ZEST_TYPE_Q4_K = 12,
+    ZEST_TYPE_Q5_K = 13,
+    ZEST_TYPE_Q6_K = 14,
+    ZEST_TYPE_BF16 = 30
+};
 
 /* GLU kinds. Not ggml's numbering (ggml_glu_op has SWIGLU_OAI at 3, which
  * this library does not run): a ggml caller maps by kind. */
@@ -84,10 +98,14 @@ ZEST_API int zest_pack_act_x(const float *x, int64_t M, int64_t K, int64_t ldx, 
  * 129-144, as bf16). */
 ZEST_API int zest_expand_act(const void *src, int64_t M, int64_t K, void *dst, void *stream);
 
-/* A GGUF weight raw[N][K] of `type` (F32, Q8_0 or Q4_K rows, as ggml stores
+/* A GGUF weight raw[N][K] of `type` (any zest_type, rows as ggml stores
  * them) -> packed bfp16 weight cache entry (zest_bfp16_bytes(N, K) bytes).
- * Dequantisation as ggml's to_float, then the same encoder. Replaces
- * xdna_npu::add_weight's unpack + bfp16_pack_b (src/xdna-npu.cpp:339-378). */
+ * Dequantisation as ggml's to_float, then the same encoder. K must be a
+ * multiple of the type's block (32 for Q4_0..Q8_0, 256 for the K-quants).
+ * Row alignment: 16 bytes for F32, F16, BF16, Q4_K and Q5_K, 4 for Q4_1,
+ * Q5_1 and Q2_K, 2 for the rest. Replaces xdna_npu::add_weight's unpack +
+ * bfp16_pack_b (src/xdna-npu.cpp:339-378), which converts any type with a
+ * to_float (src/ggml-zest.cpp:1066-1072). */
 ZEST_API int zest_convert_weight(int type, const void *raw, int64_t N, int64_t K, void *dst, void *stream);
 
 /* c[M][N] (row stride ldc floats) = A . W^T, a the expanded activation

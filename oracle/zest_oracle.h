@@ -13,9 +13,14 @@
  *                                and a brute-force sweep of all exponent bytes
  *   NPU tile order (A/B) ....... pinned: byte-equal to the reference packer's
  *                                pack_a/pack_b output on the golden shapes
- *   Q8_0 / Q4_K dequant ........ pinned by closed form (exact fp32 products) and
- *                                hand-built blocks with known values; ggml's own
- *                                to_float is absent (third-party, not vendored)
+ *   GGUF dequant (F16, BF16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K,
+ *   Q5_K, Q6_K) ................ pinned by closed form (every product is exact
+ *                                in fp32), hand-built blocks with known values,
+ *                                relations between the types (Q5_K with no
+ *                                fifth bits is Q4_K, Q4_1 with m = -8d is Q4_0,
+ *                                ...) and quantise/dequantise error bounds;
+ *                                ggml's own to_float is absent (third-party,
+ *                                not vendored)
  *   ref_mul_mat ................ pinned: integer KAT (exact under any order),
  *                                fp64 recomputation bound
  *   host ops ................... RMS_NORM/MUL/ADD/SCALE/GLU pinned by closed forms
@@ -47,10 +52,22 @@ void orc_pack_a(const float *x, int64_t M, int64_t K, int m, int k, uint8_t *out
 void orc_pack_b(const float *w, int64_t N, int64_t K, int n, int k, int cols, uint8_t *out);
 
 /* ---- GGUF dequant (ggml to_float, called at src/xdna-ref.cpp:44) ----------- */
-enum { ORC_TYPE_F32 = 0, ORC_TYPE_Q8_0 = 8, ORC_TYPE_Q4_K = 12 };
+enum {
+    ORC_TYPE_F32 = 0, ORC_TYPE_F16 = 1, ORC_TYPE_Q4_0 = 2, ORC_TYPE_Q4_1 = 3, ORC_TYPE_Q5_0 = 6, ORC_TYPE_Q5_1 = 7,
+    ORC_TYPE_Q8_0 = 8, ORC_TYPE_Q2_K = 10, ORC_TYPE_Q3_K = 11, ORC_TYPE_Q4_K = 12, ORC_TYPE_Q5_K = 13,
+    ORC_TYPE_Q6_K = 14, ORC_TYPE_BF16 = 30
+};
 size_t orc_row_bytes(int type, int64_t K);
 void orc_dequant_row(int type, const void *raw, float *y, int64_t K);
 float orc_fp16_to_fp32(uint16_t h);
+uint16_t orc_fp32_to_fp16(float f); /* round to nearest even */
+
+/* Synthetic GGUF rows for the tests (what ggml_quantize_chunk is to the
+ * reference's tests, tests/test-mul-mat.cpp:174): valid blocks of every type
+ * above from float rows. A simple min/max search, not ggml's own quantiser:
+ * the bytes are the shared input of every path under test. Returns 0, or -1
+ * for a type or K it does not cover. */
+int orc_quantize_row(int type, const float *x, void *out, int64_t K);
 
 /* ---- CPU reference matmul (src/xdna-ref.cpp:10-97) ------------------------
  * y[M][N] = x[M][K] . W[N][K]^T; W as raw GGUF rows of `type`. One weight row

@@ -40,6 +40,7 @@ blk blk_of(ggml_type t) {
         case GGML_TYPE_Q4_K: return {256, 144};
         case GGML_TYPE_Q5_K: return {256, 176};
         case GGML_TYPE_Q6_K: return {256, 210};
+        case GGML_TYPE_Q8_K: return {256, 292};
         case GGML_TYPE_I32: return {1, 4};
         default: fprintf(stderr, "mini_ggml: type %d not known\n", (int) t); abort();
     }
@@ -263,77 +264,6 @@ void ggml_build_forward_expand(ggml_cgraph * g, ggml_tensor * t) {
 
 // ---- quantisers ----------------------------------------------------------------------
 
-static uint16_t fp32_to_fp16(float f) {
-    uint32_t x;
-    memcpy(&x, &f, 4);
-    const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
-    if (ax >= 0x7f800000u) return (uint16_t) (sign | (ax > 0x7f800000u ? 0x7e00u : 0x7c00u));
-    if (ax >= 0x477ff000u) return (uint16_t) (sign | 0x7c00u);  // 65520 and up round to infinity
-    if (ax < 0x38800000u) {                                     // below 2^-14: a subnormal half
-        float v;
-        memcpy(&v, &ax, 4);
-        return (uint16_t) (sign | (uint32_t) nearbyintf(v * 16777216.0f));
-    }
-    uint32_t h = (((ax >> 23) - 112u) << 10) | ((ax & 0x7fffffu) >> 13);
-    const uint32_t rem = ax & 0x1fffu;
-    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
-    return (uint16_t) (sign | h);
-}
-
-static void put16(uint8_t * p, uint16_t v) { memcpy(p, &v, 2); }
-
-static void quantize_q8_0_row(const float * x, uint8_t * out, int64_t k) {
-    for (int64_t b = 0; b < k / 32; b++, x += 32, out += 34) {
-        float amax = 0;
-        for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(x[i]));
-        const float d = amax / 127.0f, id = d > 0 ? 1.0f / d : 0.0f;
-        put16(out, fp32_to_fp16(d));
-        for (int i = 0; i < 32; i++) out[2 + i] = (uint8_t) (int8_t) fmaxf(-128.0f, fminf(127.0f, roundf(x[i] * id)));
-    }
-}
-
-// per sub-block of 32: m = max(0, -min), s = (max + m)/15; per super-block
-// d = max(s)/63, dmin = max(m)/63 (as fp16); sc = rint(s/d), mn = rint(m/dmin);
-// q = rint((x + dmin*mn)/(d*sc)) clamped to 0..15
-static void quantize_q4_k_row(const float * x, uint8_t * out, int64_t k) {
-    for (int64_t b = 0; b < k / 256; b++, x += 256, out += 144) {
-        float s[8], m[8], smax = 0, mmax = 0;
-        for (int j = 0; j < 8; j++) {
-            float lo = x[32 * j], hi = x[32 * j];
-            for (int i = 0; i < 32; i++) {
-                lo = fminf(lo, x[32 * j + i]);
-                hi = fmaxf(hi, x[32 * j + i]);
-            }
-            m[j] = fmaxf(0.0f, -lo);
-            s[j] = fmaxf(0.0f, (hi + m[j]) / 15.0f);
-            smax = fmaxf(smax, s[j]);
-            mmax = fmaxf(mmax, m[j]);
-        }
-        const uint16_t dh = fp32_to_fp16(smax / 63.0f), mh = fp32_to_fp16(mmax / 63.0f);
-        const float d = orc_fp16_to_fp32(dh), dmin = orc_fp16_to_fp32(mh);
-        uint8_t sc[8], mq[8], q[256];
-        for (int j = 0; j < 8; j++) {
-            sc[j] = (uint8_t) (d > 0 ? fminf(63.0f, nearbyintf(s[j] / d)) : 0.0f);
-            mq[j] = (uint8_t) (dmin > 0 ? fminf(63.0f, nearbyintf(m[j] / dmin)) : 0.0f);
-            const float step = d * sc[j], off = dmin * mq[j];
-            for (int i = 0; i < 32; i++)
-                q[32 * j + i] =
-                    (uint8_t) (step > 0 ? fmaxf(0.0f, fminf(15.0f, nearbyintf((x[32 * j + i] + off) / step))) : 0.0f);
-        }
-        put16(out, dh);
-        put16(out + 2, mh);
-        uint8_t * S = out + 4;
-        for (int j = 0; j < 4; j++) {
-            S[j] = (uint8_t) (sc[j] | ((sc[j + 4] >> 4) << 6));
-            S[j + 4] = (uint8_t) (mq[j] | ((mq[j + 4] >> 4) << 6));
-            S[j + 8] = (uint8_t) ((sc[j + 4] & 0xF) | ((mq[j + 4] & 0xF) << 4));
-        }
-        uint8_t * qs = out + 16;
-        for (int g = 0; g < 4; g++)
-            for (int i = 0; i < 32; i++) qs[32 * g + i] = (uint8_t) (q[64 * g + i] | (q[64 * g + 32 + i] << 4));
-    }
-}
-
 size_t ggml_quantize_chunk(ggml_type type, const float * src, void * dst, int64_t start, int64_t nrows,
                            int64_t n_per_row, const float *) {
     const size_t rb = ggml_row_size(type, n_per_row);
@@ -341,11 +271,9 @@ size_t ggml_quantize_chunk(ggml_type type, const float * src, void * dst, int64_
     for (int64_t r = 0; r < nrows; r++) {
         const float * x = src + start + r * n_per_row;
         uint8_t * o = out + (size_t) r * rb;
-        switch (type) {
-            case GGML_TYPE_F32: memcpy(o, x, rb); break;
-            case GGML_TYPE_Q8_0: quantize_q8_0_row(x, o, n_per_row); break;
-            case GGML_TYPE_Q4_K: quantize_q4_k_row(x, o, n_per_row); break;
-            default: fprintf(stderr, "mini_ggml: no quantiser for type %d\n", (int) type); abort();
+        if (orc_quantize_row((int) type, x, o, n_per_row) != 0) {
+            fprintf(stderr, "mini_ggml: no quantiser for type %d\n", (int) type);
+            abort();
         }
     }
     return rb * (size_t) nrows;

@@ -55,10 +55,20 @@ int main() {
                "batch 1023 is not claimed (below the default threshold of 1024)");
     test_check(ggml_backend_dev_supports_op(dev, make_mul_mat(ctx, GGML_TYPE_Q4_K, k, n, 1024)),
                "batch 1024, q4_K 2048x2048 is claimed");
-    test_check(ggml_backend_dev_supports_op(dev, make_mul_mat(ctx, GGML_TYPE_Q8_0, k, n, 2048)),
-               "batch 2048, q8_0 is claimed");
+    test_check(ggml_backend_dev_supports_op(dev, make_mul_mat(ctx, GGML_TYPE_Q4_0, k, n, 2048)),
+               "batch 2048, q4_0 is claimed");
     test_check(ggml_backend_dev_supports_op(dev, make_mul_mat(ctx, GGML_TYPE_F32, k, n, 2048)),
                "batch 2048, f32 is claimed");
+    // every GGUF float and block type has a converter; Q8_K (a dot-product
+    // intermediate, no weight of a model file) has none and is not claimed
+    for (ggml_type t : {GGML_TYPE_F16, GGML_TYPE_BF16, GGML_TYPE_Q4_1, GGML_TYPE_Q5_0, GGML_TYPE_Q5_1, GGML_TYPE_Q8_0,
+                        GGML_TYPE_Q2_K, GGML_TYPE_Q3_K, GGML_TYPE_Q5_K, GGML_TYPE_Q6_K}) {
+        char what[64];
+        snprintf(what, sizeof what, "batch 2048, type %d is claimed", (int) t);
+        test_check(ggml_backend_dev_supports_op(dev, make_mul_mat(ctx, t, k, n, 2048)), "%s", what);
+    }
+    test_check(!ggml_backend_dev_supports_op(dev, make_mul_mat(ctx, GGML_TYPE_Q8_K, k, n, 2048)),
+               "a type with no converter (q8_K) is not claimed");
     // 2*1024*64*1024 = 134 MFLOP, under the 256 MFLOP floor
     test_check(!ggml_backend_dev_supports_op(dev, make_mul_mat(ctx, GGML_TYPE_Q4_K, 1024, 64, 1024)),
                "a tiny matmul is not claimed even at a large batch");
@@ -91,11 +101,11 @@ int main() {
     // same-shape tensor that may sit in host memory
     {
         ggml_tensor * x = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, k, 2048);
-        ggml_tensor * mm1 = ggml_mul_mat(ctx, ggml_new_tensor_2d(ctx, GGML_TYPE_Q4_K, k, n), x);
-        ggml_tensor * mm2 = ggml_mul_mat(ctx, ggml_new_tensor_2d(ctx, GGML_TYPE_Q4_K, k, n), x);
+        ggml_tensor * mm1 = ggml_mul_mat(ctx, ggml_new_tensor_2d(ctx, GGML_TYPE_Q4_0, k, n), x);
+        ggml_tensor * mm2 = ggml_mul_mat(ctx, ggml_new_tensor_2d(ctx, GGML_TYPE_Q4_0, k, n), x);
         test_check(ggml_backend_dev_supports_op(dev, ggml_add(ctx, mm1, mm2)),
                    "an ADD of two claimed matmuls is claimed (block claiming)");
-        ggml_tensor * emb = ggml_get_rows(ctx, ggml_new_tensor_2d(ctx, GGML_TYPE_Q8_0, k, 32000),
+        ggml_tensor * emb = ggml_get_rows(ctx, ggml_new_tensor_2d(ctx, GGML_TYPE_Q4_0, k, 32000),
                                           ggml_new_tensor_1d(ctx, GGML_TYPE_I32, 2048));
         test_check(!ggml_backend_dev_supports_op(dev, ggml_add(ctx, emb, mm1)),
                    "an ADD of a claimed matmul and the token embeddings (GET_ROWS) is not claimed");
@@ -113,7 +123,7 @@ int main() {
         test_check(ggml_backend_dev_supports_op(dev, ggml_scale(ctx, mm1, 0.25f)), "a SCALE of a claimed matmul is claimed");
         test_check(ggml_backend_dev_supports_op(dev, ggml_geglu_split(ctx, mm1, mm2)),
                    "a GeGLU of two claimed matmuls is claimed");
-        ggml_tensor * fused = ggml_mul_mat(ctx, ggml_new_tensor_2d(ctx, GGML_TYPE_Q4_K, k, 2 * n), x);
+        ggml_tensor * fused = ggml_mul_mat(ctx, ggml_new_tensor_2d(ctx, GGML_TYPE_Q4_0, k, 2 * n), x);
         test_check(ggml_backend_dev_supports_op(dev, ggml_swiglu(ctx, fused)),
                    "a SwiGLU on one claimed matmul holding gate and up is claimed");
         ggml_tensor * norm = ggml_rms_norm(ctx, mm1, 1e-6f);
@@ -142,12 +152,12 @@ int main() {
     // A mixture-of-experts model's expert step is a MUL_MAT_ID: not taken, but
     // the model's ordinary matmuls still are (the backend warns instead).
     {
-        ggml_tensor * experts = ggml_new_tensor_3d(ctx, GGML_TYPE_Q4_K, k, n, 8);
+        ggml_tensor * experts = ggml_new_tensor_3d(ctx, GGML_TYPE_Q4_0, k, n, 8);
         ggml_tensor * rows = ggml_new_tensor_3d(ctx, GGML_TYPE_F32, k, 1, 2048);
         ggml_tensor * ids = ggml_new_tensor_2d(ctx, GGML_TYPE_I32, 1, 2048);
         test_check(!ggml_backend_dev_supports_op(dev, ggml_mul_mat_id(ctx, experts, rows, ids)),
                    "the expert step (MUL_MAT_ID) is not claimed");
-        test_check(ggml_backend_dev_supports_op(dev, make_mul_mat(ctx, GGML_TYPE_Q8_0, k, n, 2048)),
+        test_check(ggml_backend_dev_supports_op(dev, make_mul_mat(ctx, GGML_TYPE_Q4_0, k, n, 2048)),
                    "... and an ordinary matmul is still claimed afterwards");
     }
 

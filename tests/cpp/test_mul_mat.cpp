@@ -130,16 +130,29 @@ int main() {
 
     const case_spec cases[] = {
         {"f32   256x128 x 64", GGML_TYPE_F32, 256, 128, 64, false, false, false},
+        {"f16   256x128 x 64", GGML_TYPE_F16, 256, 128, 64, false, false, false},
         {"q8_0  512x256 x 64", GGML_TYPE_Q8_0, 512, 256, 64, false, false, false},
+        {"q4_0  512x256 x 64", GGML_TYPE_Q4_0, 512, 256, 64, false, false, false},
         {"q4_K  512x256 x 64", GGML_TYPE_Q4_K, 512, 256, 64, false, false, false},
         {"q4_K 2048x512 x 512", GGML_TYPE_Q4_K, 2048, 512, 512, false, false, false},
+        {"q6_K  512x256 x 64", GGML_TYPE_Q6_K, 512, 256, 64, false, false, false},
+        // the other GGUF types the converter takes
+        {"bf16  256x128 x 64", GGML_TYPE_BF16, 256, 128, 64, false, false, false},
+        {"q4_1  512x256 x 64", GGML_TYPE_Q4_1, 512, 256, 64, false, false, false},
+        {"q5_0  512x256 x 64", GGML_TYPE_Q5_0, 512, 256, 64, false, false, false},
+        {"q5_1  512x256 x 64", GGML_TYPE_Q5_1, 512, 256, 64, false, false, false},
+        {"q2_K  512x256 x 64", GGML_TYPE_Q2_K, 512, 256, 64, false, false, false},
+        {"q3_K  512x256 x 64", GGML_TYPE_Q3_K, 512, 256, 64, false, false, false},
+        {"q5_K  512x256 x 64", GGML_TYPE_Q5_K, 512, 256, 64, false, false, false},
         // held in a weight buffer, as llama.cpp loads a model; one weight type
         // each: the cache is keyed by where a weight lives, and a freed
         // buffer's address comes back
-        {"q8_0 2048x1024 x 512 w", GGML_TYPE_Q8_0, 2048, 1024, 512, true, false, false},
+        {"q4_0 2048x1024 x 512 w", GGML_TYPE_Q4_0, 2048, 1024, 512, true, false, false},
         {"q4_K 2048x1024 x 600 w", GGML_TYPE_Q4_K, 2048, 1024, 600, true, false, false},
+        // a Q4_K_M model's Q6_K down projection (Qwen3-4B: 9728 -> 2560)
+        {"q6_K 9728x2560 x 256 w", GGML_TYPE_Q6_K, 9728, 2560, 256, true, false, false},
         // widths that are not multiples of the 256-row tile
-        {"q8_0 1536x896 x 512 w", GGML_TYPE_Q8_0, 1536, 896, 512, true, false, false},
+        {"q4_0 1536x896 x 512 w", GGML_TYPE_Q4_0, 1536, 896, 512, true, false, false},
         {"q8_0 1536x256 x 512 w", GGML_TYPE_Q8_0, 1536, 256, 512, true, false, false},
         {"q4_K 1536x8960 x 520 w", GGML_TYPE_Q4_K, 1536, 8960, 520, true, false, false},
         // K not a multiple of 64 (padded chunk), odd batch

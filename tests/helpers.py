@@ -77,6 +77,7 @@ class Oracle:
         L.orc_a_offset.argtypes, L.orc_a_offset.restype = [_I64, _I64, _I64, _I, _I], ctypes.c_size_t
         L.orc_b_offset.argtypes, L.orc_b_offset.restype = [_I64, _I64, _I64, _I64, _I, _I, _I], ctypes.c_size_t
         L.orc_row_bytes.argtypes, L.orc_row_bytes.restype = [_I, _I64], ctypes.c_size_t
+        L.orc_quantize_row.argtypes, L.orc_quantize_row.restype = [_I, _P, _P, _I64], ctypes.c_int
 
     def encode_rows(self, x: np.ndarray) -> np.ndarray:
         x = np.ascontiguousarray(x, dtype=np.float32)
@@ -110,6 +111,22 @@ class Oracle:
         out = np.empty((n, k), dtype=np.float32)
         for r in range(n):
             self.L.orc_dequant_row(wtype, ctypes.c_void_p(raw.ctypes.data + r * rb), ctypes.c_void_p(out.ctypes.data + r * k * 4), k)
+        return out
+
+    def row_bytes(self, wtype: int, k: int) -> int:
+        return int(self.L.orc_row_bytes(wtype, k))
+
+    def quantize(self, wtype: int, w: np.ndarray) -> np.ndarray:
+        """Synthetic GGUF rows of `wtype` from float rows w[n][k]."""
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        n, k = w.shape
+        rb = self.row_bytes(wtype, k)
+        out = np.empty((n, rb), dtype=np.uint8)
+        for r in range(n):
+            st = self.L.orc_quantize_row(wtype, ctypes.c_void_p(w.ctypes.data + r * k * 4),
+                                         ctypes.c_void_p(out.ctypes.data + r * rb), k)
+            if st != 0:
+                raise ValueError(f"no quantiser for type {wtype} at k={k}")
         return out
 
     def ref_mul_mat(self, wtype: int, raw: np.ndarray, n: int, k: int, x: np.ndarray, threads: int = 8) -> np.ndarray:

@@ -167,6 +167,218 @@ def test_quantize_dequantize_round_trip_bound(oracle, wtype):
         assert np.abs(y - w).max() < 0.02
 
 
+# The rest of GGUF's weight types (the reference converts any type ggml can
+# dequantise, src/ggml-zest.cpp:1066-1072; its own test covers f16, q4_0 and
+# q6_K, tests/test-mul-mat.cpp:140-156). The builders below pack blocks from
+# per-position codes, field by field in the order of the block structs, so
+# that a value read from the wrong nibble, bit or scale shows up as a wrong
+# value at a known position.
+
+F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, BF16 = 1, 2, 3, 6, 7, 8, 10, 11, 12, 13, 14, 30
+ALL_TYPES = [0, F16, BF16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K]
+
+
+def _u32le(v):
+    return np.array([v], dtype="<u4").view(np.uint8)
+
+
+def _nibbles32(q):
+    """32 codes of a 32-value block: value j in the low nibble of byte j,
+    value j + 16 in the high nibble; and the fifth bits as a 32-bit word."""
+    q = np.asarray(q, dtype=np.int64)
+    qs = ((q[:16] & 0xF) | ((q[16:] & 0xF) << 4)).astype(np.uint8)
+    qh = int(sum(int(q[j] >> 4 & 1) << j for j in range(32)))
+    return qs, qh
+
+
+def test_f16_bf16_every_bit_pattern(oracle):
+    bits = np.arange(65536, dtype=np.uint16)
+    y = oracle.dequant(F16, bits.view(np.uint8), 1, 65536).reshape(-1)
+    want = bits.view(np.float16).astype(np.float32)
+    same = (y.view(np.uint32) == want.view(np.uint32)) | (np.isnan(y) & np.isnan(want))
+    assert same.all()
+    y = oracle.dequant(BF16, bits.view(np.uint8), 1, 65536).reshape(-1)
+    assert np.array_equal(y.view(np.uint32), bits.astype(np.uint32) << 16)
+
+
+def test_q4_0_q5_0_hand_built_blocks(oracle):
+    rng = np.random.default_rng(3)
+    for d in (0.5, 3.0e-4, -2.0):
+        q4 = rng.integers(0, 16, 32)
+        qs, _ = _nibbles32(q4)
+        y = oracle.dequant(Q4_0, np.concatenate([_fp16(d), qs]), 1, 32).reshape(-1)
+        assert np.array_equal(y, ((q4 - 8) * np.float64(np.float16(d))).astype(np.float32))
+        q5 = rng.integers(0, 32, 32)
+        qs, qh = _nibbles32(q5)
+        y = oracle.dequant(Q5_0, np.concatenate([_fp16(d), _u32le(qh), qs]), 1, 32).reshape(-1)
+        assert np.array_equal(y, ((q5 - 16) * np.float64(np.float16(d))).astype(np.float32))
+
+
+def test_q4_1_q5_1_hand_built_blocks(oracle):
+    rng = np.random.default_rng(4)
+    for d, m in ((0.25, -1.75), (1.0e-3, 0.3), (2.0, 0.0)):
+        dd, mm = np.float32(np.float16(d)), np.float32(np.float16(m))
+        q4 = rng.integers(0, 16, 32)
+        qs, _ = _nibbles32(q4)
+        y = oracle.dequant(Q4_1, np.concatenate([_fp16(d), _fp16(m), qs]), 1, 32).reshape(-1)
+        assert np.array_equal(y, q4.astype(np.float32) * dd + mm)  # d*q exact: one rounding
+        q5 = rng.integers(0, 32, 32)
+        qs, qh = _nibbles32(q5)
+        y = oracle.dequant(Q5_1, np.concatenate([_fp16(d), _fp16(m), _u32le(qh), qs]), 1, 32).reshape(-1)
+        assert np.array_equal(y, q5.astype(np.float32) * dd + mm)
+
+
+def test_32_value_types_agree_where_their_fields_meet(oracle):
+    # Q4_1 with m = -8d is Q4_0; Q5_1 with no fifth bits is Q4_1; Q5_0 with
+    # every fifth bit set is Q4_1 with m = 0
+    rng = np.random.default_rng(5)
+    for _ in range(20):
+        d = float(np.float16(rng.uniform(-4, 4)))
+        qs = rng.integers(0, 256, 16).astype(np.uint8)
+        a = oracle.dequant(Q4_0, np.concatenate([_fp16(d), qs]), 1, 32)
+        b = oracle.dequant(Q4_1, np.concatenate([_fp16(d), _fp16(-8 * d), qs]), 1, 32)
+        assert np.array_equal(a, b)
+        m = float(np.float16(rng.uniform(-1, 1)))
+        c = oracle.dequant(Q4_1, np.concatenate([_fp16(d), _fp16(m), qs]), 1, 32)
+        e = oracle.dequant(Q5_1, np.concatenate([_fp16(d), _fp16(m), _u32le(0), qs]), 1, 32)
+        assert np.array_equal(c, e)
+        f = oracle.dequant(Q5_0, np.concatenate([_fp16(d), _u32le(0xFFFFFFFF), qs]), 1, 32)
+        g = oracle.dequant(Q4_1, np.concatenate([_fp16(d), _fp16(0.0), qs]), 1, 32)
+        assert np.array_equal(f, g)
+
+
+def _q2k_block(d, dmin, sc, mn, q):
+    """256 two-bit codes; 16 (scale, min) nibble pairs. Half h, group g of 16:
+    codes at bits 2(g//2) of qs[32h + 16(g%2) + l], scale byte 8h + g."""
+    q = np.asarray(q, dtype=np.int64).reshape(2, 8, 16)
+    qs = np.zeros((2, 32), dtype=np.int64)
+    for h in range(2):
+        for g in range(8):
+            qs[h, 16 * (g % 2):16 * (g % 2) + 16] |= q[h, g] << (2 * (g // 2))
+    scales = (np.asarray(sc) | (np.asarray(mn) << 4)).astype(np.uint8)
+    return np.concatenate([scales, qs.reshape(-1).astype(np.uint8), _fp16(d), _fp16(dmin)])
+
+
+def _q3k_block(d, s6, q):
+    """256 codes in -4..3 and 16 signed scales in -32..31."""
+    q = np.asarray(q, dtype=np.int64).reshape(2, 8, 16)
+    u = np.asarray(s6, dtype=np.int64) + 32
+    sc = np.zeros(12, dtype=np.int64)
+    for i in range(16):
+        sc[i % 8] |= (u[i] & 0xF) << (0 if i < 8 else 4)
+        sc[8 + i % 4] |= (u[i] >> 4) << (2 * (i // 4))
+    qs = np.zeros((2, 32), dtype=np.int64)
+    hm = np.zeros(32, dtype=np.int64)
+    for h in range(2):
+        for g in range(8):
+            o = 16 * (g % 2)
+            qs[h, o:o + 16] |= (q[h, g] & 3) << (2 * (g // 2))
+            hm[o:o + 16] |= (q[h, g] >= 0).astype(np.int64) << (4 * h + g // 2)
+    return np.concatenate([hm.astype(np.uint8), qs.reshape(-1).astype(np.uint8), sc.astype(np.uint8), _fp16(d)])
+
+
+def _q5k_block(d, dmin, sc, mn, q):
+    """Q4_K's header and nibbles, and the fifth bits of group j of 64 at bits
+    2j (first 32) and 2j + 1 (second 32) of qh[l]."""
+    q = np.asarray(q, dtype=np.int64).reshape(4, 2, 32)
+    base = _q4k_block(d, dmin, sc, mn, (q & 0xF).reshape(-1))
+    qh = np.zeros(32, dtype=np.int64)
+    for j in range(4):
+        qh |= (q[j, 0] >> 4) << (2 * j)
+        qh |= (q[j, 1] >> 4) << (2 * j + 1)
+    return np.concatenate([base[:16], qh.astype(np.uint8), base[16:]])
+
+
+def _q6k_block(d, sc, q):
+    """256 codes in -32..31, 16 int8 scales. Half h, quarter c of 32: value
+    l's low 4 bits in nibble c//2 of ql[64h + 32(c%2) + l], high 2 bits at
+    bits 2c of qh[32h + l]."""
+    u = (np.asarray(q, dtype=np.int64) + 32).reshape(2, 4, 32)
+    ql = np.zeros((2, 64), dtype=np.int64)
+    qh = np.zeros((2, 32), dtype=np.int64)
+    for h in range(2):
+        for c in range(4):
+            ql[h, 32 * (c % 2):32 * (c % 2) + 32] |= (u[h, c] & 0xF) << (4 * (c // 2))
+            qh[h] |= (u[h, c] >> 4) << (2 * c)
+    return np.concatenate([ql.reshape(-1).astype(np.uint8), qh.reshape(-1).astype(np.uint8),
+                           np.asarray(sc, dtype=np.int8).view(np.uint8), _fp16(d)])
+
+
+def test_q2_k_hand_built_blocks(oracle):
+    rng = np.random.default_rng(6)
+    q = rng.integers(0, 4, 256)
+    sc, mn = rng.integers(0, 16, 16), rng.integers(0, 16, 16)
+    d, dmin = np.float32(np.float16(0.0625)), np.float32(np.float16(0.01))
+    y = oracle.dequant(Q2_K, _q2k_block(d, dmin, sc, mn, q), 1, 256).reshape(-1)
+    g = np.arange(256) // 16
+    want = (d * sc[g].astype(np.float32)) * q.astype(np.float32) - dmin * mn[g].astype(np.float32)
+    assert np.array_equal(y, want)
+
+
+def test_q3_k_hand_built_blocks_and_q2_k_relation(oracle):
+    rng = np.random.default_rng(7)
+    q = rng.integers(-4, 4, 256)
+    s6 = rng.integers(-32, 32, 16)
+    d = np.float32(np.float16(0.125))
+    y = oracle.dequant(Q3_K, _q3k_block(d, s6, q), 1, 256).reshape(-1)
+    g = np.arange(256) // 16
+    assert np.array_equal(y, (d * s6[g].astype(np.float32)) * q.astype(np.float32))
+    # with every hmask bit set the codes are Q2_K's 2-bit fields, and a scale
+    # of 0..15 with min 0 is Q2_K's scale byte
+    raw = _q3k_block(d, rng.integers(0, 16, 16), rng.integers(0, 4, 256))
+    raw[:32] = 0xFF
+    s = np.array([(raw[96 + i % 8] >> (0 if i < 8 else 4) & 0xF) | ((raw[104 + i % 4] >> (2 * (i // 4)) & 3) << 4)
+                  for i in range(16)]) - 32
+    q2 = np.concatenate([s.astype(np.uint8), raw[32:96], _fp16(d), _fp16(0.0)])
+    assert np.array_equal(oracle.dequant(Q3_K, raw, 1, 256), oracle.dequant(Q2_K, q2, 1, 256))
+
+
+def test_q5_k_hand_built_blocks_and_q4_k_relation(oracle):
+    rng = np.random.default_rng(8)
+    q = rng.integers(0, 32, 256)
+    sc, mn = rng.integers(0, 64, 8), rng.integers(0, 64, 8)
+    d, dmin = np.float32(np.float16(0.03125)), np.float32(np.float16(0.0078125))
+    y = oracle.dequant(Q5_K, _q5k_block(d, dmin, sc, mn, q), 1, 256).reshape(-1)
+    g = np.arange(256) // 32
+    assert np.array_equal(y, (d * sc[g].astype(np.float32)) * q.astype(np.float32) - dmin * mn[g].astype(np.float32))
+    # with no fifth bits it is Q4_K over the same header and nibbles
+    q4 = rng.integers(0, 16, 256)
+    raw = _q5k_block(d, dmin, sc, mn, q4)
+    assert not raw[16:48].any()
+    assert np.array_equal(oracle.dequant(Q5_K, raw, 1, 256),
+                          oracle.dequant(Q4_K, np.concatenate([raw[:16], raw[48:]]), 1, 256))
+
+
+def test_q6_k_hand_built_blocks(oracle):
+    rng = np.random.default_rng(9)
+    q = rng.integers(-32, 32, 256)
+    sc = rng.integers(-128, 128, 16)
+    for d in (0.001, -0.5):
+        dd = np.float32(np.float16(d))
+        y = oracle.dequant(Q6_K, _q6k_block(d, sc, q), 1, 256).reshape(-1)
+        g = np.arange(256) // 16
+        assert np.array_equal(y, (dd * sc[g].astype(np.float32)) * q.astype(np.float32))
+    # every position alone: one nonzero code walks the block
+    for pos in (0, 15, 16, 31, 32, 63, 64, 95, 96, 127, 128, 191, 224, 255):
+        qq = np.zeros(256, dtype=np.int64)
+        qq[pos] = 31
+        y = oracle.dequant(Q6_K, _q6k_block(1.0, np.ones(16), qq), 1, 256).reshape(-1)
+        assert np.flatnonzero(y).tolist() == [pos] and y[pos] == 31.0
+
+
+@pytest.mark.parametrize("wtype,bound", [
+    (F16, 5e-4), (BF16, 4e-3), (Q4_0, 0.1), (Q4_1, 0.09), (Q5_0, 0.05), (Q5_1, 0.045), (Q8_0, 0.006),
+    (Q2_K, 0.45), (Q3_K, 0.2), (Q4_K, 0.09), (Q5_K, 0.045), (Q6_K, 0.025)])
+def test_oracle_quantiser_round_trip(oracle, wtype, bound):
+    # the synthetic rows decode to the weights they came from, within the
+    # type's resolution (nrmse over normal weights)
+    n, k = 32, 512
+    w = Rng(41 + wtype).normal(n * k, 0.0, 0.02).reshape(n, k)
+    raw = oracle.quantize(wtype, w)
+    assert raw.shape == (n, oracle.row_bytes(wtype, k))
+    assert nrmse(oracle.dequant(wtype, raw, n, k), w) < bound
+
+
 # ---- the reference matmul --------------------------------------------------------
 
 def test_ref_mul_mat_integer_kat(oracle):

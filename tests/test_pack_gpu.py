@@ -161,3 +161,87 @@ def test_convert_extreme_quant_blocks(zest_gpu, oracle):
     raw = raw.reshape(n, -1)
     want = oracle.encode_rows(oracle.dequant(8, raw, n, k))
     assert np.array_equal(gpu_convert(zest_gpu, 8, raw, n, k), want)
+
+
+# ---- every GGUF weight type --------------------------------------------------------
+# The reference converts any type ggml dequantises (src/ggml-zest.cpp:1066-1072);
+# its test covers f16, q4_0 and q6_K beside q8_0 and q4_K (tests/test-mul-mat.cpp:
+# 140-156). Byte-exact against the oracle's dequantisation + encoder, on
+# quantised normal weights and on random bytes (every code, bit and scale).
+
+GGUF = {"f16": 1, "bf16": 30, "q4_0": 2, "q4_1": 3, "q5_0": 6, "q5_1": 7, "q8_0": 8,
+        "q2_K": 10, "q3_K": 11, "q4_K": 12, "q5_K": 13, "q6_K": 14}
+K_QUANTS = {10, 11, 12, 13, 14}
+# byte ranges of each block's fp16 fields (kept finite in the random blocks)
+F16_FIELDS = {2: [(0, 2)], 3: [(0, 4)], 6: [(0, 2)], 7: [(0, 4)], 8: [(0, 2)], 10: [(80, 84)],
+              11: [(108, 110)], 12: [(0, 4)], 13: [(0, 4)], 14: [(208, 210)]}
+
+
+def random_gguf(oracle, wtype: int, n: int, k: int, seed: int) -> np.ndarray:
+    """n rows of random GGUF bytes whose fp16 (bf16) fields are finite."""
+    rng = np.random.default_rng(seed)
+    rb = oracle.row_bytes(wtype, k)
+    raw = rng.integers(0, 256, (n, rb), dtype=np.uint8)
+    if wtype in (1, 30):
+        v = raw.view(np.uint16)
+        exp_mask, top = (0x7C00, 0x4000) if wtype == 1 else (0x7F80, 0x4000)
+        v[(v & exp_mask) == exp_mask] &= np.uint16(~top & 0xFFFF)
+        return raw
+    blk = 256 if wtype in K_QUANTS else 32
+    bb = rb // (k // blk)
+    b = raw.reshape(n, k // blk, bb)
+    for lo, hi in F16_FIELDS[wtype]:
+        h = rng.normal(0, 1, (n, k // blk, (hi - lo) // 2)) * np.exp2(rng.integers(-20, 8, (n, k // blk, (hi - lo) // 2)))
+        b[:, :, lo:hi] = h.astype(np.float16).view(np.uint8).reshape(n, k // blk, hi - lo)
+    return raw
+
+
+def _shapes(wtype):
+    if wtype in K_QUANTS:
+        return [(256, 512), (300, 2560), (37, 256)]
+    if wtype in (1, 30):
+        return [(256, 512), (300, 2560), (37, 200)]  # K % 64 == 8
+    return [(256, 512), (300, 2560), (37, 96)]  # K % 64 == 32: half a tile column of padding
+
+
+@pytest.mark.parametrize("name", list(GGUF))
+def test_convert_every_type_matches_oracle(zest_gpu, oracle, name):
+    wtype = GGUF[name]
+    for i, (N, K) in enumerate(_shapes(wtype)):
+        w = Rng(N + K + wtype).normal(N * K, 0.0, 0.02).reshape(N, K)
+        raw = oracle.quantize(wtype, w)
+        want = oracle.encode_rows(oracle.dequant(wtype, raw, N, K))
+        assert np.array_equal(gpu_convert(zest_gpu, wtype, raw, N, K), want), (name, N, K)
+        raw = random_gguf(oracle, wtype, N, K, seed=wtype * 100 + i)
+        want = oracle.encode_rows(oracle.dequant(wtype, raw, N, K))
+        assert np.array_equal(gpu_convert(zest_gpu, wtype, raw, N, K), want), (name, N, K, "random")
+
+
+@pytest.mark.parametrize("name", ["q4_0", "q5_1", "q3_K", "q6_K", "f16"])
+def test_convert_gu_every_type_is_the_interleaved_pair(zest_gpu, oracle, name):
+    import torch
+    wtype, F, K = GGUF[name], 96, 512
+    gate, up = (torch.from_numpy(random_gguf(oracle, wtype, F, K, seed=s)).cuda() for s in (1, 2))
+    pair = zest_gpu.convert_weight_gu(wtype, gate, up, F, K).cpu().numpy()
+    bg = zest_gpu.tiles_to_blocks(zest_gpu.convert_weight(wtype, gate, F, K).cpu().numpy(), F, K)
+    bu = zest_gpu.tiles_to_blocks(zest_gpu.convert_weight(wtype, up, F, K).cpu().numpy(), F, K)
+    bp = zest_gpu.tiles_to_blocks(pair, zest_gpu.rows_pad(2 * F), K)
+    r = np.arange(F)
+    dst = (r // 32) * 64 + r % 32
+    assert np.array_equal(bp[dst], bg) and np.array_equal(bp[dst + 32], bu)
+
+
+def test_convert_rejects_bad_rows(zest_gpu, oracle):
+    import torch
+    raw = torch.zeros(4096, dtype=torch.uint8, device="cuda")
+    with pytest.raises(RuntimeError):
+        zest_gpu.convert_weight(3, raw[2:], 16, 256)     # Q4_1 rows need 4-byte alignment
+    with pytest.raises(RuntimeError):
+        zest_gpu.convert_weight(13, raw[4:], 16, 256)    # Q5_K rows need 16
+    with pytest.raises(RuntimeError):
+        zest_gpu.convert_weight(14, raw, 4, 128)         # Q6_K: K % 256 != 0
+    with pytest.raises(RuntimeError):
+        zest_gpu.convert_weight(2, raw, 4, 48)           # Q4_0: K % 32 != 0
+    with pytest.raises(RuntimeError):
+        zest_gpu.convert_weight(15, raw, 4, 256)         # Q8_K: no converter
+    torch.cuda.synchronize()
