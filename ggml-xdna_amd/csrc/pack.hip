@@ -155,300 +155,286 @@ __global__ __launch_bounds__(256) void convert_q8_0_kernel(const uint8_t * __res
     *reinterpret_cast<uint32_t *>(tile + ZEST_TILE_MANT + rr * 8 + half * 4) = ex;
 }
 
-// Encodes 64 consecutive values of one row (a tile row: 8 blocks) and stores
-// them at row dr of tile column kc: 64 mantissa bytes (four 16-byte stores)
-// and the 8 exponent bytes (one 8-byte store).
-__device__ inline void store_tile_row(uint8_t * dst, int64_t R_pad, int64_t dr, int64_t kc, const float v[64]) {
-    uint4 m[4];
-    uint32_t e[8];
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-        e[2 * u] = encode8(v + 16 * u, m[u].x, m[u].y);
-        e[2 * u + 1] = encode8(v + 16 * u + 8, m[u].z, m[u].w);
-    }
-    uint8_t * tile = dst + zest_tile_offset(dr / ZEST_TILE_ROWS, kc, R_pad);
-    const int64_t rr = dr % ZEST_TILE_ROWS;
-    uint4 * mp = reinterpret_cast<uint4 *>(tile + rr * ZEST_TILE_K);
-#pragma unroll
-    for (int u = 0; u < 4; u++) mp[u] = m[u];
-    *reinterpret_cast<uint2 *>(tile + ZEST_TILE_MANT + rr * 8) =
-        make_uint2(e[0] | (e[1] << 8) | (e[2] << 16) | (e[3] << 24), e[4] | (e[5] << 8) | (e[6] << 16) | (e[7] << 24));
-}
-
-// Q4_K: 144-byte super-blocks of 256: fp16 d, fp16 dmin, 12 bytes of 6-bit
-// (scale, min) pairs, 128 bytes of nibbles. Sub-block s (0..7) is 32 values:
-// the low (s even) or high (s odd) nibbles of qs[32*(s/2) ..+32), with pair s:
-// y = (d*sc)*q - dmin*m. The products are exact in fp32, so the one rounding
-// is the subtraction's and fma gives the same float. One thread per quarter
-// super-block: sub-blocks 2p and 2p+1, the two nibbles of the same 32 bytes,
-// i.e. 64 consecutive values, one tile row. Three aligned 16-byte loads (the
-// 16-byte header; the 32 nibble bytes). Workgroup: 16 rows x 4 super-blocks.
-__global__ __launch_bounds__(256) void convert_q4_k_kernel(const uint8_t * __restrict__ raw, int64_t N, int64_t K,
-                                                           uint8_t * __restrict__ dst, int64_t R_pad, int64_t K_pad,
-                                                           int64_t R_src, int gu) {
-    const int t = threadIdx.x, p = t & 3;
-    const int64_t r = (int64_t) blockIdx.y * ZEST_TILE_ROWS + (t >> 4);
-    const int64_t sb = (int64_t) blockIdx.x * 4 + ((t >> 2) & 3);
-    const int64_t col = sb * 256 + p * 64;
-    if (col >= K_pad || r >= R_src) return;
-    float v[64];
-    if (r < N && col < K) {
-        const uint8_t * blk = raw + r * (K / 256 * 144) + sb * 144;
-        const uint4 hdr = *reinterpret_cast<const uint4 *>(blk);
-        const uint4 qa = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * p);
-        const uint4 qb = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * p);
-        const float d = half_to_float((uint16_t) (hdr.x & 0xffff)), dmin = half_to_float((uint16_t) (hdr.x >> 16));
-        const uint32_t scw[3] = {hdr.y, hdr.z, hdr.w};
-        auto sc = [&](int i) { return (scw[i >> 2] >> ((i & 3) * 8)) & 0xffu; };
-        const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int s = 2 * p + h;
-            uint32_t scv, mv;
-            if (s < 4) {
-                scv = sc(s) & 63;
-                mv = sc(s + 4) & 63;
-            } else {
-                scv = (sc(s + 4) & 0xF) | ((sc(s - 4) >> 6) << 4);
-                mv = (sc(s + 4) >> 4) | ((sc(s) >> 6) << 4);
-            }
-            const float d1 = d * (float) scv, m1f = dmin * (float) mv;
-#pragma unroll
-            for (int i = 0; i < 32; i++) {
-                const uint32_t nib = (w[i >> 2] >> ((i & 3) * 8 + h * 4)) & 0xF;
-                v[32 * h + i] = fmaf(d1, (float) nib, -m1f);
-            }
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 64; i++) v[i] = 0.0f;
-    }
-    store_tile_row(dst, R_pad, dst_row(r, gu), col / ZEST_TILE_K, v);
-}
-
-// ---- the other GGUF types ------------------------------------------------------
-// One thread per 64 consecutive values of a row (one tile row of one tile
-// column), dequantised as ggml's to_float does: every product below is exact
-// in fp32 (fp16 scale x small integers), so where the format adds an offset
-// the one rounding is the addition's and fmaf gives the same float.
+// ---- every GGUF type: one thread per half tile row ----------------------------
+// One thread dequantises 32 consecutive values of a row (col % 32 == 0) as
+// ggml's to_float does and encodes them (four bfp16 blocks). Every product
+// below is exact in fp32 (an fp16 scale times integers of at most 8 bits,
+// or a 6-bit scale product times at most 6 bits), so each form written as
+// fma(u, d, c) with an offset code u = q + bias gives the reference's value:
+// where the reference computes d*q exactly (Q4_0, Q5_0, Q8_0, Q3_K, Q6_K),
+// the fma's exact result is representable and no rounding happens; where it
+// adds an offset after an exact product (Q4_1, Q5_1, Q2_K, Q4_K, Q5_K), the
+// one rounding is the same addition's.
+//
+// Codes are assembled four at a time, one per byte of a 32-bit word, so
+// each value costs one byte-to-float convert (v_cvt_f32_ubyte0..3) and one
+// fma. `finite` says the block's scale fields are finite, so its values hold
+// no NaN and the encoder may take the exponent from the largest magnitude.
 
 __device__ inline uint32_t ld16(const uint8_t * p) { return *reinterpret_cast<const uint16_t *>(p); }  // 2-aligned
 __device__ inline uint32_t ld32(const uint8_t * p) { return *reinterpret_cast<const uint32_t *>(p); }  // 4-aligned
 __device__ inline uint32_t ld32h(const uint8_t * p) { return ld16(p) | (ld16(p + 2) << 16); }          // 2-aligned
 __device__ inline uint32_t byte_of(const uint32_t * w, int i) { return (w[i >> 2] >> ((i & 3) * 8)) & 0xffu; }
 
-// 32-value blocks: byte j of qs holds value j (low nibble) and j + 16 (high);
-// bit j of the 32-bit qh is value j's fifth bit. SIGNED: q - 2^(bits-1)
-// times d; else q*d + m.
-template <int BITS, bool SIGNED>
-__device__ inline void dq_block32(float d, float m, uint32_t qh, const uint32_t qs[4], float * v) {
-#pragma unroll
-    for (int j = 0; j < 16; j++) {
-        const uint32_t b = byte_of(qs, j);
-        int lo = (int) (b & 0xF), hi = (int) (b >> 4);
-        if (BITS == 5) {
-            lo |= (int) ((qh >> j) & 1u) << 4;
-            hi |= (int) ((qh >> (j + 16)) & 1u) << 4;
-        }
-        if (SIGNED) {
-            v[j] = (float) (lo - (1 << (BITS - 1))) * d;
-            v[j + 16] = (float) (hi - (1 << (BITS - 1))) * d;
-        } else {
-            v[j] = fmaf((float) lo, d, m);
-            v[j + 16] = fmaf((float) hi, d, m);
-        }
-    }
+// v[0..3] = fma(byte k of u, d, c). The empty asm hides how u was masked,
+// so each byte converts with one v_cvt_f32_ubyte<k> (the compiler would
+// otherwise fold the mask into a bit-field extract plus a convert).
+__device__ inline void fma_bytes(uint32_t u, float d, float c, float * v) {
+    asm("" : "+v"(u));
+    v[0] = fmaf((float) (u & 0xffu), d, c);
+    v[1] = fmaf((float) ((u >> 8) & 0xffu), d, c);
+    v[2] = fmaf((float) ((u >> 16) & 0xffu), d, c);
+    v[3] = fmaf((float) (u >> 24), d, c);
 }
 
+// bits 0..3 of x -> bit 0 of bytes 0..3 (the four terms x << 7k do not overlap)
+__device__ inline uint32_t spread4(uint32_t x) { return ((x & 0xFu) * 0x00204081u) & 0x01010101u; }
+
+__device__ inline bool finite(float x) { return __builtin_isfinite(x); }
+
+// 32-value blocks: byte j of qs holds value j (low nibble) and j + 16 (high);
+// bit j of the little-endian 32-bit qh is value j's fifth bit.
 template <int TYPE>
-__device__ inline void dq_32(const uint8_t * p, float * v) {
-    uint32_t qs[4];
+__device__ inline bool dq_32(const uint8_t * p, float * v) {
+    constexpr bool Q5 = TYPE == ZEST_TYPE_Q5_0 || TYPE == ZEST_TYPE_Q5_1;
+    constexpr bool AFFINE = TYPE == ZEST_TYPE_Q4_1 || TYPE == ZEST_TYPE_Q5_1;  // y = d*q + m
+    float d, c;
+    uint32_t qh = 0, qs[4];
     if (TYPE == ZEST_TYPE_Q4_0) {  // d, qs[16]: 18 bytes
+        d = half_to_float((uint16_t) ld16(p));
 #pragma unroll
         for (int i = 0; i < 4; i++) qs[i] = ld32h(p + 2 + 4 * i);
-        dq_block32<4, true>(half_to_float((uint16_t) ld16(p)), 0.0f, 0, qs, v);
     } else if (TYPE == ZEST_TYPE_Q4_1) {  // d, m, qs[16]: 20 bytes
         const uint32_t h = ld32(p);
+        d = half_to_float((uint16_t) (h & 0xffff));
+        c = half_to_float((uint16_t) (h >> 16));
 #pragma unroll
         for (int i = 0; i < 4; i++) qs[i] = ld32(p + 4 + 4 * i);
-        dq_block32<4, false>(half_to_float((uint16_t) (h & 0xffff)), half_to_float((uint16_t) (h >> 16)), 0, qs, v);
     } else if (TYPE == ZEST_TYPE_Q5_0) {  // d, qh[4], qs[16]: 22 bytes
+        d = half_to_float((uint16_t) ld16(p));
+        qh = ld32h(p + 2);
 #pragma unroll
         for (int i = 0; i < 4; i++) qs[i] = ld32h(p + 6 + 4 * i);
-        dq_block32<5, true>(half_to_float((uint16_t) ld16(p)), 0.0f, ld32h(p + 2), qs, v);
     } else {  // Q5_1: d, m, qh[4], qs[16]: 24 bytes
         const uint32_t h = ld32(p);
+        d = half_to_float((uint16_t) (h & 0xffff));
+        c = half_to_float((uint16_t) (h >> 16));
+        qh = ld32(p + 4);
 #pragma unroll
         for (int i = 0; i < 4; i++) qs[i] = ld32(p + 8 + 4 * i);
-        dq_block32<5, false>(half_to_float((uint16_t) (h & 0xffff)), half_to_float((uint16_t) (h >> 16)), ld32(p + 4),
-                             qs, v);
     }
+    if (!AFFINE) c = (Q5 ? -16.0f : -8.0f) * d;  // signed codes: y = d*(u - bias)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint32_t lo = qs[i] & 0x0F0F0F0Fu, hi = (qs[i] >> 4) & 0x0F0F0F0Fu;
+        if (Q5) {
+            lo |= spread4(qh >> (4 * i)) << 4;
+            hi |= spread4(qh >> (16 + 4 * i)) << 4;
+        }
+        fma_bytes(lo, d, c, v + 4 * i);
+        fma_bytes(hi, d, c, v + 16 + 4 * i);
+    }
+    return AFFINE ? finite(d) && finite(c) : finite(d);
 }
 
-// Values [col, col + 64) of one row (col % 64 == 0, col < K).
+// Values [col, col + 32) of one row (col % 32 == 0, col < K): half a tile
+// row. Returns whether they are NaN-free by construction.
 template <int TYPE>
-__device__ inline void dq_64(const uint8_t * row, int64_t col, int64_t K, float v[64]) {
+__device__ inline bool dq_half(const uint8_t * row, int64_t col, int64_t K, float v[32]) {
     if (TYPE == ZEST_TYPE_F16 || TYPE == ZEST_TYPE_BF16) {
-        // K % 8 == 0 but maybe not % 64: 8-value chunks past K read as zero
+        // K % 8 == 0 but maybe not % 32: 8-value chunks past K read as zero
         const uint4 * p = reinterpret_cast<const uint4 *>(row + col * 2);
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
+        for (int i = 0; i < 4; i++) {
             const uint4 q = col + 8 * i < K ? p[i] : make_uint4(0, 0, 0, 0);
             const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                const uint32_t lo = w[k] & 0xffff, hi = w[k] >> 16;
                 if (TYPE == ZEST_TYPE_F16) {
-                    v[8 * i + 2 * k] = half_to_float((uint16_t) lo);
-                    v[8 * i + 2 * k + 1] = half_to_float((uint16_t) hi);
+                    v[8 * i + 2 * k] = half_to_float((uint16_t) (w[k] & 0xffff));
+                    v[8 * i + 2 * k + 1] = half_to_float((uint16_t) (w[k] >> 16));
                 } else {
-                    v[8 * i + 2 * k] = __uint_as_float(lo << 16);
-                    v[8 * i + 2 * k + 1] = __uint_as_float(hi << 16);
+                    v[8 * i + 2 * k] = __uint_as_float(w[k] << 16);
+                    v[8 * i + 2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
                 }
             }
         }
+        return false;  // the values are the file's own: NaN is possible
     } else if (TYPE == ZEST_TYPE_Q4_0 || TYPE == ZEST_TYPE_Q4_1 || TYPE == ZEST_TYPE_Q5_0 ||
                TYPE == ZEST_TYPE_Q5_1) {
         constexpr int B = TYPE == ZEST_TYPE_Q4_0 ? 18 : TYPE == ZEST_TYPE_Q4_1 ? 20 : TYPE == ZEST_TYPE_Q5_0 ? 22 : 24;
-        const uint8_t * p = row + (col / 32) * B;
-        dq_32<TYPE>(p, v);
-        if (col + 32 < K) {
-            dq_32<TYPE>(p + B, v + 32);
+        return dq_32<TYPE>(row + (col / 32) * B, v);
+    } else if (TYPE == ZEST_TYPE_Q8_0) {
+        // d, qs[32]: 34 bytes; y = d*q = d*(u - 128) with u = q ^ 0x80
+        const uint8_t * p = row + (col / 32) * 34;
+        const float d = half_to_float((uint16_t) ld16(p)), c = -128.0f * d;
+#pragma unroll
+        for (int i = 0; i < 8; i++) fma_bytes(ld32h(p + 2 + 4 * i) ^ 0x80808080u, d, c, v + 4 * i);
+        return finite(d);
+    } else if (TYPE == ZEST_TYPE_Q2_K || TYPE == ZEST_TYPE_Q3_K) {
+        // Q2_K: scales[16], qs[64], d, dmin (84 bytes); Q3_K: hmask[32],
+        // qs[64], scales[12], d (110 bytes). Eighth e8 = half h, shift 2j
+        // (j = e8 % 4): groups g = 2j (qs[32h + l], l < 16) and 2j + 1
+        // (qs[32h + 16 + l]), scale 8h + g.
+        //   Q2_K: scale byte s: y = (d*(s & 15))*q - dmin*(s >> 4)
+        //   Q3_K: q = field - 4 where bit 4h + j of hmask[16(g%2) + l] is
+        //         clear; 6-bit signed scale: y = (d*scale)*q = dl*(u - 4)
+        //         with u = field | hbit << 2
+        const int64_t sb = col / 256;
+        const int e8 = (int) ((col % 256) / 32), h = e8 >> 2, j = e8 & 3;
+        const bool q3 = TYPE == ZEST_TYPE_Q3_K;
+        const uint8_t * p = row + sb * (q3 ? 110 : 84);
+        const uint8_t * qs = p + (q3 ? 32 : 16) + 32 * h;
+        float dl[2], c[2];
+        bool ok;
+        if (!q3) {
+            const uint32_t dd = ld32(p + 80), sw = ld16(p + 8 * h + 2 * j);
+            const float d = half_to_float((uint16_t) (dd & 0xffff)), dmin = half_to_float((uint16_t) (dd >> 16));
+#pragma unroll
+            for (int gi = 0; gi < 2; gi++) {
+                const uint32_t sc = (sw >> (8 * gi)) & 0xffu;
+                dl[gi] = d * (float) (sc & 0xF);
+                c[gi] = -(dmin * (float) (sc >> 4));
+            }
+            ok = finite(d) && finite(dmin);
         } else {
+            const float d = half_to_float((uint16_t) ld16(p + 108));
+            uint32_t sc[3];
 #pragma unroll
-            for (int i = 32; i < 64; i++) v[i] = 0.0f;
+            for (int i = 0; i < 3; i++) sc[i] = ld32h(p + 96 + 4 * i);
+#pragma unroll
+            for (int gi = 0; gi < 2; gi++) {
+                const int si = 8 * h + 2 * j + gi;
+                const int lo = si < 8 ? (int) (byte_of(sc, si) & 0xF) : (int) (byte_of(sc, si - 8) >> 4);
+                const int hi = (int) ((byte_of(sc, 8 + (si & 3)) >> (2 * (si >> 2))) & 3u);
+                dl[gi] = d * (float) ((lo | (hi << 4)) - 32);
+                c[gi] = -4.0f * dl[gi];
+            }
+            ok = finite(d);
         }
-    } else if (TYPE == ZEST_TYPE_Q2_K) {
-        // scales[16], qs[64], d, dmin: 84 bytes. Quarter c4 = half h, groups
-        // 4c..4c+3 of 16 (c = c4 % 2); group g takes 2-bit field g/2 of
-        // qs[32h + 16(g%2) + l], scale byte 8h + g: y = (d*(s&15))*q - dmin*(s>>4)
-        const int64_t sb = col / 256;
-        const int c4 = (int) ((col % 256) / 64), h = c4 >> 1, c = c4 & 1;
-        const uint8_t * p = row + sb * 84;
-        const uint32_t dd = ld32(p + 80), sw = ld32(p + 8 * h + 4 * c);
-        const float d = half_to_float((uint16_t) (dd & 0xffff)), dmin = half_to_float((uint16_t) (dd >> 16));
-        uint32_t q[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) q[i] = ld32(p + 16 + 32 * h + 4 * i);
-#pragma unroll
-        for (int gi = 0; gi < 4; gi++) {
-            const int g = 4 * c + gi, sh = 2 * (g >> 1);
-            const uint32_t s = (sw >> (8 * gi)) & 0xffu;
-            const float dl = d * (float) (s & 0xF), ml = dmin * (float) (s >> 4);
-#pragma unroll
-            for (int l = 0; l < 16; l++)
-                v[16 * gi + l] = fmaf(dl, (float) ((byte_of(q, 16 * (gi & 1) + l) >> sh) & 3u), -ml);
-        }
-    } else if (TYPE == ZEST_TYPE_Q3_K) {
-        // hmask[32], qs[64], scales[12], d: 110 bytes. As Q2_K's fields, with
-        // q = field - 4 where bit 4h + g/2 of hmask[16(g%2) + l] is clear, and
-        // 6-bit signed scales: y = (d*scale)*q, exact.
-        const int64_t sb = col / 256;
-        const int c4 = (int) ((col % 256) / 64), h = c4 >> 1, c = c4 & 1;
-        const uint8_t * p = row + sb * 110;
-        const float d = half_to_float((uint16_t) ld16(p + 108));
-        uint32_t hm[8], q[8], sc[3];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            hm[i] = ld32h(p + 4 * i);
-            q[i] = ld32h(p + 32 + 32 * h + 4 * i);
+            uint32_t u = (ld32h(qs + 4 * i) >> (2 * j)) & 0x03030303u;
+            if (q3) u |= ((ld32h(p + 4 * i) >> (4 * h + j)) & 0x01010101u) << 2;
+            fma_bytes(u, dl[i >> 2], c[i >> 2], v + 4 * i);
         }
-#pragma unroll
-        for (int i = 0; i < 3; i++) sc[i] = ld32h(p + 96 + 4 * i);
-#pragma unroll
-        for (int gi = 0; gi < 4; gi++) {
-            const int g = 4 * c + gi, j = g >> 1, si = 8 * h + g;
-            const int lo = si < 8 ? (int) (byte_of(sc, si) & 0xF) : (int) (byte_of(sc, si - 8) >> 4);
-            const int hi = (int) ((byte_of(sc, 8 + (si & 3)) >> (2 * (si >> 2))) & 3u);
-            const float dl = d * (float) ((lo | (hi << 4)) - 32);
-#pragma unroll
-            for (int l = 0; l < 16; l++) {
-                const int o = 16 * (gi & 1) + l;
-                const int f = (int) ((byte_of(q, o) >> (2 * j)) & 3u) - ((byte_of(hm, o) >> (4 * h + j)) & 1u ? 0 : 4);
-                v[16 * gi + l] = dl * (float) f;
-            }
-        }
-    } else if (TYPE == ZEST_TYPE_Q5_K) {
-        // d, dmin, scales[12], qh[32], qs[128]: 176 bytes. Group j of 64:
-        // Q4_K's nibbles of qs[32j..32j+32) and pairs 2j, 2j+1, fifth bits
-        // 2j (low nibbles) and 2j + 1 (high) of qh[l].
+        return ok;
+    } else if (TYPE == ZEST_TYPE_Q4_K || TYPE == ZEST_TYPE_Q5_K) {
+        // Q4_K: d, dmin, scales[12], qs[128] (144 bytes); Q5_K adds qh[32]
+        // before qs (176 bytes). Sub-block s (eighth): nibble s % 2 of
+        // qs[32(s/2) + l], fifth bit s of qh[l], 6-bit pair s:
+        // y = (d*sc)*q - dmin*m.
+        constexpr int BB = TYPE == ZEST_TYPE_Q4_K ? 144 : 176, QS = TYPE == ZEST_TYPE_Q4_K ? 16 : 48;
         const int64_t sb = col / 256;
-        const int jq = (int) ((col % 256) / 64);
-        const uint8_t * p = row + sb * 176;
+        const int s = (int) ((col % 256) / 32);
+        const uint8_t * p = row + sb * BB;
         const uint4 hdr = *reinterpret_cast<const uint4 *>(p);
-        const uint4 h0 = *reinterpret_cast<const uint4 *>(p + 16), h1 = *reinterpret_cast<const uint4 *>(p + 32);
-        const uint4 qa = *reinterpret_cast<const uint4 *>(p + 48 + 32 * jq);
-        const uint4 qb = *reinterpret_cast<const uint4 *>(p + 64 + 32 * jq);
+        const uint4 qa = *reinterpret_cast<const uint4 *>(p + QS + 32 * (s >> 1));
+        const uint4 qb = *reinterpret_cast<const uint4 *>(p + QS + 16 + 32 * (s >> 1));
         const float d = half_to_float((uint16_t) (hdr.x & 0xffff)), dmin = half_to_float((uint16_t) (hdr.x >> 16));
         const uint32_t scw[3] = {hdr.y, hdr.z, hdr.w};
-        const uint32_t qh[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
-        const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-#pragma unroll
-        for (int e = 0; e < 2; e++) {
-            const int s = 2 * jq + e;
-            uint32_t scv, mv;
-            if (s < 4) {
-                scv = byte_of(scw, s) & 63;
-                mv = byte_of(scw, s + 4) & 63;
-            } else {
-                scv = (byte_of(scw, s + 4) & 0xF) | ((byte_of(scw, s - 4) >> 6) << 4);
-                mv = (byte_of(scw, s + 4) >> 4) | ((byte_of(scw, s) >> 6) << 4);
-            }
-            const float d1 = d * (float) scv, m1 = dmin * (float) mv;
-#pragma unroll
-            for (int l = 0; l < 32; l++) {
-                const uint32_t qv = ((byte_of(w, l) >> (4 * e)) & 0xF) | (((byte_of(qh, l) >> s) & 1u) << 4);
-                v[32 * e + l] = fmaf(d1, (float) qv, -m1);
-            }
+        uint32_t scv, mv;
+        if (s < 4) {
+            scv = byte_of(scw, s) & 63;
+            mv = byte_of(scw, s + 4) & 63;
+        } else {
+            scv = (byte_of(scw, s + 4) & 0xF) | ((byte_of(scw, s - 4) >> 6) << 4);
+            mv = (byte_of(scw, s + 4) >> 4) | ((byte_of(scw, s) >> 6) << 4);
         }
+        const float d1 = d * (float) scv, c = -(dmin * (float) mv);
+        const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        uint32_t qh[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (TYPE == ZEST_TYPE_Q5_K) {
+            const uint4 h0 = *reinterpret_cast<const uint4 *>(p + 16), h1 = *reinterpret_cast<const uint4 *>(p + 32);
+            const uint32_t hv[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) qh[i] = hv[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            uint32_t u = (w[i] >> (4 * (s & 1))) & 0x0F0F0F0Fu;
+            if (TYPE == ZEST_TYPE_Q5_K) u |= ((qh[i] >> s) & 0x01010101u) << 4;
+            fma_bytes(u, d1, c, v + 4 * i);
+        }
+        return finite(d) && finite(dmin);
     } else {  // Q6_K
-        // ql[128], qh[64], int8 scales[16], d: 210 bytes. Half h, quarters
-        // c = 2c2 + e: value l's low 4 bits are nibble c2 of
-        // ql[64h + 32e + l], its high 2 bits bits 2c of qh[32h + l]; minus
-        // 32, times d*scales[8h + 2c + l/16] (products exact in fp32).
+        // ql[128], qh[64], int8 scales[16], d: 210 bytes. Eighth e8 = half
+        // h, quarter c = e8 % 4: value l's low 4 bits are nibble c/2 of
+        // ql[64h + 32(c%2) + l], its high 2 bits bits 2c of qh[32h + l];
+        // y = (d*scales[8h + 2c + l/16])*(u - 32).
         const int64_t sb = col / 256;
-        const int c4 = (int) ((col % 256) / 64), h = c4 >> 1, c2 = c4 & 1;
+        const int e8 = (int) ((col % 256) / 32), h = e8 >> 2, c = e8 & 3;
         const uint8_t * p = row + sb * 210;
         const float d = half_to_float((uint16_t) ld16(p + 208));
-        const uint32_t sw = ld32h(p + 192 + 8 * h + 4 * c2);
-        uint32_t ql[16], qh[8];
+        const uint32_t sw = ld16(p + 192 + 8 * h + 2 * c);
+        const float ds[2] = {d * (float) (int8_t) (sw & 0xffu), d * (float) (int8_t) (sw >> 8)};
 #pragma unroll
-        for (int i = 0; i < 16; i++) ql[i] = ld32h(p + 64 * h + 4 * i);
-#pragma unroll
-        for (int i = 0; i < 8; i++) qh[i] = ld32h(p + 128 + 32 * h + 4 * i);
-#pragma unroll
-        for (int e = 0; e < 2; e++) {
-            const int cq = 2 * c2 + e;
-#pragma unroll
-            for (int l = 0; l < 32; l++) {
-                const int lo = (int) ((byte_of(ql, 32 * e + l) >> (4 * c2)) & 0xF);
-                const int hi = (int) ((byte_of(qh, l) >> (2 * cq)) & 3u);
-                const int8_t s = (int8_t) ((sw >> (8 * (2 * e + l / 16))) & 0xffu);
-                v[32 * e + l] = (d * (float) s) * (float) ((lo | (hi << 4)) - 32);
-            }
+        for (int i = 0; i < 8; i++) {
+            const uint32_t lo = (ld32h(p + 64 * h + 32 * (c & 1) + 4 * i) >> (4 * (c >> 1))) & 0x0F0F0F0Fu;
+            const uint32_t hi = (ld32h(p + 128 + 32 * h + 4 * i) >> (2 * c)) & 0x03030303u;
+            fma_bytes(lo | (hi << 4), ds[i >> 2], -32.0f * ds[i >> 2], v + 4 * i);
         }
+        return finite(d);
     }
 }
 
-// Workgroup: 16 rows x 16 tile columns (1024 values of each row); lane t
-// takes row t/16 and tile column t%16, so the 16 lanes of a row read one
-// contiguous run of its GGUF bytes.
+// Encodes 32 consecutive values of one row (half a tile row: 4 blocks):
+// 32 mantissa bytes and the 4 exponent bytes.
+__device__ inline void encode_half_row(const float v[32], bool no_nan, uint4 & m0, uint4 & m1, uint32_t & ex) {
+    uint32_t e[4];
+    if (no_nan) {
+        e[0] = zest::encode8_no_nan(v, m0.x, m0.y);
+        e[1] = zest::encode8_no_nan(v + 8, m0.z, m0.w);
+        e[2] = zest::encode8_no_nan(v + 16, m1.x, m1.y);
+        e[3] = zest::encode8_no_nan(v + 24, m1.z, m1.w);
+    } else {
+        e[0] = encode8(v, m0.x, m0.y);
+        e[1] = encode8(v + 8, m0.z, m0.w);
+        e[2] = encode8(v + 16, m1.x, m1.y);
+        e[3] = encode8(v + 24, m1.z, m1.w);
+    }
+    ex = e[0] | (e[1] << 8) | (e[2] << 16) | (e[3] << 24);
+}
+
+// Workgroup: 8 rows x 32 half tile rows = the 8-row halves of 16 tiles.
+// Lane t dequantises and encodes row t/32, half t%32 (the 32 lanes of a row
+// read one contiguous run of its GGUF bytes) into LDS, laid out as the
+// tiles' own bytes: per tile 512 mantissa bytes (8 rows of 64) then 64
+// exponent bytes. The workgroup then stores each tile's two runs with
+// 16-byte stores in which consecutive lanes write consecutive bytes.
 template <int TYPE>
 __global__ __launch_bounds__(256) void convert_kernel(const uint8_t * __restrict__ raw, size_t row_bytes, int64_t N,
                                                       int64_t K, uint8_t * __restrict__ dst, int64_t R_pad,
                                                       int64_t K_pad, int64_t R_src, int gu) {
-    const int t = threadIdx.x;
-    const int64_t r = (int64_t) blockIdx.y * ZEST_TILE_ROWS + (t >> 4);
-    const int64_t kc = (int64_t) blockIdx.x * 16 + (t & 15), col = kc * ZEST_TILE_K;
-    if (col >= K_pad || r >= R_src) return;
-    float v[64];
-    if (r < N && col < K) {
-        dq_64<TYPE>(raw + r * (int64_t) row_bytes, col, K, v);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 64; i++) v[i] = 0.0f;
+    constexpr int TB = 8 * ZEST_TILE_K + 8 * 8;  // one tile's 8 rows: 576 bytes
+    __shared__ uint4 stage[16 * TB / 16];
+    uint8_t * sb = reinterpret_cast<uint8_t *>(stage);
+    const int t = threadIdx.x, rl = t >> 5, hl = t & 31;
+    const int64_t r = (int64_t) blockIdx.y * 8 + rl;
+    const int64_t col = ((int64_t) blockIdx.x * 32 + hl) * 32;
+    uint4 m0 = make_uint4(0, 0, 0, 0), m1 = m0;
+    uint32_t ex = 0;
+    if (r < N && col < K) {  // else padding: zero blocks (exponent 0, mantissas 0)
+        float v[32];
+        const bool no_nan = dq_half<TYPE>(raw + r * (int64_t) row_bytes, col, K, v);
+        encode_half_row(v, no_nan, m0, m1, ex);
     }
-    store_tile_row(dst, R_pad, dst_row(r, gu), kc, v);
+    const int j = hl >> 1, hf = hl & 1;
+    uint4 * ms = reinterpret_cast<uint4 *>(sb + j * TB + rl * ZEST_TILE_K + hf * 32);
+    ms[0] = m0;
+    ms[1] = m1;
+    *reinterpret_cast<uint32_t *>(sb + j * TB + 8 * ZEST_TILE_K + rl * 8 + hf * 4) = ex;
+    __syncthreads();
+    // the 8-row group stays whole in the destination (dst_row keeps 8-row runs)
+    const int64_t dr0 = dst_row((int64_t) blockIdx.y * 8, gu), rt = dr0 / ZEST_TILE_ROWS, rr0 = dr0 % ZEST_TILE_ROWS;
+    const int64_t kc0 = (int64_t) blockIdx.x * 16;
+    const int ntiles = (int) min((int64_t) 16, K_pad / ZEST_TILE_K - kc0);
+    for (int c = t; c < ntiles * (TB / 16); c += 256) {
+        const int tj = c / (TB / 16), q = c % (TB / 16);
+        uint8_t * tile = dst + zest_tile_offset(rt, kc0 + tj, R_pad);
+        const int64_t off = q < 32 ? rr0 * ZEST_TILE_K + q * 16 : ZEST_TILE_MANT + rr0 * 8 + (q - 32) * 16;
+        *reinterpret_cast<uint4 *>(tile + off) = stage[c];
+    }
 }
 
 bool aligned(const void * p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
@@ -557,14 +543,6 @@ static int convert(int type, const void * raw, int64_t N, int64_t K, void * dst,
                                R_pad, K_pad, R_src, gu);
             return zest::check_launch(name);
         }
-        case ZEST_TYPE_Q4_K: {
-            ZEST_REQUIRE(K % 256 == 0, "%s: Q4_K needs K %% 256 == 0 (K=%lld)", name, (long long) K);
-            ZEST_REQUIRE(aligned(raw, 16), "%s: Q4_K rows must be 16-byte aligned", name);
-            const dim3 grid((unsigned) ((K_pad / 256 + 3) / 4), (unsigned) (R_src / ZEST_TILE_ROWS));
-            hipLaunchKernelGGL(convert_q4_k_kernel, grid, dim3(256), 0, s, (const uint8_t *) raw, N, K, (uint8_t *) dst,
-                               R_pad, K_pad, R_src, gu);
-            return zest::check_launch(name);
-        }
         default: break;
     }
     const size_t rb = zest_raw_row_bytes(type, K);
@@ -576,7 +554,7 @@ static int convert(int type, const void * raw, int64_t N, int64_t K, void * dst,
     }
     ZEST_REQUIRE(aligned(raw, row_align(type)), "%s: type %d rows must be %zu-byte aligned", name, type,
                  row_align(type));
-    const dim3 grid((unsigned) ((K_pad / ZEST_TILE_K + 15) / 16), (unsigned) (R_src / ZEST_TILE_ROWS));
+    const dim3 grid((unsigned) ((K_pad / 32 + 31) / 32), (unsigned) (R_src / 8));
     const uint8_t * r8 = (const uint8_t *) raw;
     uint8_t * d8 = (uint8_t *) dst;
 #define ZEST_CONVERT(T)                                                                                         \
@@ -591,6 +569,7 @@ static int convert(int type, const void * raw, int64_t N, int64_t K, void * dst,
         ZEST_CONVERT(ZEST_TYPE_Q5_1);
         ZEST_CONVERT(ZEST_TYPE_Q2_K);
         ZEST_CONVERT(ZEST_TYPE_Q3_K);
+        ZEST_CONVERT(ZEST_TYPE_Q4_K);
         ZEST_CONVERT(ZEST_TYPE_Q5_K);
         ZEST_CONVERT(ZEST_TYPE_Q6_K);
         default: return zest::fail(ZEST_E_UNSUPPORTED, "%s: weight type %d has no converter", name, type);

@@ -13,13 +13,35 @@ namespace zest {
 // One block of eight floats -> exponent byte (returned) and eight mantissa
 // bytes (m0 = bytes 0..3, m1 = bytes 4..7). The reference's arithmetic
 // (src/npu/bfp16_pack.cpp:85-127): e = the largest biased exponent field;
-// q = RNE(x * 2^(133 - e)) saturated to [-128, 127]. ldexp is exact here
-// (|x * 2^(133-e)| < 128, and anything it would round in underflow is below
-// one half), rint rounds to nearest even, and med3 saturates.
-__device__ inline uint32_t encode8(const float v[8], uint32_t & m0, uint32_t & m1) {
-    uint32_t e = 0;
+// q = RNE(x * 2^(133 - e)) saturated to [-128, 127].
+//
+// For e in 6..254 (every finite block but the tiniest) 2^(133-e) is a normal
+// float s, and one fma computes x*s exactly and adds 1.5 * 2^23, whose
+// binade has ulp 1: the sum is 1.5 * 2^23 + q with q = RNE(x*s) (|x*s| < 128,
+// so it stays in the binade), and q's two's-complement byte is the sum's low
+// byte (1.5 * 2^23 has a zero low byte). med3 on the sum saturates q to
+// [-128, 127]; v_perm gathers the low bytes. Three VALU ops per value.
+// Other blocks (zeros and subnormals, infinities, NaN) take the direct form:
+// ldexp (exact: |x * 2^(133-e)| < 128, and anything it would round in
+// underflow is below one half), rint to nearest even, med3.
+__device__ inline uint32_t lo_bytes4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    const uint32_t ab = __builtin_amdgcn_perm(b, a, 0x0c0c0400u), cd = __builtin_amdgcn_perm(d, c, 0x0c0c0400u);
+    return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
+}
+
+// Mantissas of a block whose exponent byte e is known.
+__device__ inline void encode8_mant(const float v[8], uint32_t e, uint32_t & m0, uint32_t & m1) {
+    if (__builtin_expect(e - 6u < 249u, 1)) {
+        constexpr float MAGIC = 12582912.0f;  // 1.5 * 2^23
+        const float s = __uint_as_float((260u - e) << 23);  // 2^(133 - e)
+        uint32_t t[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) e = max(e, (__float_as_uint(v[i]) >> 23) & 0xffu);
+        for (int i = 0; i < 8; i++)
+            t[i] = __float_as_uint(__builtin_amdgcn_fmed3f(fmaf(v[i], s, MAGIC), MAGIC - 128.0f, MAGIC + 127.0f));
+        m0 = lo_bytes4(t[0], t[1], t[2], t[3]);
+        m1 = lo_bytes4(t[4], t[5], t[6], t[7]);
+        return;
+    }
     const int sh = 133 - (int) e;
     uint32_t b[8];
 #pragma unroll
@@ -29,6 +51,26 @@ __device__ inline uint32_t encode8(const float v[8], uint32_t & m0, uint32_t & m
     }
     m0 = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
     m1 = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+}
+
+__device__ inline uint32_t encode8(const float v[8], uint32_t & m0, uint32_t & m1) {
+    uint32_t e = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) e = max(e, (__float_as_uint(v[i]) >> 23) & 0xffu);
+    encode8_mant(v, e, m0, m1);
+    return e;
+}
+
+// encode8 for a block that holds no NaN: the largest exponent field is the
+// exponent of the largest magnitude (v_max3_f32 with free abs modifiers, four
+// ops for the eight values; a NaN would be skipped by the max, which is why
+// the general encoder reads the fields one by one).
+__device__ inline uint32_t encode8_no_nan(const float v[8], uint32_t & m0, uint32_t & m1) {
+    const float a = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fabsf(v[2]));
+    const float b = fmaxf(fmaxf(a, fabsf(v[3])), fabsf(v[4]));
+    const float c = fmaxf(fmaxf(b, fabsf(v[5])), fabsf(v[6]));
+    const uint32_t e = __float_as_uint(fmaxf(c, fabsf(v[7]))) >> 23;
+    encode8_mant(v, e, m0, m1);
     return e;
 }
 

@@ -245,3 +245,32 @@ def test_convert_rejects_bad_rows(zest_gpu, oracle):
     with pytest.raises(RuntimeError):
         zest_gpu.convert_weight(15, raw, 4, 256)         # Q8_K: no converter
     torch.cuda.synchronize()
+
+
+def test_convert_blocks_at_the_exponent_edges(zest_gpu, oracle):
+    # blocks whose largest exponent field is 0..12 (subnormals next to the
+    # smallest normals) or 240..254, with the other seven values anywhere
+    # below it, including values that round to +-128 and saturate
+    rng = np.random.default_rng(12)
+    n, k = 64, 512
+    nb = n * k // 8
+    top = np.concatenate([np.arange(0, 13), np.arange(240, 255)])
+    e = top[rng.integers(0, len(top), nb)]
+    lead = ((e.astype(np.uint32) << 23) | rng.integers(0, 1 << 23, nb).astype(np.uint32)
+            | (rng.integers(0, 2, nb).astype(np.uint32) << 31))
+    rest_e = np.maximum(e[:, None] - rng.integers(0, 30, (nb, 7)), 0).astype(np.uint32)
+    rest = ((rest_e << 23) | rng.integers(0, 1 << 23, (nb, 7)).astype(np.uint32)
+            | (rng.integers(0, 2, (nb, 7)).astype(np.uint32) << 31))
+    # some blocks: a value just under the top of the binade (rounds to 128)
+    near = rng.random(nb) < 0.2
+    lead[near] = (lead[near] & np.uint32(0xFF800000)) | np.uint32(0x7FFFFF)
+    blocks = np.concatenate([lead[:, None], rest], axis=1)
+    perm = rng.permuted(np.tile(np.arange(8), (nb, 1)), axis=1)
+    blocks = np.take_along_axis(blocks, perm, axis=1)
+    w = blocks.reshape(n, k).view(np.float32)
+    want = oracle.encode_rows(w)
+    assert np.array_equal(gpu_convert(zest_gpu, 0, w.view(np.uint8), n, k), want)
+    # the same values through a 16-bit type's path (BF16 keeps the exponent)
+    bf = (w.view(np.uint32) >> 16).astype(np.uint16)
+    want = oracle.encode_rows(oracle.dequant(30, bf.view(np.uint8), n, k))
+    assert np.array_equal(gpu_convert(zest_gpu, 30, bf.view(np.uint8), n, k), want)
