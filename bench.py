@@ -17,6 +17,7 @@ events: the same shapes, tiles and K splits), and the reference's CPU path
 a bounded sample.
 
     python bench.py [--steps K] [--warmup W] [--workload qwen3-4b] [--chunk M] [--no-cpu]
+    python bench.py --hbm      # converter (every GGUF type) and pack HBM rates
 
 The roofline's `traffic` (HBM bytes per GEMM launch) comes from two
 rocprofv3 counter runs of this script's probe mode, summarised into
@@ -144,6 +145,73 @@ def convert_bandwidth(z, wtype: int, n: int, k: int, reps: int = 10) -> dict:
             "frac": round(gbs / HBM_PEAK, 3)}
 
 
+# GGUF block types: (values per block, bytes per block, byte ranges of the
+# block's fp16 scale fields)
+GGUF_BLOCKS = {"F16": (1, 1, 2, []), "BF16": (30, 1, 2, []), "Q4_0": (2, 32, 18, [(0, 2)]),
+               "Q4_1": (3, 32, 20, [(0, 4)]), "Q5_0": (6, 32, 22, [(0, 2)]), "Q5_1": (7, 32, 24, [(0, 4)]),
+               "Q8_0": (8, 32, 34, [(0, 2)]), "Q2_K": (10, 256, 84, [(80, 84)]), "Q3_K": (11, 256, 110, [(108, 110)]),
+               "Q4_K": (12, 256, 144, [(0, 4)]), "Q5_K": (13, 256, 176, [(0, 4)]), "Q6_K": (14, 256, 210, [(208, 210)])}
+
+
+def random_gguf(name: str, n: int, k: int, seed: int):
+    """n rows of random GGUF blocks with finite scales (the converter's speed
+    does not depend on the values)."""
+    import torch
+    wtype, blk, bb, fields = GGUF_BLOCKS[name]
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    raw = torch.randint(0, 256, (n * (k // blk), bb), dtype=torch.uint8, device="cuda", generator=g)
+    if blk == 1:  # F16 / BF16: keep the exponent field off all-ones
+        v = raw.view(-1).view(torch.int16)
+        top = 0x7C00 if wtype == 1 else 0x7F80
+        v[(v & top) == top] &= 0x3FFF
+    for lo, hi in fields:
+        d = (torch.rand((raw.shape[0], (hi - lo) // 2), device="cuda", generator=g) * 0.01).to(torch.float16)
+        raw[:, lo:hi] = d.view(torch.uint8)
+    return raw.view(n, -1)
+
+
+def hbm_kernels(args) -> int:
+    """HBM rates of the converter (every GGUF type) and the activation pack,
+    on shapes whose footprint (four rotating sets) exceeds the 256 MB
+    Infinity Cache. One JSON line per kernel."""
+    import torch
+    z = load_pkg()
+    torch.cuda.set_device(0)
+    z.init(0)
+    n, k, sets, reps = 17408, 5120, 4, 5
+
+    def timed(fn, count):
+        fn(0)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(count):
+            fn(i)
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / count
+
+    for name, (wtype, blk, bb, _) in GGUF_BLOCKS.items():
+        raws = [random_gguf(name, n, k, s) for s in range(sets)]
+        outs = [z.empty_packed(n, k) for _ in range(sets)]
+        us = timed(lambda i: z.convert_weight(wtype, raws[i % sets], n, k, out=outs[i % sets]), sets * reps)
+        nbytes = raws[0].numel() + n * k * 9 / 8
+        gbs = nbytes / (us * 1e-6) / 1e9
+        print(json.dumps({"kernel": "convert", "type": name, "shape": [n, k], "bytes": int(nbytes), "us": round(us, 2),
+                          "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK, 3)}), flush=True)
+        del raws, outs
+    m, kk = 8192, 5120
+    xs = [torch.randn((m, kk), device="cuda") for _ in range(sets)]
+    for label, fn, mk, per in (("pack", z.pack_act, z.empty_packed, 5.125), ("pack_x", z.pack_act_x, z.empty_act, 6.0)):
+        outs = [mk(m, kk) for _ in range(sets)]
+        us = timed(lambda i: fn(xs[i % sets], out=outs[i % sets]), sets * reps)
+        gbs = per * m * kk / (us * 1e-6) / 1e9
+        print(json.dumps({"kernel": label, "shape": [m, kk], "bytes": int(per * m * kk), "us": round(us, 2),
+                          "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK, 3)}), flush=True)
+        del outs
+    return 0
+
+
 CALIB_FLOATS = 64 << 20  # the calibration kernel's floats: 256 MiB each way
 
 
@@ -212,7 +280,10 @@ def main() -> int:
     ap.add_argument("--chunk", type=int, default=None, help="tokens per chunk (default: the workload's)")
     ap.add_argument("--traffic-probe", action="store_true", help="one step and the calibration kernel, for rocprofv3")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
+    ap.add_argument("--hbm", action="store_true", help="HBM rates of the converter (every type) and the pack")
     args = ap.parse_args()
+    if args.hbm:
+        return hbm_kernels(args)
     if args.traffic_summary:
         return traffic_summary(*args.traffic_summary)
     if args.traffic_probe:

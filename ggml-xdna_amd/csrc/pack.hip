@@ -12,6 +12,7 @@
 namespace {
 
 using zest::encode8;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Row r of a weight in the packed operand: itself, or (gu = 0 / 1) its place
 // in a gate/up pair interleaved by 32-row groups: rows 64g..64g+31 hold gate
@@ -79,8 +80,10 @@ __global__ __launch_bounds__(256) void pack_act_kernel(const float * __restrict_
             uint32_t b[4];
 #pragma unroll
             for (int q = 0; q < 4; q++) b[q] = __float_as_uint((float) qi[q] * sc) >> 16;
-            *reinterpret_cast<uint2 *>(dst + zest_xtile_offset(rt, kc, R_pad) + rr * 128 + j * 8) =
-                make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
+            // nontemporal: the operand is written once per chunk and read by the GEMMs after
+            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+            const u32x2 bb = {b[0] | (b[1] << 16), b[2] | (b[3] << 16)};
+            __builtin_nontemporal_store(bb, reinterpret_cast<u32x2 *>(dst + zest_xtile_offset(rt, kc, R_pad) + rr * 128 + j * 8));
         } else {
             uint8_t * tile = dst + zest_tile_offset(rt, kc, R_pad);
             *reinterpret_cast<uint32_t *>(tile + rr * ZEST_TILE_K + j * 4) =
@@ -114,46 +117,6 @@ __global__ __launch_bounds__(256) void expand_act_kernel(const uint8_t * __restr
 }
 
 __device__ inline float half_to_float(uint16_t h) { return (float) __builtin_bit_cast(_Float16, h); }
-
-// Q8_0: 34-byte blocks of fp16 d + 32 int8; y = d * q, exact in fp32. One
-// thread takes one GGUF block = half a tile row: 32 mantissa bytes (two
-// 16-byte stores) and four exponent bytes. Workgroup: 8 rows x 32 blocks.
-__global__ __launch_bounds__(256) void convert_q8_0_kernel(const uint8_t * __restrict__ raw, int64_t N, int64_t K,
-                                                           uint8_t * __restrict__ dst, int64_t R_pad, int64_t K_pad,
-                                                           int64_t R_src, int gu) {
-    const int t = threadIdx.x;
-    const int64_t r = (int64_t) blockIdx.y * 8 + (t >> 5);
-    const int64_t jb = (int64_t) blockIdx.x * 32 + (t & 31);  // 32-column block
-    const int64_t col = jb * 32;
-    if (col >= K_pad || r >= R_src) return;
-    uint4 m0 = make_uint4(0, 0, 0, 0), m1 = make_uint4(0, 0, 0, 0);
-    uint32_t ex = 0;
-    if (r < N && col < K) {
-        const uint8_t * b = raw + r * (K / 32 * 34) + jb * 34;
-        const uint16_t * h = reinterpret_cast<const uint16_t *>(b);  // 2-byte aligned
-        const float d = half_to_float(h[0]);
-        float v[32];
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const uint16_t pair = h[1 + i];
-            v[2 * i] = (float) (int8_t) (pair & 0xff) * d;
-            v[2 * i + 1] = (float) (int8_t) (pair >> 8) * d;
-        }
-        uint32_t e[4];
-        e[0] = encode8(v, m0.x, m0.y);
-        e[1] = encode8(v + 8, m0.z, m0.w);
-        e[2] = encode8(v + 16, m1.x, m1.y);
-        e[3] = encode8(v + 24, m1.z, m1.w);
-        ex = e[0] | (e[1] << 8) | (e[2] << 16) | (e[3] << 24);
-    }
-    const int64_t dr = dst_row(r, gu);
-    uint8_t * tile = dst + zest_tile_offset(dr / ZEST_TILE_ROWS, col / ZEST_TILE_K, R_pad);
-    const int64_t rr = dr % ZEST_TILE_ROWS, half = (col % ZEST_TILE_K) / 32;
-    uint4 * mp = reinterpret_cast<uint4 *>(tile + rr * ZEST_TILE_K + half * 32);
-    mp[0] = m0;
-    mp[1] = m1;
-    *reinterpret_cast<uint32_t *>(tile + ZEST_TILE_MANT + rr * 8 + half * 4) = ex;
-}
 
 // ---- every GGUF type: one thread per half tile row ----------------------------
 // One thread dequantises 32 consecutive values of a row (col % 32 == 0) as
@@ -396,22 +359,31 @@ __device__ inline void encode_half_row(const float v[32], bool no_nan, uint4 & m
     ex = e[0] | (e[1] << 8) | (e[2] << 16) | (e[3] << 24);
 }
 
-// Workgroup: 8 rows x 32 half tile rows = the 8-row halves of 16 tiles.
-// Lane t dequantises and encodes row t/32, half t%32 (the 32 lanes of a row
-// read one contiguous run of its GGUF bytes) into LDS, laid out as the
-// tiles' own bytes: per tile 512 mantissa bytes (8 rows of 64) then 64
-// exponent bytes. The workgroup then stores each tile's two runs with
-// 16-byte stores in which consecutive lanes write consecutive bytes.
-template <int TYPE>
+#ifndef ZEST_CONVERT_ROWS
+#define ZEST_CONVERT_ROWS 16
+#endif
+
+// Workgroup: ROWS rows x 128/ROWS tile columns (256 threads, a half tile row
+// each). Lane t dequantises and encodes row t / (256/ROWS), half tile row
+// t % (256/ROWS) of the band (the lanes of a row read one contiguous run of
+// its GGUF bytes) into LDS, laid out as the destination's own bytes. With
+// ROWS >= 16 a tile column's ROWS/16 tiles are consecutive in the packed
+// operand, so the workgroup stores each tile column as one contiguous run,
+// 16 bytes a lane, consecutive lanes on consecutive bytes (with ROWS = 8, a
+// run of 512 mantissa bytes and one of 64 exponent bytes per tile).
+template <int TYPE, int ROWS>
 __global__ __launch_bounds__(256) void convert_kernel(const uint8_t * __restrict__ raw, size_t row_bytes, int64_t N,
                                                       int64_t K, uint8_t * __restrict__ dst, int64_t R_pad,
                                                       int64_t K_pad, int64_t R_src, int gu) {
-    constexpr int TB = 8 * ZEST_TILE_K + 8 * 8;  // one tile's 8 rows: 576 bytes
-    __shared__ uint4 stage[16 * TB / 16];
+    static_assert(ROWS == 8 || ROWS == 16 || ROWS == 32, "rows per workgroup");
+    constexpr int TILES = 128 / ROWS, HALVES = 2 * TILES;
+    // LDS bytes of one tile column: ROWS rows of 64 mantissas and 8 exponents
+    constexpr int RUN = ROWS * (ZEST_TILE_K + 8);
+    __shared__ uint4 stage[TILES * RUN / 16];
     uint8_t * sb = reinterpret_cast<uint8_t *>(stage);
-    const int t = threadIdx.x, rl = t >> 5, hl = t & 31;
-    const int64_t r = (int64_t) blockIdx.y * 8 + rl;
-    const int64_t col = ((int64_t) blockIdx.x * 32 + hl) * 32;
+    const int t = threadIdx.x, rl = t / HALVES, hl = t % HALVES;
+    const int64_t r = (int64_t) blockIdx.y * ROWS + rl;
+    const int64_t col = ((int64_t) blockIdx.x * HALVES + hl) * 32;
     uint4 m0 = make_uint4(0, 0, 0, 0), m1 = m0;
     uint32_t ex = 0;
     if (r < N && col < K) {  // else padding: zero blocks (exponent 0, mantissas 0)
@@ -420,20 +392,30 @@ __global__ __launch_bounds__(256) void convert_kernel(const uint8_t * __restrict
         encode_half_row(v, no_nan, m0, m1, ex);
     }
     const int j = hl >> 1, hf = hl & 1;
-    uint4 * ms = reinterpret_cast<uint4 *>(sb + j * TB + rl * ZEST_TILE_K + hf * 32);
+    // ROWS = 8: mantissas (8 rows of 64) then exponents (8 rows of 8);
+    // else whole tiles in the packed layout, ROWS/16 of them
+    const int mo = ROWS == 8 ? j * RUN + rl * ZEST_TILE_K
+                             : j * RUN + (rl >> 4) * ZEST_TILE_BYTES + (rl & 15) * ZEST_TILE_K;
+    const int eo = ROWS == 8 ? j * RUN + 8 * ZEST_TILE_K + rl * 8
+                             : j * RUN + (rl >> 4) * ZEST_TILE_BYTES + ZEST_TILE_MANT + (rl & 15) * 8;
+    uint4 * ms = reinterpret_cast<uint4 *>(sb + mo + hf * 32);
     ms[0] = m0;
     ms[1] = m1;
-    *reinterpret_cast<uint32_t *>(sb + j * TB + 8 * ZEST_TILE_K + rl * 8 + hf * 4) = ex;
+    *reinterpret_cast<uint32_t *>(sb + eo + hf * 4) = ex;
     __syncthreads();
-    // the 8-row group stays whole in the destination (dst_row keeps 8-row runs)
-    const int64_t dr0 = dst_row((int64_t) blockIdx.y * 8, gu), rt = dr0 / ZEST_TILE_ROWS, rr0 = dr0 % ZEST_TILE_ROWS;
-    const int64_t kc0 = (int64_t) blockIdx.x * 16;
-    const int ntiles = (int) min((int64_t) 16, K_pad / ZEST_TILE_K - kc0);
-    for (int c = t; c < ntiles * (TB / 16); c += 256) {
-        const int tj = c / (TB / 16), q = c % (TB / 16);
+    // the row band stays whole in the destination (dst_row keeps 32-row runs)
+    const int64_t dr0 = dst_row((int64_t) blockIdx.y * ROWS, gu), rt = dr0 / ZEST_TILE_ROWS, rr0 = dr0 % ZEST_TILE_ROWS;
+    const int64_t kc0 = (int64_t) blockIdx.x * TILES;
+    const int ntiles = (int) min((int64_t) TILES, K_pad / ZEST_TILE_K - kc0);
+    for (int c = t; c < ntiles * (RUN / 16); c += 256) {
+        const int tj = c / (RUN / 16), q = c % (RUN / 16);
         uint8_t * tile = dst + zest_tile_offset(rt, kc0 + tj, R_pad);
-        const int64_t off = q < 32 ? rr0 * ZEST_TILE_K + q * 16 : ZEST_TILE_MANT + rr0 * 8 + (q - 32) * 16;
-        *reinterpret_cast<uint4 *>(tile + off) = stage[c];
+        const int64_t off =
+            ROWS == 8 ? (q < 32 ? rr0 * ZEST_TILE_K + q * 16 : ZEST_TILE_MANT + rr0 * 8 + (q - 32) * 16) : q * 16;
+        // nontemporal: the operand is written once and read much later
+        const uint4 v = stage[c];
+        const u32x4 vv = {v.x, v.y, v.z, v.w};
+        __builtin_nontemporal_store(vv, reinterpret_cast<u32x4 *>(tile + off));
     }
 }
 
@@ -535,14 +517,6 @@ static int convert(int type, const void * raw, int64_t N, int64_t K, void * dst,
                                (uint8_t *) dst, R_pad, K_pad, gu);
             return zest::check_launch(name);
         }
-        case ZEST_TYPE_Q8_0: {
-            ZEST_REQUIRE(K % 32 == 0, "%s: Q8_0 needs K %% 32 == 0 (K=%lld)", name, (long long) K);
-            ZEST_REQUIRE(aligned(raw, 2), "%s: Q8_0 rows must be 2-byte aligned", name);
-            const dim3 grid((unsigned) ((K_pad / 32 + 31) / 32), (unsigned) (R_src / 8));
-            hipLaunchKernelGGL(convert_q8_0_kernel, grid, dim3(256), 0, s, (const uint8_t *) raw, N, K, (uint8_t *) dst,
-                               R_pad, K_pad, R_src, gu);
-            return zest::check_launch(name);
-        }
         default: break;
     }
     const size_t rb = zest_raw_row_bytes(type, K);
@@ -554,14 +528,17 @@ static int convert(int type, const void * raw, int64_t N, int64_t K, void * dst,
     }
     ZEST_REQUIRE(aligned(raw, row_align(type)), "%s: type %d rows must be %zu-byte aligned", name, type,
                  row_align(type));
-    const dim3 grid((unsigned) ((K_pad / 32 + 31) / 32), (unsigned) (R_src / 8));
+    constexpr int RW = ZEST_CONVERT_ROWS;
+    const dim3 grid((unsigned) ((K_pad / ZEST_TILE_K + 128 / RW - 1) / (128 / RW)), (unsigned) (R_src / RW));
     const uint8_t * r8 = (const uint8_t *) raw;
     uint8_t * d8 = (uint8_t *) dst;
 #define ZEST_CONVERT(T)                                                                                         \
-    case T: hipLaunchKernelGGL(convert_kernel<T>, grid, dim3(256), 0, s, r8, rb, N, K, d8, R_pad, K_pad, R_src, gu); \
+    case T:                                                                                                     \
+        hipLaunchKernelGGL((convert_kernel<T, RW>), grid, dim3(256), 0, s, r8, rb, N, K, d8, R_pad, K_pad, R_src, gu); \
         break
     switch (type) {
         ZEST_CONVERT(ZEST_TYPE_F16);
+        ZEST_CONVERT(ZEST_TYPE_Q8_0);
         ZEST_CONVERT(ZEST_TYPE_BF16);
         ZEST_CONVERT(ZEST_TYPE_Q4_0);
         ZEST_CONVERT(ZEST_TYPE_Q4_1);
