@@ -963,7 +963,7 @@ const char * dev_description(ggml_backend_dev_t) { return XDNA_DESCRIPTION; }
 // The GPU's own memory: the model's weights live there with their cache.
 void dev_memory(ggml_backend_dev_t, size_t * free, size_t * total) {
     *free = *total = 0;
-    if (mode() == run_mode::gpu && hipMemGetInfo(free, total) != hipSuccess) *free = *total = 0;
+    if (mode() == run_mode::gpu && !plan_only() && hipMemGetInfo(free, total) != hipSuccess) *free = *total = 0;
 }
 ggml_backend_dev_type dev_type(ggml_backend_dev_t) { return GGML_BACKEND_DEVICE_TYPE_GPU; }
 
@@ -981,7 +981,7 @@ ggml_backend_t dev_init(ggml_backend_dev_t dev, const char *) {
     if (mode() != run_mode::gpu) return nullptr;
     auto * ctx = new context;
     std::string err;
-    if (!env_int("GGML_XDNA_PLAN_ONLY", 0) && !ctx->init(err)) {
+    if (!plan_only() && !ctx->init(err)) {
         log(LOG_ERROR, "%s\n", err.c_str());
         delete ctx;
         return nullptr;

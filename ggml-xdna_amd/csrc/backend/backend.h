@@ -15,6 +15,9 @@ namespace zest {
 enum class run_mode { off, gpu };
 run_mode mode();
 int device_index();
+// GGML_XDNA_PLAN_ONLY=1: the device is offered for planning only (no GPU is
+// opened, no memory reported, every graph_compute fails).
+bool plan_only();
 
 // Set when the GPU path fails during a graph (a kernel error, non-finite
 // results, an injected failure): from then on the backend claims nothing

@@ -57,7 +57,7 @@ int device_index() {
 // GGML_XDNA_PLAN_ONLY=1 offers the device for planning only (supports_op,
 // the budget) without a GPU, so the gate can be tested on a machine without
 // one; every graph_compute then fails.
-static bool plan_only() {
+bool plan_only() {
     static const bool v = env_int("GGML_XDNA_PLAN_ONLY", 0) != 0;
     return v;
 }

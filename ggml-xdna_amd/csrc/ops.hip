@@ -79,7 +79,8 @@ __device__ inline void zero_row_expanded(uint8_t * packed, int64_t R_pad, int64_
                                    (r % ZEST_TILE_ROWS) * 128 + (c % ZEST_TILE_K) * 2) = make_uint2(0, 0);
 }
 
-// One wave per row: sum of squares (fp32), sc = 1/sqrt(ss/d + eps),
+// Rows wider than rms_norm_row_kernel takes: one wave per row, sum of
+// squares (fp32), sc = 1/sqrt(ss/d + eps),
 // y = x * sc (* w). Lane l takes the 4 floats at columns 4l + 256i, so a
 // wave's load covers 1 KB of the row; the sum is a wave reduction, no LDS.
 // The second pass re-reads the row (from L2) and writes y and/or the packed
@@ -149,6 +150,89 @@ __global__ __launch_bounds__(NORM_ROWS * 64) void rms_norm_kernel(const float * 
 #pragma unroll
                 for (int i = 0; i < 4; i++)
                     if (c + i < d) yr[c + i] = o[i];
+            }
+        }
+        if (packed) pack4_expanded(packed, R_pad, r, c, o);
+    }
+}
+
+// One workgroup (four waves) per row, for rows of at most 1024*NCH columns
+// (padding included): thread t holds the 4 floats at columns 4t + 1024i,
+// loaded at once; the sum of squares is a wave reduction and then a sum of
+// the four waves' partials through LDS. Four times the waves of
+// rms_norm_kernel for the same rows, so more loads are in flight.
+template <int NCH>
+__global__ __launch_bounds__(256) void rms_norm_row_kernel(const float * __restrict__ x, int64_t rows, int64_t d,
+                                                           float eps, const float * __restrict__ w,
+                                                           float * __restrict__ y, uint8_t * __restrict__ packed,
+                                                           int64_t R_pad) {
+    __shared__ float part[4];
+    const int t = threadIdx.x, lane = t & 63;
+    const int64_t r = blockIdx.x;
+    const int64_t d_pad = zest_k_padded(d);
+    if (r >= rows) {  // a padding row of the packed operand (the whole workgroup takes this branch)
+        for (int64_t c = t * 4; c < d_pad; c += 1024)
+            *reinterpret_cast<uint2 *>(packed + zest_xtile_offset(r / ZEST_TILE_ROWS, c / ZEST_TILE_K, R_pad) +
+                                       (r % ZEST_TILE_ROWS) * 128 + (c % ZEST_TILE_K) * 2) = make_uint2(0, 0);
+        return;
+    }
+    const float * xr = x + r * d;
+    const bool vec = (d & 3) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+    float v[NCH][4];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NCH; i++) {
+        const int64_t c = t * 4 + 1024 * i;
+        if (vec && c + 4 <= d) {
+            const float4 q = *reinterpret_cast<const float4 *>(xr + c);
+            v[i][0] = q.x;
+            v[i][1] = q.y;
+            v[i][2] = q.z;
+            v[i][3] = q.w;
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; q++) v[i][q] = c + q < d ? xr[c + q] : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NCH; i++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) ss += v[i][q] * v[i][q];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    if (lane == 0) part[t >> 6] = ss;
+    __syncthreads();
+    ss = (part[0] + part[1]) + (part[2] + part[3]);
+    const float sc = 1.0f / sqrtf(ss / (float) d + eps);
+    const bool wvec = w && vec && (reinterpret_cast<uintptr_t>(w) & 15) == 0;
+    const int64_t c_end = packed ? d_pad : d;
+#pragma unroll
+    for (int i = 0; i < NCH; i++) {
+        const int64_t c = t * 4 + 1024 * i;
+        if (c >= c_end) continue;  // pair-uniform: c_end is a multiple of 8
+        float o[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) o[q] = v[i][q] * sc;
+        if (w) {
+            if (wvec && c + 4 <= d) {
+                const float4 q = *reinterpret_cast<const float4 *>(w + c);
+                o[0] *= q.x;
+                o[1] *= q.y;
+                o[2] *= q.z;
+                o[3] *= q.w;
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; q++) o[q] *= c + q < d ? w[c + q] : 0.0f;
+            }
+        }
+        if (y && c < d) {
+            float * yr = y + r * d;
+            if (vec && c + 4 <= d) {
+                *reinterpret_cast<float4 *>(yr + c) = make_float4(o[0], o[1], o[2], o[3]);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    if (c + q < d) yr[c + q] = o[q];
             }
         }
         if (packed) pack4_expanded(packed, R_pad, r, c, o);
@@ -261,9 +345,21 @@ int zest_rms_norm(const float * x, int64_t rows, int64_t d, float eps, const flo
     ZEST_REQUIRE(!packed || d % 8 == 0, "zest_rms_norm: packing needs d %% 8 == 0");
     // with a packed output, the grid also covers its padding rows (zeroed)
     const int64_t R_pad = zest_rows_padded(rows), grid_rows = packed ? R_pad : rows;
-    hipLaunchKernelGGL(rms_norm_kernel, dim3((unsigned) ((grid_rows + NORM_ROWS - 1) / NORM_ROWS)),
-                       dim3(NORM_ROWS * 64), 0, zest::as_stream(stream), x, rows, d, eps, w, y, (uint8_t *) packed,
-                       R_pad);
+    const int64_t chunks = (zest_k_padded(d) + 255) / 256;  // the output pass covers the padded width
+    hipStream_t s = zest::as_stream(stream);
+    uint8_t * pk = (uint8_t *) packed;
+    if (chunks <= 4)  // up to 1024 columns: one workgroup per row
+        hipLaunchKernelGGL(rms_norm_row_kernel<1>, dim3((unsigned) grid_rows), dim3(256), 0, s, x, rows, d, eps, w, y,
+                           pk, R_pad);
+    else if (chunks <= 12)  // up to 3072
+        hipLaunchKernelGGL(rms_norm_row_kernel<3>, dim3((unsigned) grid_rows), dim3(256), 0, s, x, rows, d, eps, w, y,
+                           pk, R_pad);
+    else if (chunks <= 24)  // up to 6144
+        hipLaunchKernelGGL(rms_norm_row_kernel<6>, dim3((unsigned) grid_rows), dim3(256), 0, s, x, rows, d, eps, w, y,
+                           pk, R_pad);
+    else
+        hipLaunchKernelGGL(rms_norm_kernel, dim3((unsigned) ((grid_rows + NORM_ROWS - 1) / NORM_ROWS)),
+                           dim3(NORM_ROWS * 64), 0, s, x, rows, d, eps, w, y, pk, R_pad);
     return zest::check_launch("zest_rms_norm");
 }
 

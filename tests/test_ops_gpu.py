@@ -25,7 +25,7 @@ def _host(t):
     return t.cpu().numpy()
 
 
-@pytest.mark.parametrize("rows,d", [(8, 256), (2048, 2560), (5, 200), (3, 5120)])
+@pytest.mark.parametrize("rows,d", [(8, 256), (2048, 2560), (5, 200), (3, 5120), (40, 6144), (6, 7000), (3, 9728)])
 def test_rms_norm_mul_and_fused_pack(zest_gpu, oracle, rows, d):
     import torch
     x = Rng(rows + d).normal(rows * d, 0, 1.5).reshape(rows, d)
