@@ -106,8 +106,9 @@ def act_bytes(rows: int, k: int) -> int:
 def expanded_to_rows(buf: np.ndarray, rows: int, k: int) -> np.ndarray:
     """Expanded operand bytes -> float32 [rows][k] (the bf16 values widened)."""
     rp, kp = rows_pad(rows), k_pad(k)
-    t = np.frombuffer(np.ascontiguousarray(buf).tobytes(), dtype=np.uint16).reshape(kp // 64, rp // 16, 16, 64)
-    full = t.transpose(1, 2, 0, 3).reshape(rp, kp)
+    # [64-column chunk][32-row group][16-column quarter][row][column]
+    t = np.frombuffer(np.ascontiguousarray(buf).tobytes(), dtype=np.uint16).reshape(kp // 64, rp // 32, 4, 32, 16)
+    full = t.transpose(1, 3, 0, 2, 4).reshape(rp, kp)
     return (full.astype(np.uint32) << 16).view(np.float32)[:rows, :k]
 
 

@@ -34,6 +34,9 @@
 #ifndef ZEST_GEMM_GROUP_M
 #define ZEST_GEMM_GROUP_M 4  // tile rows per group of the tile order
 #endif
+#ifndef ZEST_GEMM_AREG
+#define ZEST_GEMM_AREG 1  // producers stage the A slab through registers, two steps ahead (else LDS DMA, one step)
+#endif
 #ifndef ZEST_GEMM_XSTEP
 #define ZEST_GEMM_XSTEP 1  // consumers read a step's first fragments before the barrier that starts it
 #endif
@@ -48,10 +51,13 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // BM x BN tile; CWM x CWN consumer waves, each a WM x WN block of 32x32 MFMA
-// tiles; as many producer waves.
-template <int BM_, int BN_, int CWM_, int CWN_>
+// tiles; as many producer waves. ADIRECT: the consumers load their A
+// fragments from memory straight into registers and LDS holds W alone; else
+// the producers stage the A slab in LDS too.
+template <int BM_, int BN_, int CWM_, int CWN_, bool ADIRECT_ = false>
 struct gemm_cfg {
     static constexpr int BM = BM_, BN = BN_, CWM = CWM_, CWN = CWN_;
+    static constexpr bool ADIRECT = ADIRECT_;
     static constexpr int NC = 64 * CWM * CWN;  // consumer threads
     static constexpr int NP = NC;              // producer threads
     static constexpr int NT = NC + NP;
@@ -60,10 +66,12 @@ struct gemm_cfg {
     static constexpr int AC = BM * 8 / NP;  // A chunks (16 B = one block) per producer thread per K-step
     static constexpr int BU = BN * 4 / NP;  // W units (two blocks) per producer thread per K-step
     static constexpr int ROWB = 128;        // LDS bytes per row (64 bf16)
-    static constexpr int A_BYTES = BM * ROWB;  // a stage: A rows, then W rows
-    static constexpr int STAGE = (BM + BN) * ROWB;
+    static constexpr int A_BYTES = ADIRECT ? 0 : BM * ROWB;  // a stage: A rows, then W rows
+    static constexpr int STAGE = A_BYTES + BN * ROWB;
     static constexpr int STAGES = 3;
-    static constexpr size_t LDS_BYTES = (size_t) STAGES * STAGE;
+    // the ring, or the epilogues' per-wave regions (WM x WN floats each)
+    static constexpr size_t LDS_BYTES =
+        (size_t) STAGES * STAGE > (size_t) BM * BN * 4 ? (size_t) STAGES * STAGE : (size_t) BM * BN * 4;
     static constexpr int A_STEP = NP * 16;                     // bytes between a thread's A chunks
     static_assert(BM * 8 % NP == 0 && BN * 4 % NP == 0, "work must divide evenly");
     static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be whole 32x32 MFMA tiles");
@@ -122,12 +130,14 @@ __device__ inline void wait_vm_lgkm0() {
 // The producer side. Loads go through buffer resources: the slab's byte
 // offset is wave-uniform (a scalar offset), the lane's place in it a fixed
 // vector offset, and a read past the operand returns zeros.
-//   A: the K-step's A slab (BM rows of 128 bytes) is one contiguous run (BM/16
-//      consecutive 2 KB tiles). It goes straight from memory into LDS
-//      (buffer_load ... lds): instruction j of the step fills LDS rows
+//   A: the K-step's A slab (BM rows of 64 columns) is one contiguous run
+//      (BM/32 consecutive 4 KB groups of the expanded layout). By LDS DMA
+//      (buffer_load ... lds), instruction j of the step fills LDS rows
 //      8j..8j+7, lane l writing the 16 bytes at 16*l, i.e. row 8j + l/8,
-//      position l%8. The swizzle is applied on the source side: lane l reads
-//      the chunk that belongs at that position, (l%8) ^ swz(row).
+//      position l%8; lane l reads the chunk that belongs at that position,
+//      (l%8) ^ swz(row), wherever the layout puts it. Through registers, lane
+//      l of wave pw reads the slab's bytes in order (sub-tile pw of group i:
+//      row 32i + l/2, chunk 2pw + l%2) and stores them swizzled.
 //   W: thread p takes two adjacent units of tile p/32 of the W slab: row
 //      p%16, column quarters 2h and 2h+1 with h = p/16%2, i.e. 32 contiguous
 //      mantissa bytes (two 16-byte loads) and 4 contiguous exponent bytes
@@ -137,12 +147,14 @@ __device__ inline void wait_vm_lgkm0() {
 template <class C>
 struct producer {
     static constexpr int NPW = C::NP / 64;          // producer waves
-    static constexpr int AI = C::BM / 8 / NPW;      // A instructions per producer wave per K-step
+    static constexpr int AI = C::ADIRECT ? 1 : C::BM / 8 / NPW;  // A instructions per producer wave per K-step
     static constexpr int WI = 3;                    // W load instructions per K-step (load_w)
     static_assert(C::BU == 2 && C::NP / 32 == C::BN / 16, "two W units per producer thread, 32 threads a tile");
+    static_assert(C::ADIRECT || NPW == 4, "the A slab's rows map to four producer waves");
     __amdgpu_buffer_rsrc_t ra, rw;
     int pw;                // producer wave
     int va, vwm, vwe;      // lane offsets: A chunk, W mantissas, W exponents
+    int vla, sta;          // A through registers: the lane's chunk in the slab, its LDS offset
     int stw[2][2];         // LDS offsets of the two W units' two chunks each
 
     __device__ producer(const uint8_t * A, int64_t a_bytes, const uint8_t * W, int64_t w_bytes, int p) {
@@ -150,9 +162,14 @@ struct producer {
         rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(W), (short) 0, (int) w_bytes, 0x00020000);
         pw = __builtin_amdgcn_readfirstlane(p >> 6);
         const int l = p & 63;
-        // instruction j = i*NPW + pw: j and pw have the same parity, so
-        // swz(8j + l/8) is the same for every i
-        va = pw * 1024 + (l >> 3) * 128 + ((l & 7) ^ swz(8 * (pw & 1) + (l >> 3))) * 16;
+        // DMA instruction j = i*NPW + pw fills LDS rows 32i + 8pw + l/8 (NPW = 4):
+        // j and pw have the same parity, so swz(8j + l/8) is the same for every
+        // i, and the source row's place in its 32-row group is 8pw + l/8
+        const int ca = (l & 7) ^ swz(8 * (pw & 1) + (l >> 3));
+        va = (ca >> 1) * ZEST_XSUB_BYTES + (8 * pw + (l >> 3)) * 32 + (ca & 1) * 16;
+        // through registers: slab bytes in order, stored swizzled
+        vla = pw * 1024 + l * 16;
+        sta = (l >> 1) * C::ROWB + ((2 * pw + (l & 1)) ^ swz(l >> 1)) * 16;
         const int t = p >> 5, row = p & 15, h = (p >> 4) & 1;
         vwm = t * ZEST_TILE_BYTES + row * ZEST_TILE_K + h * 32;
         vwe = t * ZEST_TILE_BYTES + ZEST_TILE_MANT + row * 8 + h * 4;
@@ -173,6 +190,20 @@ struct producer {
                                                      a_off + i * NPW * 1024, 0, 0);
     }
 
+    // A chunks [i0, i0 + n) of the slab at byte a_off, into registers; chunk
+    // i is row 32i + l/2, chunk 2pw + l%2 of the slab.
+    __device__ void load_a(uint4 (&a)[AI], int a_off, int i0 = 0, int n = AI) const {
+        if constexpr (C::ADIRECT) return;
+#pragma unroll
+        for (int i = i0; i < i0 + n; i++) a[i] = load16(ra, vla + i * NPW * 1024, a_off);
+    }
+
+    __device__ void store_a(const uint4 (&a)[AI], uint8_t * smem, int stage, int i0 = 0, int n = AI) const {
+        if constexpr (C::ADIRECT) return;
+#pragma unroll
+        for (int i = i0; i < i0 + n; i++) lds_put(smem, stage + sta + i * NPW * 1024, a[i]);
+    }
+
     __device__ void load_w(stage_regs<C> & st, int w_off) const {
         st.wm[0] = load16(rw, vwm, w_off);
         st.wm[1] = load16(rw, vwm + 16, w_off);
@@ -181,22 +212,33 @@ struct producer {
 
     // W unit i of a step, by the branch-free fast expansion, stored; true if
     // the unit needs the general expansion (store_w_general) instead.
+    // ASYNC: stores opaque to the compiler's wait counting (beside LDS DMA).
+    template <bool ASYNC = true>
     __device__ bool store_w_unit(const stage_regs<C> & st, int i, uint8_t * smem, int stage) const {
         uint32_t b[8];
         const bool slow = zest::expand16_fast(st.wm[i], i ? st.we >> 16 : st.we & 0xffffu, b);
-        lds_put_async(smem, stw[i][0] + stage, make_uint4(b[0], b[1], b[2], b[3]));
-        lds_put_async(smem, stw[i][1] + stage, make_uint4(b[4], b[5], b[6], b[7]));
+        put<ASYNC>(smem, stw[i][0] + stage, make_uint4(b[0], b[1], b[2], b[3]));
+        put<ASYNC>(smem, stw[i][1] + stage, make_uint4(b[4], b[5], b[6], b[7]));
         return slow;
     }
 
+    template <bool ASYNC>
+    static __device__ void put(uint8_t * smem, int off, uint4 v) {
+        if (ASYNC)
+            lds_put_async(smem, off, v);
+        else
+            lds_put(smem, off, v);
+    }
+
     // Every unit of the step by the general expansion, stored.
+    template <bool ASYNC = true>
     __device__ void store_w_general(const stage_regs<C> & st, uint8_t * smem, int stage) const {
 #pragma unroll
         for (int i = 0; i < C::BU; i++) {
             uint32_t b[8];
             zest::expand16(st.wm[i], i ? st.we >> 16 : st.we & 0xffffu, b);
-            lds_put_async(smem, stw[i][0] + stage, make_uint4(b[0], b[1], b[2], b[3]));
-            lds_put_async(smem, stw[i][1] + stage, make_uint4(b[4], b[5], b[6], b[7]));
+            put<ASYNC>(smem, stw[i][0] + stage, make_uint4(b[0], b[1], b[2], b[3]));
+            put<ASYNC>(smem, stw[i][1] + stage, make_uint4(b[4], b[5], b[6], b[7]));
         }
     }
 
@@ -204,11 +246,12 @@ struct producer {
     // first unit's). The units take the branch-free fast expansion; a unit
     // whose exponent bytes need the general one is redone behind a single
     // wave-uniform branch, which real weights almost never take.
+    template <bool ASYNC = true>
     __device__ void store_w(const stage_regs<C> & st, uint8_t * smem, int stage) const {
         bool slow = false;
 #pragma unroll
-        for (int i = 0; i < C::BU; i++) slow |= store_w_unit(st, i, smem, stage);
-        if (__builtin_expect(__any(slow), 0)) store_w_general(st, smem, stage);
+        for (int i = 0; i < C::BU; i++) slow |= store_w_unit<ASYNC>(st, i, smem, stage);
+        if (__builtin_expect(__any(slow), 0)) store_w_general<ASYNC>(st, smem, stage);
     }
 };
 
@@ -249,6 +292,72 @@ __device__ inline void consume(f32x16 (&acc)[C::TI][C::TJ], bf16x8 (&af)[2][C::T
     }
 }
 
+// ADIRECT consumers: the A fragments come from memory straight into
+// registers. Fragment i of sub-step s is sub-tile s of the 32-row group
+// wm*WM/32 + i of the tile's K-step slab: lane l takes row l%32, chunk
+// 2s + l/32 (one block as bf16, the MFMA's A operand), the 16 bytes at
+// 32(l%32) + 16(l/32), so the wave's load covers one contiguous 1 KB. A load
+// past the operand returns zeros.
+template <class C>
+struct a_loader {
+    __amdgpu_buffer_rsrc_t ra;
+    int va[C::TI];
+
+    __device__ a_loader(const uint8_t * A, int64_t a_bytes, int wm, int lane) {
+        ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(A), (short) 0, (int) a_bytes, 0x00020000);
+#pragma unroll
+        for (int i = 0; i < C::TI; i++)
+            va[i] = (wm * C::WM / 32 + i) * ZEST_XGROUP_BYTES + (lane & 31) * 32 + (lane >> 5) * 16;
+    }
+
+    __device__ bf16x8 load(int i, int s, int a_off) const {
+        return __builtin_bit_cast(bf16x8,
+                                  __builtin_amdgcn_raw_buffer_load_b128(ra, va[i] + s * ZEST_XSUB_BYTES, a_off, 0));
+    }
+
+    // every fragment of a K-step
+    __device__ void load_step(bf16x8 (&a)[4][C::TI], int a_off) const {
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int i = 0; i < C::TI; i++) a[s][i] = load(i, s, a_off);
+    }
+};
+
+// One K-step of an ADIRECT consumer wave: A from registers `a` (this step's,
+// loaded two steps ago), W fragments from the stage at `cur`, read a
+// sub-step ahead (sub-step 0 of stage `nxt` during the last). As each
+// sub-step's MFMAs are issued, its A registers are reloaded with the same
+// fragments of the step at a_next (LOAD), two steps ahead, so a load has two
+// steps to land. The scheduling groups interleave the W reads and A loads
+// with the MFMAs.
+template <class C, bool LOAD>
+__device__ inline void consume_direct(f32x16 (&acc)[C::TI][C::TJ], bf16x8 (&a)[4][C::TI], bf16x8 (&bw)[2][C::TJ],
+                                      const uint8_t * smem, const int (&fw)[4], int cur, int nxt,
+                                      const a_loader<C> & al, int a_next) {
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        const int off = s < 3 ? fw[s + 1] + cur : fw[0] + nxt;
+#pragma unroll
+        for (int j = 0; j < C::TJ; j++) bw[(s + 1) & 1][j] = lds_get(smem, off + j * 32 * C::ROWB);
+#pragma unroll
+        for (int i = 0; i < C::TI; i++)
+#pragma unroll
+            for (int j = 0; j < C::TJ; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s][i], bw[s & 1][j], acc[i][j], 0, 0, 0);
+        if (LOAD) {
+#pragma unroll
+            for (int i = 0; i < C::TI; i++) a[s][i] = al.load(i, s, a_next);
+        }
+#pragma unroll
+        for (int q = 0; q < C::TI * C::TJ; q++) {
+            if (q < C::TJ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // a W fragment read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // an MFMA
+            if (LOAD && (q + 1) % C::TJ == 0) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // an A load
+        }
+    }
+}
+
 // The fp32 store. 32x32 accumulator layout: lane l, register v holds row
 // (v/4)*8 + (l/32)*4 + v%4 and column l%32 of its MFMA tile. Stores go
 // through a buffer resource covering rows [0, M) of C, so rows past M are
@@ -271,16 +380,18 @@ __device__ inline void store_tile(const f32x16 (&acc)[C::TI][C::TJ], float * Cou
     const int row0 = (int) m0 + wm * C::WM;
     const float * rl = nullptr;  // the residual block in LDS: WM rows of WN floats
     if constexpr (RES) {
-        static_assert(C::WN == 64, "a residual row segment is 16 lanes of 16 bytes");
+        // a row of the block is LPR lanes of 16 bytes; an instruction takes RPI rows
+        constexpr int LPR = C::WN / 4, RPI = 64 / LPR;
+        static_assert(64 % LPR == 0 && C::WM % RPI == 0, "whole residual rows per instruction");
         uint8_t * region = smem + wave * (C::WM * C::WN * 4);
         const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<float *>(res), (short) 0, (int) (M * ldr * 4), 0x00020000);
-        // instruction q: rows 4q..4q+3 of the block, lane l taking row 4q + l/16, bytes 16(l%16)
-        const int voff = (int) ((row0 + (lane >> 4)) * ldr * 4 + (n0 + wn * C::WN) * 4 + (lane & 15) * 16);
+        // instruction q: rows RPI*q.. of the block, lane l taking row RPI*q + l/LPR, bytes 16(l%LPR)
+        const int voff = (int) ((row0 + lane / LPR) * ldr * 4 + (n0 + wn * C::WN) * 4 + (lane % LPR) * 16);
 #pragma unroll
-        for (int q = 0; q < C::WM / 4; q++)
+        for (int q = 0; q < C::WM / RPI; q++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_ptr_t) (region + q * 1024), 16, voff,
-                                                     (int) (4 * q * ldr * 4), 0, 0);
+                                                     (int) (RPI * q * ldr * 4), 0, 0);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         rl = reinterpret_cast<const float *>(region);
     }
@@ -307,30 +418,30 @@ __device__ inline void store_tile(const f32x16 (&acc)[C::TI][C::TJ], float * Cou
 }
 
 // The fused gate/up epilogue: the weight is a gate/up pair interleaved by
-// 32-row groups (zest_convert_weight_gu), so with 64-row wave tiles (TJ = 2)
-// accumulator tile j = 0 holds gate values and j = 1 the up values of the
-// same 32 output columns, lane l%32 = column. Computes h = glu(g, u) in fp32
-// (the GLU kernel's arithmetic) and optionally stores it. For the down
-// projection's operand the wave stages its WM x 32 block of h in LDS (the
-// K loop is over and every stage consumed), then reads it back by rows: lane
-// l takes 16 consecutive columns of one row, i.e. two whole bfp16 blocks,
-// which it encodes and stores decoded as the activation packer does
-// (store_expanded16: two 16-byte stores). Each wave has its own LDS region,
-// so no barrier is needed: a wave's LDS operations complete in order.
-// Rows and columns past M and F come from zero padding and store zeros, as
-// the packer's padding is.
+// 32-row groups (zest_convert_weight_gu), so accumulator tiles 2p and 2p+1 of
+// a wave hold the gate and the up values of the same 32 output columns, lane
+// l%32 = column. Computes h = glu(g, u) in fp32 (the GLU kernel's arithmetic)
+// and optionally stores it. For the down projection's operand the wave stages
+// its WM x HW block of h in LDS (the K loop is over and every stage consumed),
+// then reads it back by rows: lane l takes 16 consecutive columns of one row,
+// i.e. two whole bfp16 blocks, which it encodes and stores decoded as the
+// activation packer does (store_expanded16: two 16-byte stores). Each wave
+// has its own LDS region, so no barrier is needed: a wave's LDS operations
+// complete in order. Rows and columns past M and F come from zero padding and
+// store zeros, as the packer's padding is.
 template <class C, int KIND>
 __device__ inline void store_glu(const f32x16 (&acc)[C::TI][C::TJ], uint8_t * smem, uint8_t * xout, float * h,
                                  int64_t ldh, int64_t M, int64_t F, int64_t m0, int64_t n0, int wave, int wm, int wn,
                                  int lane, uint32_t * nonfinite) {
-    static_assert(C::TJ == 2 && C::WN == 64, "the fused GLU needs 64-row wave tiles: gate and up");
-    // staged rows of 36 floats: the 16-lane groups of the row reads below
+    constexpr int NPAIR = C::TJ / 2, HW = 32 * NPAIR;  // gate/up pairs; h columns of the wave
+    static_assert(C::TJ % 2 == 0 && HW <= ZEST_TILE_K, "the fused GLU needs whole gate/up pairs in one K chunk");
+    // staged rows of HW + 4 floats: the 16-lane groups of the row reads below
     // (rows r..r+15, one 16-byte column chunk) then hit distinct banks
-    constexpr int P = 36;
-    static_assert(P <= C::WN && (size_t) C::BM * C::BN * 4 <= C::LDS_BYTES, "staging must fit the LDS ring");
+    constexpr int P = HW + 4;
+    static_assert(P <= C::WN && (size_t) C::BM * C::BN * 4 <= C::LDS_BYTES, "staging must fit the wave's region");
     // the wave's LDS region, the one the split-K fixup uses: WM x WN floats
     float * st = reinterpret_cast<float *>(smem + wave * (C::WM * C::WN * 4));
-    const int64_t c0 = n0 / 2 + wn * 32, col = c0 + (lane & 31);
+    const int64_t c0 = n0 / 2 + wn * HW;
     bool bad = false;
 #pragma unroll
     for (int i = 0; i < C::TI; i++)
@@ -338,42 +449,46 @@ __device__ inline void store_glu(const f32x16 (&acc)[C::TI][C::TJ], uint8_t * sm
         for (int v = 0; v < 16; v++) {
             const int rw = i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);  // row in the wave tile
             const int64_t row = m0 + wm * C::WM + rw;
-            const float g = acc[i][0][v], u = acc[i][1][v];
-            const float hv = zest::glu(KIND, g, u);
-            bad |= !(__builtin_fabsf(g) <= 3.402823466e38f) || !(__builtin_fabsf(u) <= 3.402823466e38f) ||
-                   !(__builtin_fabsf(hv) <= 3.402823466e38f);
-            if (h && row < M && col < F) h[row * ldh + col] = hv;
-            if (xout) st[rw * P + (lane & 31)] = hv;
+#pragma unroll
+            for (int q = 0; q < NPAIR; q++) {
+                const float g = acc[i][2 * q][v], u = acc[i][2 * q + 1][v];
+                const float hv = zest::glu(KIND, g, u);
+                const int64_t col = c0 + q * 32 + (lane & 31);
+                bad |= !(__builtin_fabsf(g) <= 3.402823466e38f) || !(__builtin_fabsf(u) <= 3.402823466e38f) ||
+                       !(__builtin_fabsf(hv) <= 3.402823466e38f);
+                if (h && row < M && col < F) h[row * ldh + col] = hv;
+                if (xout) st[rw * P + q * 32 + (lane & 31)] = hv;
+            }
         }
     if (xout) {
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         __builtin_amdgcn_wave_barrier();
         const int64_t M_pad = zest_rows_padded(M);
-        const int half = lane >> 5;
+        // a pass reads RPP rows, lane l taking row l%RPP and 16-column chunk l/RPP
+        constexpr int QPR = HW / 16, RPP = 64 / QPR;
+        const int q = lane / RPP;
 #pragma unroll
-        for (int j = 0; j < C::TI; j++) {
-            const int rw = j * 32 + (lane & 31);
-            const float4 * p = reinterpret_cast<const float4 *>(st + rw * P + half * 16);
+        for (int j = 0; j < C::WM / RPP; j++) {
+            const int rw = j * RPP + lane % RPP;
+            const float4 * p = reinterpret_cast<const float4 *>(st + rw * P + q * 16);
             float v[16];
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const float4 f = p[q];
-                v[4 * q] = f.x;
-                v[4 * q + 1] = f.y;
-                v[4 * q + 2] = f.z;
-                v[4 * q + 3] = f.w;
+            for (int x = 0; x < 4; x++) {
+                const float4 f = p[x];
+                v[4 * x] = f.x;
+                v[4 * x + 1] = f.y;
+                v[4 * x + 2] = f.z;
+                v[4 * x + 3] = f.w;
             }
-            zest::store_expanded16(xout, M_pad, m0 + wm * C::WM + rw, c0 + half * 16, v);
+            zest::store_expanded16(xout, M_pad, m0 + wm * C::WM + rw, c0 + q * 16, v);
         }
         // The last tile row also zeroes the operand's rows that no tile
-        // reaches, [m0 + BM, M_pad): 4 lanes per row, 16 bytes each.
-        if (m0 + C::BM >= M) {
-            uint8_t * base = xout + zest_xtile_offset(0, c0 / ZEST_TILE_K, M_pad) + (c0 % ZEST_TILE_K) * 2 +
-                             (lane & 3) * 16;
-            for (int64_t row = m0 + C::BM + wm * 16 + (lane >> 2); row < M_pad; row += 16 * C::CWM)
-                *reinterpret_cast<uint4 *>(base + (row / ZEST_TILE_ROWS) * ZEST_XTILE_BYTES +
-                                           (row % ZEST_TILE_ROWS) * 128) = make_uint4(0, 0, 0, 0);
-        }
+        // reaches, [m0 + BM, M_pad): a row's HW columns are Z lanes of 16
+        // bytes, so a wave covers 64/Z rows at a time.
+        constexpr int Z = HW / 8, RZ = 64 / Z;
+        if (m0 + C::BM >= M)
+            for (int64_t row = m0 + C::BM + wm * RZ + lane / Z; row < M_pad; row += RZ * C::CWM)
+                *reinterpret_cast<uint4 *>(xout + zest_xoffset(row, c0 + (lane % Z) * 8, M_pad)) = make_uint4(0, 0, 0, 0);
     }
     if (nonfinite && __any(bad) && lane == 0) atomicOr(nonfinite, 1u);
 }
@@ -604,6 +719,113 @@ __device__ inline void produce(const producer<C> & pr, uint8_t * smem, int a0, i
     }
 }
 
+// One K-step's loads, held in a producer thread's registers.
+template <class C>
+struct step_regs {
+    uint4 a[producer<C>::AI];
+    stage_regs<C> w;
+};
+
+// s_waitcnt lgkmcnt(0) alone: this wave's LDS stores done, loads left in flight
+__device__ inline void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// One steady-state step of the register producer: step j's A chunks and W
+// units (loaded two steps ago) stored into `stage`, step j+2's requested into
+// the same registers. The A chunks go out in groups between the W units'
+// expansions, each group's loads right after its stores, so the address unit
+// works while the wave expands.
+template <class C>
+__device__ inline void reg_step(const producer<C> & pr, uint8_t * smem, int stage, step_regs<C> & r, int a_off_next,
+                                int w_off_next) {
+    constexpr int AI = producer<C>::AI, PER = C::ADIRECT ? 0 : AI / C::BU;
+    static_assert(C::ADIRECT || AI % C::BU == 0, "A chunks must split evenly between W units");
+    bool slow = false;
+#pragma unroll
+    for (int u = 0; u < C::BU; u++) {
+        pr.store_a(r.a, smem, stage, u * PER, PER);
+        pr.load_a(r.a, a_off_next, u * PER, PER);
+        __builtin_amdgcn_sched_barrier(0);
+        slow |= pr.template store_w_unit<false>(r.w, u, smem, stage);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (__builtin_expect(__any(slow), 0)) pr.template store_w_general<false>(r.w, smem, stage);
+    pr.load_w(r.w, w_off_next);
+}
+
+// The producer with the A slab staged through registers: step j's A chunks
+// and W units are loaded during step j-4 and stored into stage j%3 during
+// step j-2, so a load has two steps to land where the LDS DMA has one (the
+// consumers read step j+1's first fragments before the barrier that ends
+// step j, so a stage must be complete a step before it is consumed, and it is
+// free only after the step that last read it). All loads go into registers
+// and every LDS store is the compiler's own, so the compiler counts the loads
+// in flight and waits for exactly those whose registers a store reads; before
+// a barrier only the LDS stores are waited for. The steady state runs without
+// conditions; the last steps do their remaining stores one by one.
+template <class C>
+__device__ inline void produce_regs(const producer<C> & pr, uint8_t * smem, int a0, int w0, int a_kstride,
+                                    int w_kstride, int ns) {
+    // Steps 0-3 are requested whether or not they exist: a load past the
+    // operand returns zeros, one past this split's steps reads the next
+    // split's slab, and neither is stored. Unconditional loads keep the
+    // compiler's count of loads in flight exact where the steady state starts.
+    step_regs<C> r0, r1;
+    pr.load_a(r0.a, a0);
+    pr.load_w(r0.w, w0);
+    pr.load_a(r1.a, a0 + a_kstride);
+    pr.load_w(r1.w, w0 + w_kstride);
+    pr.store_a(r0.a, smem, 0);
+    pr.template store_w<false>(r0.w, smem, 0);
+    pr.load_a(r0.a, a0 + 2 * a_kstride);
+    pr.load_w(r0.w, w0 + 2 * w_kstride);
+    if (ns > 1) {
+        pr.store_a(r1.a, smem, C::STAGE);
+        pr.template store_w<false>(r1.w, smem, C::STAGE);
+    }
+    pr.load_a(r1.a, a0 + 3 * a_kstride);
+    pr.load_w(r1.w, w0 + 3 * w_kstride);
+    wait_lgkm0();
+    producer_barrier();
+    // during step k: step k+2 stored into stage (k+2)%3, step k+4 requested
+    int stage = 2 * C::STAGE, k = 0;
+    for (; k + 5 < ns; k += 2) {
+        reg_step<C>(pr, smem, stage, r0, a0 + (k + 4) * a_kstride, w0 + (k + 4) * w_kstride);
+        stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
+        wait_lgkm0();
+        producer_barrier();
+        reg_step<C>(pr, smem, stage, r1, a0 + (k + 5) * a_kstride, w0 + (k + 5) * w_kstride);
+        stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
+        wait_lgkm0();
+        producer_barrier();
+    }
+    for (; k < ns; k += 2) {
+        if (k + 2 < ns) {
+            pr.store_a(r0.a, smem, stage);
+            pr.template store_w<false>(r0.w, smem, stage);
+            if (k + 4 < ns) {
+                pr.load_a(r0.a, a0 + (k + 4) * a_kstride);
+                pr.load_w(r0.w, w0 + (k + 4) * w_kstride);
+            }
+        }
+        stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
+        wait_lgkm0();
+        producer_barrier();
+        if (k + 1 < ns) {
+            if (k + 3 < ns) {
+                pr.store_a(r1.a, smem, stage);
+                pr.template store_w<false>(r1.w, smem, stage);
+                if (k + 5 < ns) {
+                    pr.load_a(r1.a, a0 + (k + 5) * a_kstride);
+                    pr.load_w(r1.w, w0 + (k + 5) * w_kstride);
+                }
+            }
+            stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
+            wait_lgkm0();
+            producer_barrier();
+        }
+    }
+}
+
 // EPI: EPI_PLAIN the fp32 store, EPI_RESIDUAL the fp32 store of acc + res,
 // >= 0 the fused GLU of that kind.
 // SPLIT: split-K (p.splits > 1), else one whole tile per workgroup.
@@ -641,8 +863,16 @@ __global__ __launch_bounds__(C::NT, 1) void gemm_kernel(const gemm_params p) {
 
     if (wave >= C::NC / 64) {
         const producer<C> pr(p.a, (int64_t) p.a_kstride * nk, W.w, (int64_t) W.w_kstride * nk, tid - C::NC);
-        produce<C>(pr, smem, (int) ((m0 / ZEST_TILE_ROWS) * ZEST_XTILE_BYTES) + k0 * p.a_kstride,
-                   (int) ((n0 / ZEST_TILE_ROWS) * ZEST_TILE_BYTES) + k0 * W.w_kstride, p.a_kstride, W.w_kstride, ns);
+        // uniform, but the tile arithmetic can leave them in vector registers,
+        // and a load's scalar offset taken from one costs a loop per load
+        const int a0 =
+            __builtin_amdgcn_readfirstlane((int) ((m0 / ZEST_XGROUP_ROWS) * ZEST_XGROUP_BYTES) + k0 * p.a_kstride);
+        const int w0 =
+            __builtin_amdgcn_readfirstlane((int) ((n0 / ZEST_TILE_ROWS) * ZEST_TILE_BYTES) + k0 * W.w_kstride);
+        if constexpr (C::ADIRECT || ZEST_GEMM_AREG)
+            produce_regs<C>(pr, smem, a0, w0, p.a_kstride, W.w_kstride, ns);
+        else
+            produce<C>(pr, smem, a0, w0, p.a_kstride, W.w_kstride, ns);
         return;
     }
 
@@ -660,16 +890,51 @@ __global__ __launch_bounds__(C::NT, 1) void gemm_kernel(const gemm_params p) {
     for (int i = 0; i < C::TI; i++)
 #pragma unroll
         for (int j = 0; j < C::TJ; j++) acc[i][j] = f32x16{};
-    bf16x8 af[2][C::TI], bw[2][C::TJ];
-    __syncthreads();
-    if (ZEST_GEMM_XSTEP) read_frags<C>(af[0], bw[0], smem, fa[0], fw[0]);
-    int cur = 0;
-    for (int k = 0; k < ns; k++) {
-        const int nxt = cur == 2 * C::STAGE ? 0 : cur + C::STAGE;
-        if (!ZEST_GEMM_XSTEP) read_frags<C>(af[0], bw[0], smem, fa[0] + cur, fw[0] + cur);
-        consume<C>(acc, af, bw, smem, fa, fw, cur, nxt, ZEST_GEMM_XSTEP && k + 1 < ns);
-        cur = nxt;
+    if constexpr (C::ADIRECT) {
+        // A two steps ahead in registers; no fence at the barriers, so the
+        // loads stay in flight across them (consumers write no memory here)
+        const a_loader<C> al(p.a, (int64_t) p.a_kstride * nk, wm, lane);
+        const int ks = p.a_kstride;
+        const int a0 =
+            __builtin_amdgcn_readfirstlane((int) ((m0 / ZEST_XGROUP_ROWS) * ZEST_XGROUP_BYTES) + k0 * p.a_kstride);
+        bf16x8 a0s[4][C::TI], a1s[4][C::TI], bw[2][C::TJ];
+        al.load_step(a0s, a0);
+        al.load_step(a1s, a0 + ks);
+        producer_barrier();
+#pragma unroll
+        for (int j = 0; j < C::TJ; j++) bw[0][j] = lds_get(smem, fw[0] + j * 32 * C::ROWB);
+        int cur = 0, k = 0;
+        // pairs of steps without conditions (the loads of steps past the
+        // end read zeros or the next split's slab, and are never used)
+        for (; k + 1 < ns; k += 2) {
+            int nxt = cur == 2 * C::STAGE ? 0 : cur + C::STAGE;
+            consume_direct<C, true>(acc, a0s, bw, smem, fw, cur, nxt, al, a0 + (k + 2) * ks);
+            cur = nxt;
+            producer_barrier();
+            nxt = cur == 2 * C::STAGE ? 0 : cur + C::STAGE;
+            consume_direct<C, true>(acc, a1s, bw, smem, fw, cur, nxt, al, a0 + (k + 3) * ks);
+            cur = nxt;
+            producer_barrier();
+        }
+        if (k < ns) {
+            const int nxt = cur == 2 * C::STAGE ? 0 : cur + C::STAGE;
+            consume_direct<C, false>(acc, a0s, bw, smem, fw, cur, nxt, al, 0);
+            producer_barrier();
+        }
+        // the loads of steps past the end are still in flight
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    } else {
+        bf16x8 af[2][C::TI], bw[2][C::TJ];
         __syncthreads();
+        if (ZEST_GEMM_XSTEP) read_frags<C>(af[0], bw[0], smem, fa[0], fw[0]);
+        int cur = 0;
+        for (int k = 0; k < ns; k++) {
+            const int nxt = cur == 2 * C::STAGE ? 0 : cur + C::STAGE;
+            if (!ZEST_GEMM_XSTEP) read_frags<C>(af[0], bw[0], smem, fa[0] + cur, fw[0] + cur);
+            consume<C>(acc, af, bw, smem, fa, fw, cur, nxt, ZEST_GEMM_XSTEP && k + 1 < ns);
+            cur = nxt;
+            __syncthreads();
+        }
     }
     if (SPLIT && !fixup<C>(acc, p, smem, t, split, wave, lane)) return;
     if constexpr (EPI == EPI_RESIDUAL)
@@ -680,10 +945,11 @@ __global__ __launch_bounds__(C::NT, 1) void gemm_kernel(const gemm_params p) {
         store_glu<C, EPI>(acc, smem, p.xout, p.h, p.ldh, p.M, W.n / 2, m0, n0, wave, wm, wn, lane, p.nonfinite);
 }
 
-// 256x128 tiles (4 consumer waves of 128x64); 128x128 (64x64 each) when the
-// activations have at most 128 rows.
+// 256x128 tiles (4 consumer waves of 64x128, A straight into registers);
+// 128x128 (2x2 waves of 64x64, A staged in LDS) when the activations have at
+// most 128 rows.
 #ifndef ZEST_GEMM_BIG
-#define ZEST_GEMM_BIG 256, 128, 2, 2
+#define ZEST_GEMM_BIG 256, 128, 4, 1, true
 #endif
 #ifndef ZEST_GEMM_SMALL
 #define ZEST_GEMM_SMALL 128, 128, 2, 2
@@ -853,7 +1119,7 @@ gemm_params base_params(const void * a, int64_t M, int64_t K, uint32_t * nonfini
     gemm_params p{};
     p.a = (const uint8_t *) a;
     p.M = M;
-    p.a_kstride = (int) ((zest_rows_padded(M) / ZEST_TILE_ROWS) * ZEST_XTILE_BYTES);
+    p.a_kstride = (int) ((zest_rows_padded(M) / ZEST_XGROUP_ROWS) * ZEST_XGROUP_BYTES);
     p.nk = (int) (zest_k_padded(K) / ZEST_TILE_K);
     p.nonfinite = nonfinite;
     return p;

@@ -66,17 +66,14 @@ __device__ inline void pack4_expanded(uint8_t * packed, int64_t R_pad, int64_t r
             (int32_t) __builtin_amdgcn_fmed3f(__builtin_rintf(__builtin_ldexpf(v[q], sh)), -128.0f, 127.0f);
         b[q] = __float_as_uint((float) qi * sc) >> 16;  // exact: at most 8 significant bits
     }
-    *reinterpret_cast<uint2 *>(packed + zest_xtile_offset(r / ZEST_TILE_ROWS, c / ZEST_TILE_K, R_pad) +
-                               (r % ZEST_TILE_ROWS) * 128 + (c % ZEST_TILE_K) * 2) =
-        make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
+    *reinterpret_cast<uint2 *>(packed + zest_xoffset(r, c, R_pad)) = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
 }
 
 // Zeroes row r of an expanded operand (d_pad columns): a padding row past the
 // last real row, which the GEMM reads as zero.
 __device__ inline void zero_row_expanded(uint8_t * packed, int64_t R_pad, int64_t r, int64_t d_pad, int lane) {
     for (int64_t c = lane * 4; c < d_pad; c += 256)
-        *reinterpret_cast<uint2 *>(packed + zest_xtile_offset(r / ZEST_TILE_ROWS, c / ZEST_TILE_K, R_pad) +
-                                   (r % ZEST_TILE_ROWS) * 128 + (c % ZEST_TILE_K) * 2) = make_uint2(0, 0);
+        *reinterpret_cast<uint2 *>(packed + zest_xoffset(r, c, R_pad)) = make_uint2(0, 0);
 }
 
 // Rows wider than rms_norm_row_kernel takes: one wave per row, sum of
@@ -172,8 +169,7 @@ __global__ __launch_bounds__(256) void rms_norm_row_kernel(const float * __restr
     const int64_t d_pad = zest_k_padded(d);
     if (r >= rows) {  // a padding row of the packed operand (the whole workgroup takes this branch)
         for (int64_t c = t * 4; c < d_pad; c += 1024)
-            *reinterpret_cast<uint2 *>(packed + zest_xtile_offset(r / ZEST_TILE_ROWS, c / ZEST_TILE_K, R_pad) +
-                                       (r % ZEST_TILE_ROWS) * 128 + (c % ZEST_TILE_K) * 2) = make_uint2(0, 0);
+            *reinterpret_cast<uint2 *>(packed + zest_xoffset(r, c, R_pad)) = make_uint2(0, 0);
         return;
     }
     const float * xr = x + r * d;

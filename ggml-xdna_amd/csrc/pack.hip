@@ -34,7 +34,8 @@ __device__ inline int64_t dst_row(int64_t r, int gu) { return gu < 0 ? r : (r >>
 // t%16 = 0 and 8, which gather 4 each and store a dword. Rows past M and
 // columns past K become zero blocks.
 // XOUT: write the expanded operand instead (the 4 decoded values as bf16,
-// 8 bytes, at row t/16 of the 2048-byte tile).
+// 8 bytes, in row t/16's 32 bytes of the sub-tile: a wave's store covers four
+// 128-byte runs, one per 16-column quarter).
 template <bool XOUT>
 __global__ __launch_bounds__(256) void pack_act_kernel(const float * __restrict__ x, int64_t M, int64_t K, int64_t ldx,
                                                        uint8_t * __restrict__ dst, int64_t R_pad, int64_t K_pad, int gu) {
@@ -83,7 +84,8 @@ __global__ __launch_bounds__(256) void pack_act_kernel(const float * __restrict_
             // nontemporal: the operand is written once per chunk and read by the GEMMs after
             typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
             const u32x2 bb = {b[0] | (b[1] << 16), b[2] | (b[3] << 16)};
-            __builtin_nontemporal_store(bb, reinterpret_cast<u32x2 *>(dst + zest_xtile_offset(rt, kc, R_pad) + rr * 128 + j * 8));
+            __builtin_nontemporal_store(
+                bb, reinterpret_cast<u32x2 *>(dst + zest_xoffset(rt * ZEST_TILE_ROWS + rr, c0 + j * 4, R_pad)));
         } else {
             uint8_t * tile = dst + zest_tile_offset(rt, kc, R_pad);
             *reinterpret_cast<uint32_t *>(tile + rr * ZEST_TILE_K + j * 4) =
@@ -100,18 +102,21 @@ __global__ __launch_bounds__(256) void pack_act_kernel(const float * __restrict_
 }
 
 // One thread per 16-value unit of a packed operand: its mantissas and two
-// exponent bytes -> 16 bf16 of the expanded operand.
+// exponent bytes -> 16 bf16 of the expanded operand (32 contiguous bytes).
 __global__ __launch_bounds__(256) void expand_act_kernel(const uint8_t * __restrict__ src, uint8_t * __restrict__ dst,
-                                                         int64_t units) {
+                                                         int64_t units, int64_t R_pad) {
     const int64_t u = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     if (u >= units) return;
     const int64_t tile = u / 64, c = u % 64;  // unit c of a tile: row c/4, 16-column quarter c%4
+    const int64_t tiles_per_chunk = R_pad / ZEST_TILE_ROWS;
+    const int64_t r = (tile % tiles_per_chunk) * ZEST_TILE_ROWS + c / 4;
+    const int64_t col = (tile / tiles_per_chunk) * ZEST_TILE_K + (c % 4) * 16;
     const uint8_t * t = src + tile * ZEST_TILE_BYTES;
     const uint4 m = *reinterpret_cast<const uint4 *>(t + c * 16);
     const uint32_t e = *reinterpret_cast<const uint16_t *>(t + ZEST_TILE_MANT + c * 2);
     uint32_t b[8];
     zest::expand16(m, e, b);
-    uint4 * p = reinterpret_cast<uint4 *>(dst + tile * ZEST_XTILE_BYTES + c * 32);
+    uint4 * p = reinterpret_cast<uint4 *>(dst + zest_xoffset(r, col, R_pad));
     p[0] = make_uint4(b[0], b[1], b[2], b[3]);
     p[1] = make_uint4(b[4], b[5], b[6], b[7]);
 }
@@ -499,7 +504,7 @@ int zest_expand_act(const void * src, int64_t M, int64_t K, void * dst, void * s
     ZEST_REQUIRE(aligned(src, 16) && aligned(dst, 16), "zest_expand_act: pointers must be 16-byte aligned");
     const int64_t units = zest_rows_padded(M) * zest_k_padded(K) / 16;
     hipLaunchKernelGGL(expand_act_kernel, dim3((unsigned) ((units + 255) / 256)), dim3(256), 0,
-                       zest::as_stream(stream), (const uint8_t *) src, (uint8_t *) dst, units);
+                       zest::as_stream(stream), (const uint8_t *) src, (uint8_t *) dst, units, zest_rows_padded(M));
     return zest::check_launch("zest_expand_act");
 }
 

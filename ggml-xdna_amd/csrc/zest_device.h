@@ -199,16 +199,16 @@ __device__ inline float glu(int kind, float g, float u) {
 }
 
 // Encodes 16 values (two blocks) and writes them decoded into row r, columns
-// [col, col+16) of an expanded operand (col % 16 == 0): two 16-byte stores of
-// the bf16 values the packed bytes stand for.
+// [col, col+16) of an expanded operand (col % 16 == 0): the 32 contiguous
+// bytes of the row in its sub-tile, as two 16-byte stores of the bf16 values
+// the packed bytes stand for.
 __device__ inline void store_expanded16(uint8_t * xop, int64_t R_pad, int64_t r, int64_t col, const float v[16]) {
     uint4 m;
     const uint32_t e0 = encode8(v, m.x, m.y);
     const uint32_t e1 = encode8(v + 8, m.z, m.w);
     uint32_t b[8];
     expand16(m, e0 | (e1 << 8), b);
-    uint4 * p = reinterpret_cast<uint4 *>(xop + zest_xtile_offset(r / ZEST_TILE_ROWS, col / ZEST_TILE_K, R_pad) +
-                                          (r % ZEST_TILE_ROWS) * 128 + (col % ZEST_TILE_K) * 2);
+    uint4 * p = reinterpret_cast<uint4 *>(xop + zest_xoffset(r, col, R_pad));
     p[0] = make_uint4(b[0], b[1], b[2], b[3]);
     p[1] = make_uint4(b[4], b[5], b[6], b[7]);
 }

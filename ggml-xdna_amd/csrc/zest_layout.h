@@ -24,11 +24,17 @@
 // The GEMM's activation operand ("expanded" layout) holds the same bfp16
 // blocks already decoded, each value q * 2^(e-133) as the bf16 it is exactly
 // (a signed 8-bit mantissa times a power of two fits a bf16 significand):
-// rows padded to 256 and columns to 64 as above, tiles of 16 rows x 64
-// columns of 2048 bytes, tile (rt, kc) at byte (kc * R_pad/16 + rt) * 2048,
-// each tile row 128 bytes (8 blocks of 16 bytes). The activation packers
-// write it directly, so every activation value is expanded once rather than
-// once per output tile of the GEMM.
+// rows padded to 256 and columns to 64 as above, cut into sub-tiles of 32
+// rows x 16 columns (1 KB; a row's 16 values, two blocks, are 32 contiguous
+// bytes), ordered [64-column chunk][32-row group][16-column quarter]:
+// element (r, c) is at byte
+//   ((c/64 * R_pad/32 + r/32) * 4 + (c%64)/16) * 1024 + (r%32) * 32 + (c%16) * 2.
+// A sub-tile is exactly the A operand of one 32x32x16 MFMA (lane l: row l%32,
+// columns 8(l/32)..8(l/32)+7, the 16 bytes at 32(l%32) + 16(l/32)), so a wave
+// loads it with one instruction covering 1 KB contiguous, and a K-step (64
+// columns) of 256 rows is one contiguous 32 KB run. The activation packers write it directly, so
+// every activation value is expanded once rather than once per output tile
+// of the GEMM.
 #pragma once
 
 #include <stdint.h>
@@ -38,7 +44,9 @@
 #define ZEST_TILE_MANT 1024
 #define ZEST_TILE_BYTES 1152
 #define ZEST_ROW_ALIGN 256
-#define ZEST_XTILE_BYTES 2048
+#define ZEST_XGROUP_ROWS 32    // rows of an expanded sub-tile
+#define ZEST_XSUB_BYTES 1024   // an expanded sub-tile: 32 rows x 16 columns
+#define ZEST_XGROUP_BYTES 4096 // the four sub-tiles of a 32-row group in one 64-column chunk
 
 #ifdef __HIPCC__
 #define ZEST_HD __host__ __device__ inline
@@ -55,9 +63,10 @@ ZEST_HD int64_t zest_tile_offset(int64_t rt, int64_t kc, int64_t R_pad) {
     return (kc * (R_pad / ZEST_TILE_ROWS) + rt) * ZEST_TILE_BYTES;
 }
 
-// Byte offset of tile (rt, kc) of an expanded operand of R_pad rows.
-ZEST_HD int64_t zest_xtile_offset(int64_t rt, int64_t kc, int64_t R_pad) {
-    return (kc * (R_pad / ZEST_TILE_ROWS) + rt) * ZEST_XTILE_BYTES;
+// Byte offset of element (r, c) of an expanded operand of R_pad rows.
+ZEST_HD int64_t zest_xoffset(int64_t r, int64_t c, int64_t R_pad) {
+    return ((c / ZEST_TILE_K) * (R_pad / ZEST_XGROUP_ROWS) + r / ZEST_XGROUP_ROWS) * ZEST_XGROUP_BYTES +
+           ((c % ZEST_TILE_K) / 16) * ZEST_XSUB_BYTES + (r % ZEST_XGROUP_ROWS) * 32 + (c % 16) * 2;
 }
 
 // Where block cb (columns 8cb..8cb+7) of row r lives: its exponent byte and
