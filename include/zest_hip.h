@@ -87,7 +87,8 @@ ZEST_API int zest_pack_act(const float *x, int64_t M, int64_t K, int64_t ldx, vo
 
 /* The same pack, written as the GEMM's activation operand: every bfp16 block
  * stored decoded, each value as the bf16 it is exactly (zest_act_bytes(M, K)
- * bytes; the tile layout with 2-byte values). Equals zest_expand_act of
+ * bytes, in 32-row x 16-column sub-tiles laid out as the GEMM's MFMA reads
+ * them: zest_layout.h). Equals zest_expand_act of
  * zest_pack_act's bytes. Replaces the same reference functions: the NPU
  * expands its bfp16 operands inside the kernel, here the activations are
  * expanded once when packed. */
