@@ -231,6 +231,24 @@ def test_convert_gu_every_type_is_the_interleaved_pair(zest_gpu, oracle, name):
     assert np.array_equal(bp[dst], bg) and np.array_equal(bp[dst + 32], bu)
 
 
+@pytest.mark.parametrize("name", ["q8_0", "q4_0", "q5_0", "q3_K", "q6_K"])
+def test_convert_two_byte_aligned_rows(zest_gpu, oracle, name):
+    # the types whose rows need only 2-byte alignment, from a buffer that
+    # starts 2 bytes past a 4-byte boundary: the converter's aligned loads
+    # then start before the buffer (inside the allocation) and must neither
+    # read past its end nor take bytes of the neighbouring block
+    import torch
+    wtype = GGUF[name]
+    for N, K in ([(37, 96), (5, 32)] if wtype not in K_QUANTS else [(37, 256)]):
+        raw = random_gguf(oracle, wtype, N, K, seed=wtype + N)
+        want = oracle.encode_rows(oracle.dequant(wtype, raw, N, K))
+        buf = torch.zeros(raw.size + 16, dtype=torch.uint8, device="cuda")
+        buf[2:2 + raw.size] = torch.from_numpy(raw.reshape(-1)).cuda()
+        out = zest_gpu.convert_weight(wtype, buf[2:2 + raw.size], N, K)
+        torch.cuda.synchronize()
+        assert np.array_equal(zest_gpu.tiles_to_blocks(out.cpu().numpy(), N, K), want), (name, N, K)
+
+
 def test_convert_rejects_bad_rows(zest_gpu, oracle):
     import torch
     raw = torch.zeros(4096, dtype=torch.uint8, device="cuda")
