@@ -4,22 +4,22 @@
 //
 // Per workgroup a BM x BN output tile, in K-steps of 64 (one tile-layout
 // column chunk), by two kinds of waves:
-//   * producer waves copy the A slab (bf16) from memory straight into LDS
-//     (buffer loads with the LDS-DMA bit), and load the W slab (bfp16 units:
-//     16 mantissas + their 2 exponent bytes), expand the W units losslessly to
-//     bf16 (zest::expand16) and store them into LDS; LDS rows are 64 bf16
-//     with the 16-byte chunks XOR-swizzled by row so the stores and the MFMA
-//     fragment reads are free of bank conflicts;
-//   * consumer waves read fragments from LDS and run
-//     v_mfma_f32_32x32x16_bf16, each lane's eight K values of an operand
-//     exactly one bfp16 block, accumulating in fp32.
+//   * producer waves load the W slab (bfp16 units: 16 mantissas + their 2
+//     exponent bytes) two steps ahead into registers, expand the units
+//     losslessly to bf16 (zest::expand16) and store them into a ring of three
+//     LDS stages; LDS rows are 64 bf16 with the 16-byte chunks XOR-swizzled by
+//     row so the stores and the fragment reads are free of bank conflicts;
+//   * consumer waves (CWM of them, each WM rows by all BN columns) load their
+//     A fragments straight from memory into registers, two steps ahead (the
+//     expanded layout holds each fragment as one contiguous 1 KB), read the W
+//     fragments from LDS and run v_mfma_f32_32x32x16_bf16, each lane's eight
+//     K values of an operand exactly one bfp16 block, accumulating in fp32.
 // One consumer and one producer wave share each SIMD, so the producer's
-// expansion and the consumer's MFMAs issue side by side. Three LDS stages:
-// while the consumers work on step k, the producers fill step k+2, and step
-// k+1 is complete, so the consumers read its first fragments before step k
-// ends. One barrier per K-step. The store is fp32 row-major, as the
-// reference's output mode 0 (kernels/bfp16_gemm/aie_kernels/aie2p/
-// mm_bfp_acc.cc:106-116, 258-278).
+// expansion and the consumer's MFMAs issue side by side. While the consumers
+// work on step k, the producers fill step k+2, and step k+1 is complete, so
+// the consumers read its first fragments before step k ends. One barrier per
+// K-step. The store is fp32 row-major, as the reference's output mode 0
+// (kernels/bfp16_gemm/aie_kernels/aie2p/mm_bfp_acc.cc:106-116, 258-278).
 #include <algorithm>
 #include <map>
 #include <mutex>
@@ -34,12 +34,6 @@
 #ifndef ZEST_GEMM_GROUP_M
 #define ZEST_GEMM_GROUP_M 4  // tile rows per group of the tile order
 #endif
-#ifndef ZEST_GEMM_AREG
-#define ZEST_GEMM_AREG 1  // producers stage the A slab through registers, two steps ahead (else LDS DMA, one step)
-#endif
-#ifndef ZEST_GEMM_XSTEP
-#define ZEST_GEMM_XSTEP 1  // consumers read a step's first fragments before the barrier that starts it
-#endif
 
 namespace {
 
@@ -50,30 +44,25 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// BM x BN tile; CWM x CWN consumer waves, each a WM x WN block of 32x32 MFMA
-// tiles; as many producer waves. ADIRECT: the consumers load their A
-// fragments from memory straight into registers and LDS holds W alone; else
-// the producers stage the A slab in LDS too.
-template <int BM_, int BN_, int CWM_, int CWN_, bool ADIRECT_ = false>
+// BM x BN tile; CWM consumer waves, each a WM x BN block of 32x32 MFMA tiles
+// (TI x TJ of them); as many producer waves. LDS holds the expanded W ring;
+// after the K loop each consumer wave uses WM x BN floats of it for its
+// epilogue.
+template <int BM_, int BN_, int CWM_>
 struct gemm_cfg {
-    static constexpr int BM = BM_, BN = BN_, CWM = CWM_, CWN = CWN_;
-    static constexpr bool ADIRECT = ADIRECT_;
-    static constexpr int NC = 64 * CWM * CWN;  // consumer threads
-    static constexpr int NP = NC;              // producer threads
+    static constexpr int BM = BM_, BN = BN_, CWM = CWM_, CWN = 1;
+    static constexpr int NC = 64 * CWM;  // consumer threads
+    static constexpr int NP = NC;        // producer threads
     static constexpr int NT = NC + NP;
-    static constexpr int WM = BM / CWM, WN = BN / CWN;
+    static constexpr int WM = BM / CWM, WN = BN;
     static constexpr int TI = WM / 32, TJ = WN / 32;
-    static constexpr int AC = BM * 8 / NP;  // A chunks (16 B = one block) per producer thread per K-step
     static constexpr int BU = BN * 4 / NP;  // W units (two blocks) per producer thread per K-step
     static constexpr int ROWB = 128;        // LDS bytes per row (64 bf16)
-    static constexpr int A_BYTES = ADIRECT ? 0 : BM * ROWB;  // a stage: A rows, then W rows
-    static constexpr int STAGE = A_BYTES + BN * ROWB;
+    static constexpr int STAGE = BN * ROWB;
     static constexpr int STAGES = 3;
-    // the ring, or the epilogues' per-wave regions (WM x WN floats each)
     static constexpr size_t LDS_BYTES =
         (size_t) STAGES * STAGE > (size_t) BM * BN * 4 ? (size_t) STAGES * STAGE : (size_t) BM * BN * 4;
-    static constexpr int A_STEP = NP * 16;                     // bytes between a thread's A chunks
-    static_assert(BM * 8 % NP == 0 && BN * 4 % NP == 0, "work must divide evenly");
+    static_assert(BN * 4 % NP == 0, "work must divide evenly");
     static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be whole 32x32 MFMA tiles");
 };
 
@@ -85,17 +74,6 @@ struct gemm_cfg {
 __device__ inline int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
 __device__ inline void lds_put(uint8_t * smem, int off, uint4 v) { *reinterpret_cast<uint4 *>(smem + off) = v; }
-
-// The same store, opaque to the compiler's wait-count tracking: it would
-// otherwise make the store wait for every LDS DMA in flight (it cannot tell
-// that they write other bytes). Used only by producer waves, which never read
-// LDS; the barrier that publishes a stage waits for all LDS traffic.
-__device__ inline void lds_put_async(uint8_t * smem, int off, uint4 v) {
-    const uint32_t a = (uint32_t) reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t *) (smem + off));
-    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    const u32x4 d = {v.x, v.y, v.z, v.w};
-    asm volatile("ds_write_b128 %0, %1" ::"v"(a), "v"(d) : "memory");
-}
 
 __device__ inline bf16x8 lds_get(const uint8_t * smem, int off) {
     return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(smem + off));
@@ -115,93 +93,33 @@ struct stage_regs {
 
 typedef __attribute__((address_space(3))) void * lds_ptr_t;
 
-// s_waitcnt vmcnt(0) lgkmcnt(0): every load, DMA and LDS store of this wave done
-#define ZEST_WAIT_ALL() __builtin_amdgcn_s_waitcnt(7 << 4)
-
-// s_waitcnt vmcnt(VM) lgkmcnt(0): all but the last VM memory loads (LDS DMA
-// included; they complete in issue order) and every LDS store of this wave
-// done. (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8.)
-template <int VM>
-__device__ inline void wait_vm_lgkm0() {
-    static_assert(VM >= 0 && VM < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4));
-}
-
-// The producer side. Loads go through buffer resources: the slab's byte
+// The producer side. W loads go through a buffer resource: the slab's byte
 // offset is wave-uniform (a scalar offset), the lane's place in it a fixed
-// vector offset, and a read past the operand returns zeros.
-//   A: the K-step's A slab (BM rows of 64 columns) is one contiguous run
-//      (BM/32 consecutive 4 KB groups of the expanded layout). By LDS DMA
-//      (buffer_load ... lds), instruction j of the step fills LDS rows
-//      8j..8j+7, lane l writing the 16 bytes at 16*l, i.e. row 8j + l/8,
-//      position l%8; lane l reads the chunk that belongs at that position,
-//      (l%8) ^ swz(row), wherever the layout puts it. Through registers, lane
-//      l of wave pw reads the slab's bytes in order (sub-tile pw of group i:
-//      row 32i + l/2, chunk 2pw + l%2) and stores them swizzled.
-//   W: thread p takes two adjacent units of tile p/32 of the W slab: row
-//      p%16, column quarters 2h and 2h+1 with h = p/16%2, i.e. 32 contiguous
-//      mantissa bytes (two 16-byte loads) and 4 contiguous exponent bytes
-//      (one 4-byte load: the address unit costs the same per instruction
-//      whatever its width). 16 consecutive lanes are 16 consecutive rows,
-//      for the swizzled stores. Loaded a step ahead, expanded, stored.
+// vector offset, and a read past the operand returns zeros. Thread p takes
+// two adjacent units of tile p/32 of the W slab: row p%16, column quarters 2h
+// and 2h+1 with h = p/16%2, i.e. 32 contiguous mantissa bytes (two 16-byte
+// loads) and 4 contiguous exponent bytes (one 4-byte load). 16 consecutive
+// lanes are 16 consecutive rows, for the swizzled stores.
 template <class C>
 struct producer {
     static constexpr int NPW = C::NP / 64;          // producer waves
-    static constexpr int AI = C::ADIRECT ? 1 : C::BM / 8 / NPW;  // A instructions per producer wave per K-step
     static constexpr int WI = 3;                    // W load instructions per K-step (load_w)
     static_assert(C::BU == 2 && C::NP / 32 == C::BN / 16, "two W units per producer thread, 32 threads a tile");
-    static_assert(C::ADIRECT || NPW == 4, "the A slab's rows map to four producer waves");
-    __amdgpu_buffer_rsrc_t ra, rw;
-    int pw;                // producer wave
-    int va, vwm, vwe;      // lane offsets: A chunk, W mantissas, W exponents
-    int vla, sta;          // A through registers: the lane's chunk in the slab, its LDS offset
+    __amdgpu_buffer_rsrc_t rw;
+    int vwm, vwe;          // lane offsets: W mantissas, W exponents
     int stw[2][2];         // LDS offsets of the two W units' two chunks each
 
-    __device__ producer(const uint8_t * A, int64_t a_bytes, const uint8_t * W, int64_t w_bytes, int p) {
-        ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(A), (short) 0, (int) a_bytes, 0x00020000);
+    __device__ producer(const uint8_t * W, int64_t w_bytes, int p) {
         rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(W), (short) 0, (int) w_bytes, 0x00020000);
-        pw = __builtin_amdgcn_readfirstlane(p >> 6);
-        const int l = p & 63;
-        // DMA instruction j = i*NPW + pw fills LDS rows 32i + 8pw + l/8 (NPW = 4):
-        // j and pw have the same parity, so swz(8j + l/8) is the same for every
-        // i, and the source row's place in its 32-row group is 8pw + l/8
-        const int ca = (l & 7) ^ swz(8 * (pw & 1) + (l >> 3));
-        va = (ca >> 1) * ZEST_XSUB_BYTES + (8 * pw + (l >> 3)) * 32 + (ca & 1) * 16;
-        // through registers: slab bytes in order, stored swizzled
-        vla = pw * 1024 + l * 16;
-        sta = (l >> 1) * C::ROWB + ((2 * pw + (l & 1)) ^ swz(l >> 1)) * 16;
         const int t = p >> 5, row = p & 15, h = (p >> 4) & 1;
         vwm = t * ZEST_TILE_BYTES + row * ZEST_TILE_K + h * 32;
         vwe = t * ZEST_TILE_BYTES + ZEST_TILE_MANT + row * 8 + h * 4;
         const int wrow = t * 16 + row, sw = swz(wrow);
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            stw[i][0] = C::A_BYTES + wrow * C::ROWB + ((4 * h + 2 * i) ^ sw) * 16;
-            stw[i][1] = C::A_BYTES + wrow * C::ROWB + ((4 * h + 2 * i + 1) ^ sw) * 16;
+            stw[i][0] = wrow * C::ROWB + ((4 * h + 2 * i) ^ sw) * 16;
+            stw[i][1] = wrow * C::ROWB + ((4 * h + 2 * i + 1) ^ sw) * 16;
         }
-    }
-
-    // The A slab at byte a_off into the stage at byte `stage` of LDS:
-    // instructions [i0, i0 + n) of its AI.
-    __device__ void dma_a(uint8_t * smem, int stage, int a_off, int i0 = 0, int n = AI) const {
-#pragma unroll
-        for (int i = i0; i < i0 + n; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t) (smem + stage + (i * NPW + pw) * 1024), 16, va,
-                                                     a_off + i * NPW * 1024, 0, 0);
-    }
-
-    // A chunks [i0, i0 + n) of the slab at byte a_off, into registers; chunk
-    // i is row 32i + l/2, chunk 2pw + l%2 of the slab.
-    __device__ void load_a(uint4 (&a)[AI], int a_off, int i0 = 0, int n = AI) const {
-        if constexpr (C::ADIRECT) return;
-#pragma unroll
-        for (int i = i0; i < i0 + n; i++) a[i] = load16(ra, vla + i * NPW * 1024, a_off);
-    }
-
-    __device__ void store_a(const uint4 (&a)[AI], uint8_t * smem, int stage, int i0 = 0, int n = AI) const {
-        if constexpr (C::ADIRECT) return;
-#pragma unroll
-        for (int i = i0; i < i0 + n; i++) lds_put(smem, stage + sta + i * NPW * 1024, a[i]);
     }
 
     __device__ void load_w(stage_regs<C> & st, int w_off) const {
@@ -212,33 +130,23 @@ struct producer {
 
     // W unit i of a step, by the branch-free fast expansion, stored; true if
     // the unit needs the general expansion (store_w_general) instead.
-    // ASYNC: stores opaque to the compiler's wait counting (beside LDS DMA).
-    template <bool ASYNC = true>
     __device__ bool store_w_unit(const stage_regs<C> & st, int i, uint8_t * smem, int stage) const {
         uint32_t b[8];
         const bool slow = zest::expand16_fast(st.wm[i], i ? st.we >> 16 : st.we & 0xffffu, b);
-        put<ASYNC>(smem, stw[i][0] + stage, make_uint4(b[0], b[1], b[2], b[3]));
-        put<ASYNC>(smem, stw[i][1] + stage, make_uint4(b[4], b[5], b[6], b[7]));
+        lds_put(smem, stw[i][0] + stage, make_uint4(b[0], b[1], b[2], b[3]));
+        lds_put(smem, stw[i][1] + stage, make_uint4(b[4], b[5], b[6], b[7]));
         return slow;
     }
 
-    template <bool ASYNC>
-    static __device__ void put(uint8_t * smem, int off, uint4 v) {
-        if (ASYNC)
-            lds_put_async(smem, off, v);
-        else
-            lds_put(smem, off, v);
-    }
 
     // Every unit of the step by the general expansion, stored.
-    template <bool ASYNC = true>
     __device__ void store_w_general(const stage_regs<C> & st, uint8_t * smem, int stage) const {
 #pragma unroll
         for (int i = 0; i < C::BU; i++) {
             uint32_t b[8];
             zest::expand16(st.wm[i], i ? st.we >> 16 : st.we & 0xffffu, b);
-            put<ASYNC>(smem, stw[i][0] + stage, make_uint4(b[0], b[1], b[2], b[3]));
-            put<ASYNC>(smem, stw[i][1] + stage, make_uint4(b[4], b[5], b[6], b[7]));
+            lds_put(smem, stw[i][0] + stage, make_uint4(b[0], b[1], b[2], b[3]));
+            lds_put(smem, stw[i][1] + stage, make_uint4(b[4], b[5], b[6], b[7]));
         }
     }
 
@@ -246,54 +154,15 @@ struct producer {
     // first unit's). The units take the branch-free fast expansion; a unit
     // whose exponent bytes need the general one is redone behind a single
     // wave-uniform branch, which real weights almost never take.
-    template <bool ASYNC = true>
     __device__ void store_w(const stage_regs<C> & st, uint8_t * smem, int stage) const {
         bool slow = false;
 #pragma unroll
-        for (int i = 0; i < C::BU; i++) slow |= store_w_unit<ASYNC>(st, i, smem, stage);
-        if (__builtin_expect(__any(slow), 0)) store_w_general<ASYNC>(st, smem, stage);
+        for (int i = 0; i < C::BU; i++) slow |= store_w_unit(st, i, smem, stage);
+        if (__builtin_expect(__any(slow), 0)) store_w_general(st, smem, stage);
     }
 };
 
-template <class C>
-__device__ inline void read_frags(bf16x8 (&af)[C::TI], bf16x8 (&bw)[C::TJ], const uint8_t * smem, int fa, int fw) {
-#pragma unroll
-    for (int i = 0; i < C::TI; i++) af[i] = lds_get(smem, fa + i * 32 * C::ROWB);
-#pragma unroll
-    for (int j = 0; j < C::TJ; j++) bw[j] = lds_get(smem, fw + j * 32 * C::ROWB);
-}
-
-// One K-step of a consumer wave on the stage at byte `cur`: 4 sub-steps of 16
-// K. The fragments of the next sub-step (sub-step 0 of stage `nxt` after the
-// last, if `more`) are read while this sub-step's MFMAs run; the scheduling
-// barriers keep those reads ahead of the MFMAs, so the two fragment sets live
-// in separate registers.
-template <class C>
-__device__ inline void consume(f32x16 (&acc)[C::TI][C::TJ], bf16x8 (&af)[2][C::TI], bf16x8 (&bw)[2][C::TJ],
-                               const uint8_t * smem, const int (&fa)[4], const int (&fw)[4], int cur, int nxt,
-                               bool more) {
-#pragma unroll
-    for (int s = 0; s < 4; s++) {
-        if (s < 3)
-            read_frags<C>(af[(s + 1) & 1], bw[(s + 1) & 1], smem, fa[s + 1] + cur, fw[s + 1] + cur);
-        else if (more)
-            read_frags<C>(af[0], bw[0], smem, fa[0] + nxt, fw[0] + nxt);
-#pragma unroll
-        for (int i = 0; i < C::TI; i++)
-#pragma unroll
-            for (int j = 0; j < C::TJ; j++)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s & 1][i], bw[s & 1][j], acc[i][j], 0, 0, 0);
-        constexpr int R = C::TI + C::TJ, P = C::TI * C::TJ;
-#pragma unroll
-        for (int q = 0; q < P; q++) {
-            if (q < R) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // a fragment read
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);              // an MFMA
-        }
-    }
-}
-
-// ADIRECT consumers: the A fragments come from memory straight into
-// registers. Fragment i of sub-step s is sub-tile s of the 32-row group
+// The consumers' A fragments come from memory straight into registers. Fragment i of sub-step s is sub-tile s of the 32-row group
 // wm*WM/32 + i of the tile's K-step slab: lane l takes row l%32, chunk
 // 2s + l/32 (one block as bf16, the MFMA's A operand), the 16 bytes at
 // 32(l%32) + 16(l/32), so the wave's load covers one contiguous 1 KB. A load
@@ -324,7 +193,7 @@ struct a_loader {
     }
 };
 
-// One K-step of an ADIRECT consumer wave: A from registers `a` (this step's,
+// One K-step of a consumer wave: A from registers `a` (this step's,
 // loaded two steps ago), W fragments from the stage at `cur`, read a
 // sub-step ahead (sub-step 0 of stage `nxt` during the last). As each
 // sub-step's MFMAs are issued, its A registers are reloaded with the same
@@ -332,7 +201,7 @@ struct a_loader {
 // steps to land. The scheduling groups interleave the W reads and A loads
 // with the MFMAs.
 template <class C, bool LOAD>
-__device__ inline void consume_direct(f32x16 (&acc)[C::TI][C::TJ], bf16x8 (&a)[4][C::TI], bf16x8 (&bw)[2][C::TJ],
+__device__ inline void consume(f32x16 (&acc)[C::TI][C::TJ], bf16x8 (&a)[4][C::TI], bf16x8 (&bw)[2][C::TJ],
                                       const uint8_t * smem, const int (&fw)[4], int cur, int nxt,
                                       const a_loader<C> & al, int a_next) {
 #pragma unroll
@@ -616,212 +485,88 @@ __device__ inline bool fixup(f32x16 (&acc)[C::TI][C::TJ], const gemm_params & p,
     return true;
 }
 
-// The producer's barrier: no fence, so the compiler adds no wait of its own
-// (a workgroup fence would wait for every LDS DMA in flight); the waits it
-// needs are explicit before it.
-__device__ inline void producer_barrier() {
+// The workgroup barrier without a fence: no wave writes global memory in the
+// K loop, and a fence would make the compiler wait for every load in flight;
+// the LDS waits a barrier needs are explicit before it.
+__device__ inline void bare_barrier() {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 }
 
-// One steady-state producer step: the A slab into `stage` by DMA, the W
-// units in `cur` (loaded a step ago) expanded and stored into it, and the
-// next step's W units loaded into `nxt`. The four producer waves of a CU
-// share its address unit, which takes about 16 cycles per load instruction
-// (a wave's A DMA alone is ~500 cycles of it), so the DMA instructions go
-// out in groups between the units' expansions: the address unit works
-// through one group while the wave expands. The scheduling barriers keep
-// that order. The W loads go last, so they are the loads the step may leave
-// in flight.
-template <class C>
-__device__ inline void steady_step(const producer<C> & pr, uint8_t * smem, int stage, int a_off,
-                                   const stage_regs<C> & cur, stage_regs<C> & nxt, int w_off_next) {
-    constexpr int AI = producer<C>::AI, PER = AI / C::BU;
-    static_assert(AI % C::BU == 0, "A instructions must split evenly between W units");
-    bool slow = false;
-#pragma unroll
-    for (int u = 0; u < C::BU; u++) {
-        pr.dma_a(smem, stage, a_off, u * PER, PER);
-        __builtin_amdgcn_sched_barrier(0);
-        slow |= pr.store_w_unit(cur, u, smem, stage);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    pr.load_w(nxt, w_off_next);
-    if (__builtin_expect(__any(slow), 0)) pr.store_w_general(cur, smem, stage);
-}
-
-// The producer's part of one tile over K-steps [k0, k0 + ns). During step k,
-// step k+2 goes into stage (k+2)%3: first its A slab by DMA, then step k+3's
-// W units are requested, then step k+2's W units (requested during step k+1)
-// are expanded and stored. Before the barrier that ends step k it waits only
-// for what the consumers need after it; loads issued in the step and not
-// needed yet stay in flight (they complete in issue order):
-//   ZEST_GEMM_XSTEP 1: the consumers read the first fragments of step k+1
-//     before that barrier, so stage (k+2)%3 is read during step k+1: the
-//     step's A DMA completes, its W loads (for step k+3) stay in flight;
-//   ZEST_GEMM_XSTEP 0: stage (k+1)%3, filled during step k-1, is the only one
-//     read next: the step's A DMA and W loads both stay in flight.
-// The steady state runs without conditions, so the compiler counts the
-// loads in flight exactly; the last steps take full waits. The barriers
-// match the consumer's, step for step.
-template <class C>
-__device__ inline void produce(const producer<C> & pr, uint8_t * smem, int a0, int w0, int a_kstride, int w_kstride,
-                               int ns) {
-    constexpr int AI = producer<C>::AI, WI = producer<C>::WI;  // VMEM instructions per step: A DMA, W loads
-    constexpr int FLY = ZEST_GEMM_XSTEP ? WI : AI + WI;
-    stage_regs<C> s0, s1;
-    pr.dma_a(smem, 0, a0);
-    pr.load_w(s0, w0);
-    if (ns > 1) {
-        pr.dma_a(smem, C::STAGE, a0 + a_kstride);
-        pr.load_w(s1, w0 + w_kstride);
-    }
-    pr.store_w(s0, smem, 0);
-    if (ns > 2) pr.load_w(s0, w0 + 2 * w_kstride);
-    if (ns > 1) pr.store_w(s1, smem, C::STAGE);
-    // stages 0 and 1 complete; step 2's W loads may stay in flight
-    if (ns > 2)
-        wait_vm_lgkm0<WI>();
-    else
-        ZEST_WAIT_ALL();
-    producer_barrier();
-    int stage = 2 * C::STAGE, k = 0;
-    for (; k + 4 < ns; k += 2) {
-        steady_step<C>(pr, smem, stage, a0 + (k + 2) * a_kstride, s0, s1, w0 + (k + 3) * w_kstride);
-        stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
-        wait_vm_lgkm0<FLY>();
-        producer_barrier();
-        steady_step<C>(pr, smem, stage, a0 + (k + 3) * a_kstride, s1, s0, w0 + (k + 4) * w_kstride);
-        stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
-        wait_vm_lgkm0<FLY>();
-        producer_barrier();
-    }
-    for (; k < ns; k += 2) {
-        if (k + 2 < ns) {
-            pr.dma_a(smem, stage, a0 + (k + 2) * a_kstride);
-            if (k + 3 < ns) pr.load_w(s1, w0 + (k + 3) * w_kstride);
-            pr.store_w(s0, smem, stage);
-        }
-        stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
-        ZEST_WAIT_ALL();
-        producer_barrier();
-        if (k + 1 < ns) {
-            if (k + 3 < ns) {
-                pr.dma_a(smem, stage, a0 + (k + 3) * a_kstride);
-                if (k + 4 < ns) pr.load_w(s0, w0 + (k + 4) * w_kstride);
-                pr.store_w(s1, smem, stage);
-            }
-            stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
-            ZEST_WAIT_ALL();
-            producer_barrier();
-        }
-    }
-}
-
-// One K-step's loads, held in a producer thread's registers.
-template <class C>
-struct step_regs {
-    uint4 a[producer<C>::AI];
-    stage_regs<C> w;
-};
-
 // s_waitcnt lgkmcnt(0) alone: this wave's LDS stores done, loads left in flight
+// (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
 __device__ inline void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
-// One steady-state step of the register producer: step j's A chunks and W
-// units (loaded two steps ago) stored into `stage`, step j+2's requested into
-// the same registers. The A chunks go out in groups between the W units'
-// expansions, each group's loads right after its stores, so the address unit
-// works while the wave expands.
+// One steady-state producer step: step j's W units (loaded two steps ago)
+// expanded and stored into `stage`, step j+2's requested into the same
+// registers. A unit whose exponent bytes need the general expansion is
+// redone behind one wave-uniform branch, which real weights almost never take.
 template <class C>
-__device__ inline void reg_step(const producer<C> & pr, uint8_t * smem, int stage, step_regs<C> & r, int a_off_next,
-                                int w_off_next) {
-    constexpr int AI = producer<C>::AI, PER = C::ADIRECT ? 0 : AI / C::BU;
-    static_assert(C::ADIRECT || AI % C::BU == 0, "A chunks must split evenly between W units");
+__device__ inline void produce_step(const producer<C> & pr, uint8_t * smem, int stage, stage_regs<C> & r,
+                                   int w_off_next) {
     bool slow = false;
 #pragma unroll
     for (int u = 0; u < C::BU; u++) {
-        pr.store_a(r.a, smem, stage, u * PER, PER);
-        pr.load_a(r.a, a_off_next, u * PER, PER);
-        __builtin_amdgcn_sched_barrier(0);
-        slow |= pr.template store_w_unit<false>(r.w, u, smem, stage);
+        slow |= pr.store_w_unit(r, u, smem, stage);
         __builtin_amdgcn_sched_barrier(0);
     }
-    if (__builtin_expect(__any(slow), 0)) pr.template store_w_general<false>(r.w, smem, stage);
-    pr.load_w(r.w, w_off_next);
+    if (__builtin_expect(__any(slow), 0)) pr.store_w_general(r, smem, stage);
+    pr.load_w(r, w_off_next);
 }
 
-// The producer with the A slab staged through registers: step j's A chunks
-// and W units are loaded during step j-4 and stored into stage j%3 during
-// step j-2, so a load has two steps to land where the LDS DMA has one (the
-// consumers read step j+1's first fragments before the barrier that ends
-// step j, so a stage must be complete a step before it is consumed, and it is
-// free only after the step that last read it). All loads go into registers
-// and every LDS store is the compiler's own, so the compiler counts the loads
-// in flight and waits for exactly those whose registers a store reads; before
-// a barrier only the LDS stores are waited for. The steady state runs without
-// conditions; the last steps do their remaining stores one by one.
+// The producer's part of one tile over K-steps [k0, k0 + ns): step j's W
+// units are loaded during step j-4 and stored into stage j%3 during step j-2
+// (the consumers read step j+1's first fragments before the barrier that
+// ends step j, so a stage must be complete a step before it is consumed, and
+// it is free only after the step that last read it). Every load goes into
+// registers and every LDS store is the compiler's own, so the compiler counts
+// the loads in flight and waits for exactly those whose registers a store
+// reads; before a barrier only the LDS stores are waited for. Steps 0-3 are
+// requested whether or not they exist (a load past the operand returns zeros,
+// one past this split's steps reads the next split's slab, and neither is
+// stored), so the steady state starts with an exact count; it runs without
+// conditions, and the last steps do their remaining stores one by one. The
+// barriers match the consumers', step for step.
 template <class C>
-__device__ inline void produce_regs(const producer<C> & pr, uint8_t * smem, int a0, int w0, int a_kstride,
-                                    int w_kstride, int ns) {
-    // Steps 0-3 are requested whether or not they exist: a load past the
-    // operand returns zeros, one past this split's steps reads the next
-    // split's slab, and neither is stored. Unconditional loads keep the
-    // compiler's count of loads in flight exact where the steady state starts.
-    step_regs<C> r0, r1;
-    pr.load_a(r0.a, a0);
-    pr.load_w(r0.w, w0);
-    pr.load_a(r1.a, a0 + a_kstride);
-    pr.load_w(r1.w, w0 + w_kstride);
-    pr.store_a(r0.a, smem, 0);
-    pr.template store_w<false>(r0.w, smem, 0);
-    pr.load_a(r0.a, a0 + 2 * a_kstride);
-    pr.load_w(r0.w, w0 + 2 * w_kstride);
-    if (ns > 1) {
-        pr.store_a(r1.a, smem, C::STAGE);
-        pr.template store_w<false>(r1.w, smem, C::STAGE);
-    }
-    pr.load_a(r1.a, a0 + 3 * a_kstride);
-    pr.load_w(r1.w, w0 + 3 * w_kstride);
+__device__ inline void produce(const producer<C> & pr, uint8_t * smem, int w0, int w_kstride, int ns) {
+    stage_regs<C> r0, r1;
+    pr.load_w(r0, w0);
+    pr.load_w(r1, w0 + w_kstride);
+    pr.store_w(r0, smem, 0);
+    pr.load_w(r0, w0 + 2 * w_kstride);
+    if (ns > 1) pr.store_w(r1, smem, C::STAGE);
+    pr.load_w(r1, w0 + 3 * w_kstride);
     wait_lgkm0();
-    producer_barrier();
+    bare_barrier();
     // during step k: step k+2 stored into stage (k+2)%3, step k+4 requested
     int stage = 2 * C::STAGE, k = 0;
     for (; k + 5 < ns; k += 2) {
-        reg_step<C>(pr, smem, stage, r0, a0 + (k + 4) * a_kstride, w0 + (k + 4) * w_kstride);
+        produce_step<C>(pr, smem, stage, r0, w0 + (k + 4) * w_kstride);
         stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
         wait_lgkm0();
-        producer_barrier();
-        reg_step<C>(pr, smem, stage, r1, a0 + (k + 5) * a_kstride, w0 + (k + 5) * w_kstride);
+        bare_barrier();
+        produce_step<C>(pr, smem, stage, r1, w0 + (k + 5) * w_kstride);
         stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
         wait_lgkm0();
-        producer_barrier();
+        bare_barrier();
     }
     for (; k < ns; k += 2) {
         if (k + 2 < ns) {
-            pr.store_a(r0.a, smem, stage);
-            pr.template store_w<false>(r0.w, smem, stage);
-            if (k + 4 < ns) {
-                pr.load_a(r0.a, a0 + (k + 4) * a_kstride);
-                pr.load_w(r0.w, w0 + (k + 4) * w_kstride);
-            }
+            pr.store_w(r0, smem, stage);
+            if (k + 4 < ns) pr.load_w(r0, w0 + (k + 4) * w_kstride);
         }
         stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
         wait_lgkm0();
-        producer_barrier();
+        bare_barrier();
         if (k + 1 < ns) {
             if (k + 3 < ns) {
-                pr.store_a(r1.a, smem, stage);
-                pr.template store_w<false>(r1.w, smem, stage);
-                if (k + 5 < ns) {
-                    pr.load_a(r1.a, a0 + (k + 5) * a_kstride);
-                    pr.load_w(r1.w, w0 + (k + 5) * w_kstride);
-                }
+                pr.store_w(r1, smem, stage);
+                if (k + 5 < ns) pr.load_w(r1, w0 + (k + 5) * w_kstride);
             }
             stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
             wait_lgkm0();
-            producer_barrier();
+            bare_barrier();
         }
     }
 }
@@ -862,35 +607,26 @@ __global__ __launch_bounds__(C::NT, 1) void gemm_kernel(const gemm_params p) {
     const int64_t m0 = (int64_t) tm * C::BM, n0 = (int64_t) (tn - W.tile0) * C::BN;
 
     if (wave >= C::NC / 64) {
-        const producer<C> pr(p.a, (int64_t) p.a_kstride * nk, W.w, (int64_t) W.w_kstride * nk, tid - C::NC);
-        // uniform, but the tile arithmetic can leave them in vector registers,
+        const producer<C> pr(W.w, (int64_t) W.w_kstride * nk, tid - C::NC);
+        // uniform, but the tile arithmetic can leave it in a vector register,
         // and a load's scalar offset taken from one costs a loop per load
-        const int a0 =
-            __builtin_amdgcn_readfirstlane((int) ((m0 / ZEST_XGROUP_ROWS) * ZEST_XGROUP_BYTES) + k0 * p.a_kstride);
         const int w0 =
             __builtin_amdgcn_readfirstlane((int) ((n0 / ZEST_TILE_ROWS) * ZEST_TILE_BYTES) + k0 * W.w_kstride);
-        if constexpr (C::ADIRECT || ZEST_GEMM_AREG)
-            produce_regs<C>(pr, smem, a0, w0, p.a_kstride, W.w_kstride, ns);
-        else
-            produce<C>(pr, smem, a0, w0, p.a_kstride, W.w_kstride, ns);
+        produce<C>(pr, smem, w0, W.w_kstride, ns);
         return;
     }
 
-    // Consumer.
-    const int wm = wave / C::CWN, wn = wave % C::CWN, khalf = lane >> 5;
-    const int ar = wm * C::WM + (lane & 31), wr = wn * C::WN + (lane & 31);
-    int fa[4], fw[4];
+    // Consumer: rows wm*WM.. of the tile, every column.
+    const int wm = wave, wn = 0, khalf = lane >> 5, wr = lane & 31;
+    int fw[4];
 #pragma unroll
-    for (int s = 0; s < 4; s++) {
-        fa[s] = ar * C::ROWB + ((2 * s + khalf) ^ swz(ar)) * 16;
-        fw[s] = C::A_BYTES + wr * C::ROWB + ((2 * s + khalf) ^ swz(wr)) * 16;
-    }
+    for (int s = 0; s < 4; s++) fw[s] = wr * C::ROWB + ((2 * s + khalf) ^ swz(wr)) * 16;
     f32x16 acc[C::TI][C::TJ];
 #pragma unroll
     for (int i = 0; i < C::TI; i++)
 #pragma unroll
         for (int j = 0; j < C::TJ; j++) acc[i][j] = f32x16{};
-    if constexpr (C::ADIRECT) {
+    {
         // A two steps ahead in registers; no fence at the barriers, so the
         // loads stay in flight across them (consumers write no memory here)
         const a_loader<C> al(p.a, (int64_t) p.a_kstride * nk, wm, lane);
@@ -900,7 +636,7 @@ __global__ __launch_bounds__(C::NT, 1) void gemm_kernel(const gemm_params p) {
         bf16x8 a0s[4][C::TI], a1s[4][C::TI], bw[2][C::TJ];
         al.load_step(a0s, a0);
         al.load_step(a1s, a0 + ks);
-        producer_barrier();
+        bare_barrier();
 #pragma unroll
         for (int j = 0; j < C::TJ; j++) bw[0][j] = lds_get(smem, fw[0] + j * 32 * C::ROWB);
         int cur = 0, k = 0;
@@ -908,33 +644,21 @@ __global__ __launch_bounds__(C::NT, 1) void gemm_kernel(const gemm_params p) {
         // end read zeros or the next split's slab, and are never used)
         for (; k + 1 < ns; k += 2) {
             int nxt = cur == 2 * C::STAGE ? 0 : cur + C::STAGE;
-            consume_direct<C, true>(acc, a0s, bw, smem, fw, cur, nxt, al, a0 + (k + 2) * ks);
+            consume<C, true>(acc, a0s, bw, smem, fw, cur, nxt, al, a0 + (k + 2) * ks);
             cur = nxt;
-            producer_barrier();
+            bare_barrier();
             nxt = cur == 2 * C::STAGE ? 0 : cur + C::STAGE;
-            consume_direct<C, true>(acc, a1s, bw, smem, fw, cur, nxt, al, a0 + (k + 3) * ks);
+            consume<C, true>(acc, a1s, bw, smem, fw, cur, nxt, al, a0 + (k + 3) * ks);
             cur = nxt;
-            producer_barrier();
+            bare_barrier();
         }
         if (k < ns) {
             const int nxt = cur == 2 * C::STAGE ? 0 : cur + C::STAGE;
-            consume_direct<C, false>(acc, a0s, bw, smem, fw, cur, nxt, al, 0);
-            producer_barrier();
+            consume<C, false>(acc, a0s, bw, smem, fw, cur, nxt, al, 0);
+            bare_barrier();
         }
         // the loads of steps past the end are still in flight
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-    } else {
-        bf16x8 af[2][C::TI], bw[2][C::TJ];
-        __syncthreads();
-        if (ZEST_GEMM_XSTEP) read_frags<C>(af[0], bw[0], smem, fa[0], fw[0]);
-        int cur = 0;
-        for (int k = 0; k < ns; k++) {
-            const int nxt = cur == 2 * C::STAGE ? 0 : cur + C::STAGE;
-            if (!ZEST_GEMM_XSTEP) read_frags<C>(af[0], bw[0], smem, fa[0] + cur, fw[0] + cur);
-            consume<C>(acc, af, bw, smem, fa, fw, cur, nxt, ZEST_GEMM_XSTEP && k + 1 < ns);
-            cur = nxt;
-            __syncthreads();
-        }
     }
     if (SPLIT && !fixup<C>(acc, p, smem, t, split, wave, lane)) return;
     if constexpr (EPI == EPI_RESIDUAL)
@@ -945,14 +669,13 @@ __global__ __launch_bounds__(C::NT, 1) void gemm_kernel(const gemm_params p) {
         store_glu<C, EPI>(acc, smem, p.xout, p.h, p.ldh, p.M, W.n / 2, m0, n0, wave, wm, wn, lane, p.nonfinite);
 }
 
-// 256x128 tiles (4 consumer waves of 64x128, A straight into registers);
-// 128x128 (2x2 waves of 64x64, A staged in LDS) when the activations have at
-// most 128 rows.
+// 256x128 tiles (4 consumer waves of 64x128); 128x128 (4 of 32x128) where
+// the cost model prefers them (few rows, or too few big tiles).
 #ifndef ZEST_GEMM_BIG
-#define ZEST_GEMM_BIG 256, 128, 4, 1, true
+#define ZEST_GEMM_BIG 256, 128, 4
 #endif
 #ifndef ZEST_GEMM_SMALL
-#define ZEST_GEMM_SMALL 128, 128, 2, 2
+#define ZEST_GEMM_SMALL 128, 128, 4
 #endif
 // Launch cost model, in K-steps of a 256x128 tile at full occupancy (about
 // 0.85 us): T tiles on P CUs take ceil(T/P) rounds of nk steps, plus PROLOGUE
