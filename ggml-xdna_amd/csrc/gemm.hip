@@ -102,8 +102,6 @@ typedef __attribute__((address_space(3))) void * lds_ptr_t;
 // lanes are 16 consecutive rows, for the swizzled stores.
 template <class C>
 struct producer {
-    static constexpr int NPW = C::NP / 64;          // producer waves
-    static constexpr int WI = 3;                    // W load instructions per K-step (load_w)
     static_assert(C::BU == 2 && C::NP / 32 == C::BN / 16, "two W units per producer thread, 32 threads a tile");
     __amdgpu_buffer_rsrc_t rw;
     int vwm, vwe;          // lane offsets: W mantissas, W exponents
@@ -138,7 +136,6 @@ struct producer {
         return slow;
     }
 
-
     // Every unit of the step by the general expansion, stored.
     __device__ void store_w_general(const stage_regs<C> & st, uint8_t * smem, int stage) const {
 #pragma unroll
@@ -150,10 +147,9 @@ struct producer {
         }
     }
 
-    // W unit i is row +i*NP/4 (a multiple of 16 rows, so the swizzle is the
-    // first unit's). The units take the branch-free fast expansion; a unit
-    // whose exponent bytes need the general one is redone behind a single
-    // wave-uniform branch, which real weights almost never take.
+    // The units take the branch-free fast expansion; a unit whose exponent
+    // bytes need the general one is redone behind a single wave-uniform
+    // branch, which real weights almost never take.
     __device__ void store_w(const stage_regs<C> & st, uint8_t * smem, int stage) const {
         bool slow = false;
 #pragma unroll
@@ -162,11 +158,12 @@ struct producer {
     }
 };
 
-// The consumers' A fragments come from memory straight into registers. Fragment i of sub-step s is sub-tile s of the 32-row group
-// wm*WM/32 + i of the tile's K-step slab: lane l takes row l%32, chunk
-// 2s + l/32 (one block as bf16, the MFMA's A operand), the 16 bytes at
-// 32(l%32) + 16(l/32), so the wave's load covers one contiguous 1 KB. A load
-// past the operand returns zeros.
+// The consumers' A fragments come from memory straight into registers.
+// Fragment i of sub-step s is sub-tile s of the 32-row group wm*WM/32 + i of
+// the tile's K-step slab: lane l takes row l%32, chunk 2s + l/32 (one block
+// as bf16, the MFMA's A operand), the 16 bytes at 32(l%32) + 16(l/32), so the
+// wave's load covers one contiguous 1 KB. A load past the operand returns
+// zeros.
 template <class C>
 struct a_loader {
     __amdgpu_buffer_rsrc_t ra;
@@ -202,8 +199,8 @@ struct a_loader {
 // with the MFMAs.
 template <class C, bool LOAD>
 __device__ inline void consume(f32x16 (&acc)[C::TI][C::TJ], bf16x8 (&a)[4][C::TI], bf16x8 (&bw)[2][C::TJ],
-                                      const uint8_t * smem, const int (&fw)[4], int cur, int nxt,
-                                      const a_loader<C> & al, int a_next) {
+                               const uint8_t * smem, const int (&fw)[4], int cur, int nxt, const a_loader<C> & al,
+                               int a_next) {
 #pragma unroll
     for (int s = 0; s < 4; s++) {
         const int off = s < 3 ? fw[s + 1] + cur : fw[0] + nxt;
