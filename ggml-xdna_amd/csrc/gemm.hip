@@ -393,6 +393,10 @@ struct gemm_params {
     int splits;
     float * partial;
     uint32_t * counters;
+    // Mixed launches (gemm_kernel_mixed): the first nbig tiles (mt x nt
+    // tiles of the big shape) run whole, each of the others as two tiles of
+    // half its rows (the small shape).
+    int nbig;
 };
 
 // Byte offset of a consumer wave's float4 (i, j, quad q) in a unit's partial
@@ -568,30 +572,13 @@ __device__ inline void produce(const producer<C> & pr, uint8_t * smem, int w0, i
     }
 }
 
-// EPI: EPI_PLAIN the fp32 store, EPI_RESIDUAL the fp32 store of acc + res,
-// >= 0 the fused GLU of that kind.
-// SPLIT: split-K (p.splits > 1), else one whole tile per workgroup.
-template <class C, int EPI, bool SPLIT>
-__global__ __launch_bounds__(C::NT, 1) void gemm_kernel(const gemm_params p) {
-    extern __shared__ uint4 smem_u4[];
-    uint8_t * smem = reinterpret_cast<uint8_t *>(smem_u4);
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int nk = p.nk;
-    // Workgroups go to the 8 XCDs round-robin by linear id; v numbers them so
-    // that each XCD holds a contiguous run of v, i.e. of tiles.
-    const int G = (int) gridDim.x, b = (int) blockIdx.x;
-#if ZEST_GEMM_XCD
-    const int v = (b % 8) * (G / 8) + min(b % 8, G % 8) + b / 8;
-#else
-    const int v = b;
-#endif
-    const int T = p.mt * p.nt;
-    const int split = SPLIT ? v / T : 0, t = SPLIT ? v - split * T : v;
-    const int k0 = SPLIT ? split * nk / p.splits : 0, ns = SPLIT ? (split + 1) * nk / p.splits - k0 : nk;
-    // Tile t: tiles go in groups of GROUP_M tile rows, M-fastest inside a
-    // group, so the ~32 workgroups resident on one XCD cover a compact block
-    // of about 4 x 8 tiles and share their A and W slabs in its L2.
+// Tile t of a launch in the tile order: tiles go in groups of GROUP_M tile
+// rows, M-fastest inside a group, so the ~32 workgroups resident on one XCD
+// cover a compact block of about 4 x 8 tiles and share their A and W slabs in
+// its L2. Returns the tile's weight (of a group launch) and its first row and
+// column.
+template <class C>
+__device__ inline gemm_weight tile_of(const gemm_params & p, int t, int64_t & m0, int64_t & n0) {
     const int per_group = ZEST_GEMM_GROUP_M * p.nt, first_m = t / per_group * ZEST_GEMM_GROUP_M;
     const int gm = min(p.mt - first_m, ZEST_GEMM_GROUP_M), in = t % per_group;
     const int tm = first_m + in % gm, tn = in / gm;
@@ -600,9 +587,29 @@ __global__ __launch_bounds__(C::NT, 1) void gemm_kernel(const gemm_params p) {
     for (int i = 1; i < ZEST_GEMM_MAX_GROUP; i++)
         if (i < p.nw && tn >= p.wt[i].tile0) g = i;
     g = __builtin_amdgcn_readfirstlane(g);
-    const gemm_weight W = p.wt[g];
-    const int64_t m0 = (int64_t) tm * C::BM, n0 = (int64_t) (tn - W.tile0) * C::BN;
+    m0 = (int64_t) tm * C::BM;
+    n0 = (int64_t) (tn - p.wt[g].tile0) * C::BN;
+    return p.wt[g];
+}
 
+// Workgroups go to the 8 XCDs round-robin by linear id b; the n workgroups
+// numbered by this map hold a contiguous run of it on each XCD.
+__device__ inline int xcd_order(int b, int n) {
+#if ZEST_GEMM_XCD
+    return (b % 8) * (n / 8) + min(b % 8, n % 8) + b / 8;
+#else
+    return b;
+#endif
+}
+
+// One output tile (rows m0.., columns n0.. of weight W), over K-steps
+// [k0, k0 + ns); with SPLIT, unit `split` of tile t.
+template <class C, int EPI, bool SPLIT>
+__device__ inline void run_tile(const gemm_params & p, uint8_t * smem, const gemm_weight & W, int64_t m0, int64_t n0,
+                                int k0, int ns, int t, int split) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nk = p.nk;
     if (wave >= C::NC / 64) {
         const producer<C> pr(W.w, (int64_t) W.w_kstride * nk, tid - C::NC);
         // uniform, but the tile arithmetic can leave it in a vector register,
@@ -664,6 +671,47 @@ __global__ __launch_bounds__(C::NT, 1) void gemm_kernel(const gemm_params p) {
         store_tile<C>(acc, W.c, p.M, W.n, W.ldc, m0, n0, wm, wn, lane, p.nonfinite);
     else
         store_glu<C, EPI>(acc, smem, p.xout, p.h, p.ldh, p.M, W.n / 2, m0, n0, wave, wm, wn, lane, p.nonfinite);
+}
+
+// EPI: EPI_PLAIN the fp32 store, EPI_RESIDUAL the fp32 store of acc + res,
+// >= 0 the fused GLU of that kind.
+// SPLIT: split-K (p.splits > 1), else one whole tile per workgroup.
+template <class C, int EPI, bool SPLIT>
+__global__ __launch_bounds__(C::NT, 1) void gemm_kernel(const gemm_params p) {
+    extern __shared__ uint4 smem_u4[];
+    uint8_t * smem = reinterpret_cast<uint8_t *>(smem_u4);
+    const int v = xcd_order((int) blockIdx.x, (int) gridDim.x), nk = p.nk;
+    const int T = p.mt * p.nt;
+    const int split = SPLIT ? v / T : 0, t = SPLIT ? v - split * T : v;
+    const int k0 = SPLIT ? split * nk / p.splits : 0, ns = SPLIT ? (split + 1) * nk / p.splits - k0 : nk;
+    int64_t m0, n0;
+    const gemm_weight W = tile_of<C>(p, t, m0, n0);
+    run_tile<C, EPI, SPLIT>(p, smem, W, m0, n0, k0, ns, t, split);
+}
+
+// The mixed launch: CB tiles (p.mt x p.nt of them) whose count is a whole
+// number of rounds of the GPU plus a part of one; that part runs as tiles of
+// half the rows (CS), twice as many workgroups of about half the time, so the
+// last round ends sooner. On each XCD the whole tiles come first (the first
+// workgroups it is given), then the halves.
+template <class CB, class CS, int EPI>
+__global__ __launch_bounds__(CB::NT, 1) void gemm_kernel_mixed(const gemm_params p) {
+    static_assert(CB::NT == CS::NT && CS::BM * 2 == CB::BM && CS::BN == CB::BN, "halves of the big tiles");
+    extern __shared__ uint4 smem_u4[];
+    uint8_t * smem = reinterpret_cast<uint8_t *>(smem_u4);
+    const int b = (int) blockIdx.x, per_xcd = p.nbig / 8, i = b / 8;
+    int64_t m0, n0;
+    if (i < per_xcd) {
+        const int t = (b % 8) * per_xcd + i;
+        const gemm_weight W = tile_of<CB>(p, t, m0, n0);
+        run_tile<CB, EPI, false>(p, smem, W, m0, n0, 0, p.nk, t, 0);
+    } else {
+        const int nhalf = (int) gridDim.x - p.nbig;
+        const int u = xcd_order(b - p.nbig, nhalf);  // b - nbig keeps b's XCD: nbig % 8 == 0
+        const int t = p.nbig + u / 2;
+        const gemm_weight W = tile_of<CB>(p, t, m0, n0);
+        run_tile<CS, EPI, false>(p, smem, W, m0 + (u % 2) * CS::BM, n0, 0, p.nk, t, 0);
+    }
 }
 
 // 256x128 tiles (4 consumer waves of 64x128); 128x128 (4 of 32x128) where
@@ -761,6 +809,20 @@ int set_lds(const char * name) {
     return ZEST_OK;
 }
 
+template <int EPI>
+int set_lds_mixed(const char * name) {
+    static bool attr_set = false;
+    if (!attr_set) {
+        const size_t bytes = std::max(cfg_big::LDS_BYTES, cfg_small::LDS_BYTES);
+        const hipError_t e =
+            hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_kernel_mixed<cfg_big, cfg_small, EPI>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int) bytes);
+        if (e != hipSuccess) return zest::fail(ZEST_E_HIP, "%s: LDS attribute: %s", name, hipGetErrorString(e));
+        attr_set = true;
+    }
+    return ZEST_OK;
+}
+
 struct gemm_plan {
     int splits = 1;
     double cost = 0;
@@ -820,6 +882,29 @@ int launch(gemm_params p, const int64_t * N, int splits, hipStream_t s, const ch
     return zest::check_launch(name);
 }
 
+// A mixed launch: the first nbig big tiles whole, the rest as halves.
+template <int EPI>
+int launch_mixed(gemm_params p, const int64_t * N, int64_t nbig, hipStream_t s, const char * name) {
+    using CB = cfg_big;
+    p.mt = (int) ((p.M + CB::BM - 1) / CB::BM);
+    int nt = 0;
+    for (int i = 0; i < p.nw; i++) {
+        p.wt[i].tile0 = nt;
+        nt += (int) ((N[i] + CB::BN - 1) / CB::BN);
+    }
+    p.nt = nt;
+    const int64_t T = (int64_t) p.mt * nt, grid = nbig + 2 * (T - nbig);
+    if (grid >= (1ll << 31) || nbig % 8 || nbig >= T)
+        return zest::fail(ZEST_E_ARG, "%s: mixed launch of %lld tiles", name, (long long) T);
+    p.splits = 1;
+    p.nbig = (int) nbig;
+    const int st = set_lds_mixed<EPI>(name);
+    if (st != ZEST_OK) return st;
+    hipLaunchKernelGGL((gemm_kernel_mixed<cfg_big, cfg_small, EPI>), dim3((unsigned) grid), dim3(CB::NT),
+                       std::max(cfg_big::LDS_BYTES, cfg_small::LDS_BYTES), s, p);
+    return zest::check_launch(name);
+}
+
 // The tile shape and K splits of a launch (the cost model above).
 template <int EPI>
 int launch_any(gemm_params p, const int64_t * N, hipStream_t s, const char * name) {
@@ -830,6 +915,12 @@ int launch_any(gemm_params p, const int64_t * N, hipStream_t s, const char * nam
                                       (double) cfg_big::BM * cfg_big::BN * 4, 1.0);
     const gemm_plan small = plan_splits(tiles_of(p, N, cfg_small::BM, cfg_small::BN), p.nk, P,
                                         (double) cfg_small::BM * cfg_small::BN * 4, ZEST_GEMM_SMALL_STEP);
+    // mixed: whole rounds of big tiles, the part-round left as half tiles
+    const int64_t Tb = tiles_of(p, N, cfg_big::BM, cfg_big::BN), R = Tb / P, rem = Tb - R * P;
+    double mixed = 1e300;
+    if (R >= 1 && rem > 0 && R * P % 8 == 0)
+        mixed = ((double) R + (double) ((2 * rem + P - 1) / P) * ZEST_GEMM_SMALL_STEP) * (p.nk + ZEST_GEMM_PROLOGUE);
+    if (mixed < big.cost && mixed < small.cost) return launch_mixed<EPI>(p, N, R * P, s, name);
     if (small.cost < big.cost) return launch<cfg_small, EPI>(p, N, small.splits, s, name);
     return launch<cfg_big, EPI>(p, N, big.splits, s, name);
 }

@@ -214,6 +214,29 @@ def test_gemm_group(zest_gpu, oracle, M, K, ns, wtype):
         assert worst <= 1.0, i
 
 
+def test_gemm_part_round_as_half_tiles(zest_gpu, oracle):
+    # M = 2048, N = 6144: 384 tiles of 256 x 128, one round of the GPU's 256
+    # CUs and half of another; the launch runs the last 128 tiles as 256 of
+    # 128 x 128. Each output is summed over K in the same order either way, so
+    # the result equals, bit for bit, two launches over the column halves (192
+    # whole tiles each), and the oracle within the GEMM bar.
+    M, N, K = 2048, 6144, 512
+    x = Rng(3).normal(M * K).reshape(M, K)
+    w = Rng(4).normal(N * K, 0, 0.02).reshape(N, K)
+    c, nf, a, wp = run_gemm(zest_gpu, x, 0, w.view(np.uint8), N)
+    assert nf == 0
+    half = N // 2
+    parts = [zest_gpu.gemm(a, M, zest_gpu.convert_weight(0, _dev(np.ascontiguousarray(w[h * half:(h + 1) * half])
+                                                                 .view(np.uint8)), half, K), half, K)
+             for h in range(2)]
+    both = np.concatenate([q.cpu().numpy() for q in parts], axis=1)
+    assert np.array_equal(c.view(np.uint32), both.view(np.uint32))
+    rows = np.unique(np.concatenate([np.linspace(0, M - 1, 40).astype(int), [1024, 1151, 1152, 1279, 2047]]))
+    r64, ab = oracle.mul_mat_f64(decoded(zest_gpu, oracle, wp, N, K), decoded_act(zest_gpu, oracle, a, M, K)[rows])
+    worst, maxrel = gemm_check(c[rows], r64, ab, K)
+    assert worst <= 1.0 and maxrel <= 1e-3
+
+
 def test_gemm_group_rejects_bad_counts(zest_gpu):
     import torch
     a = zest_gpu.empty_act(64, 64)
