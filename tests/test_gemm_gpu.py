@@ -253,6 +253,7 @@ def test_gemm_group_rejects_bad_counts(zest_gpu):
     (2048, 2560, 9728),   # its down projection (split K)
     (300, 200, 256),      # ragged rows, 128x128 tiles
     (1024, 1000, 512),    # a width that is not a tile multiple
+    (2048, 6144, 512),    # 384 tiles: a round and a half, the half as 128-row tiles
 ])
 def test_gemm_residual_is_gemm_then_add(zest_gpu, M, N, K):
     # the residual epilogue adds in the store: the same floats as the GEMM
