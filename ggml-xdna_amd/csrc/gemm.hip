@@ -23,6 +23,7 @@
 #include <algorithm>
 #include <map>
 #include <mutex>
+#include <type_traits>
 #include <utility>
 
 #include "zest_common.h"
@@ -45,14 +46,14 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // BM x BN tile; CWM consumer waves, each a WM x BN block of 32x32 MFMA tiles
-// (TI x TJ of them); as many producer waves. LDS holds the expanded W ring;
+// (TI x TJ of them); NP/64 producer waves (as many by default). LDS holds the expanded W ring;
 // after the K loop each consumer wave uses WM x BN floats of it for its
 // epilogue.
-template <int BM_, int BN_, int CWM_>
+template <int BM_, int BN_, int CWM_, int NP_ = 64 * CWM_>
 struct gemm_cfg {
     static constexpr int BM = BM_, BN = BN_, CWM = CWM_, CWN = 1;
     static constexpr int NC = 64 * CWM;  // consumer threads
-    static constexpr int NP = NC;        // producer threads
+    static constexpr int NP = NP_;       // producer threads
     static constexpr int NT = NC + NP;
     static constexpr int WM = BM / CWM, WN = BN;
     static constexpr int TI = WM / 32, TJ = WN / 32;
@@ -741,8 +742,15 @@ __global__ __launch_bounds__(CB::NT, 1) void gemm_kernel_mixed(const gemm_params
 #ifndef ZEST_GEMM_SMALL_STEP
 #define ZEST_GEMM_SMALL_STEP 0.8
 #endif
+// The fused GLU's 256x128 tiles: 8 consumer waves of 32x128 and 4 producer
+// waves, two consumers on each SIMD (the GLU's long launches gain ~3% from
+// the second consumer; the others lose it to the doubled W fragment reads).
+#ifndef ZEST_GEMM_GLU
+#define ZEST_GEMM_GLU 256, 128, 8, 256
+#endif
 using cfg_big = gemm_cfg<ZEST_GEMM_BIG>;
 using cfg_small = gemm_cfg<ZEST_GEMM_SMALL>;
+using cfg_glu = gemm_cfg<ZEST_GEMM_GLU>;
 
 // Per device and stream: the split-K workspace (grown as needed; counters
 // zeroed when allocated, and zero again after every launch).
@@ -911,18 +919,22 @@ int launch_any(gemm_params p, const int64_t * N, hipStream_t s, const char * nam
     int dev = 0;
     (void) hipGetDevice(&dev);
     const int64_t P = cu_count(dev);
-    const gemm_plan big = plan_splits(tiles_of(p, N, cfg_big::BM, cfg_big::BN), p.nk, P,
-                                      (double) cfg_big::BM * cfg_big::BN * 4, 1.0);
+    using CB = std::conditional_t<(EPI >= 0), cfg_glu, cfg_big>;
+    const gemm_plan big =
+        plan_splits(tiles_of(p, N, CB::BM, CB::BN), p.nk, P, (double) CB::BM * CB::BN * 4, 1.0);
     const gemm_plan small = plan_splits(tiles_of(p, N, cfg_small::BM, cfg_small::BN), p.nk, P,
                                         (double) cfg_small::BM * cfg_small::BN * 4, ZEST_GEMM_SMALL_STEP);
-    // mixed: whole rounds of big tiles, the part-round left as half tiles
-    const int64_t Tb = tiles_of(p, N, cfg_big::BM, cfg_big::BN), R = Tb / P, rem = Tb - R * P;
-    double mixed = 1e300;
-    if (R >= 1 && rem > 0 && R * P % 8 == 0)
-        mixed = ((double) R + (double) ((2 * rem + P - 1) / P) * ZEST_GEMM_SMALL_STEP) * (p.nk + ZEST_GEMM_PROLOGUE);
-    if (mixed < big.cost && mixed < small.cost) return launch_mixed<EPI>(p, N, R * P, s, name);
+    if constexpr (EPI < 0) {
+        // mixed: whole rounds of big tiles, the part-round left as half tiles
+        const int64_t Tb = tiles_of(p, N, cfg_big::BM, cfg_big::BN), R = Tb / P, rem = Tb - R * P;
+        if (R >= 1 && rem > 0 && R * P % 8 == 0) {
+            const double mixed =
+                ((double) R + (double) ((2 * rem + P - 1) / P) * ZEST_GEMM_SMALL_STEP) * (p.nk + ZEST_GEMM_PROLOGUE);
+            if (mixed < big.cost && mixed < small.cost) return launch_mixed<EPI>(p, N, R * P, s, name);
+        }
+    }
     if (small.cost < big.cost) return launch<cfg_small, EPI>(p, N, small.splits, s, name);
-    return launch<cfg_big, EPI>(p, N, big.splits, s, name);
+    return launch<CB, EPI>(p, N, big.splits, s, name);
 }
 
 // The parts of a launch's parameters common to every kind.
