@@ -379,7 +379,7 @@ __device__ inline void encode_half_row(const float v[32], bool no_nan, uint4 & m
 template <int TYPE, int ROWS>
 __global__ __launch_bounds__(256) void convert_kernel(const uint8_t * __restrict__ raw, size_t row_bytes, int64_t N,
                                                       int64_t K, uint8_t * __restrict__ dst, int64_t R_pad,
-                                                      int64_t K_pad, int64_t R_src, int gu) {
+                                                      int64_t K_pad, int gu) {
     static_assert(ROWS == 8 || ROWS == 16 || ROWS == 32, "rows per workgroup");
     constexpr int TILES = 128 / ROWS, HALVES = 2 * TILES;
     // LDS bytes of one tile column: ROWS rows of 64 mantissas and 8 exponents
@@ -539,7 +539,7 @@ static int convert(int type, const void * raw, int64_t N, int64_t K, void * dst,
     uint8_t * d8 = (uint8_t *) dst;
 #define ZEST_CONVERT(T)                                                                                         \
     case T:                                                                                                     \
-        hipLaunchKernelGGL((convert_kernel<T, RW>), grid, dim3(256), 0, s, r8, rb, N, K, d8, R_pad, K_pad, R_src, gu); \
+        hipLaunchKernelGGL((convert_kernel<T, RW>), grid, dim3(256), 0, s, r8, rb, N, K, d8, R_pad, K_pad, gu); \
         break
     switch (type) {
         ZEST_CONVERT(ZEST_TYPE_F16);
