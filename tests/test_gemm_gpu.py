@@ -273,3 +273,56 @@ def test_gemm_residual_is_gemm_then_add(zest_gpu, M, N, K):
     assert torch.equal(out.view(torch.int32), want.view(torch.int32))
     assert torch.equal(h.view(torch.int32), want.view(torch.int32))
     assert int(nf.item()) == 0
+
+
+def test_gemm_random_shapes(zest_gpu, oracle):
+    # a seeded sweep over odd shapes (rows from 1 to a few rounds of tiles,
+    # widths in steps of 32, K in steps of 8) through the plain, residual and
+    # grouped launches, against the oracle within the GEMM bar, and the fused
+    # GLU bit-exact with the unfused chain over the same GEMM; the launch picks
+    # tile shapes, splits and mixed rounds as it would for any caller
+    import torch
+    rng = np.random.default_rng(20260)
+    for case in range(24):
+        M = int(rng.choice([1, 7, 100, 129, 300, 513, 1000, 1500, 2100]))
+        N = int(rng.integers(1, 64)) * 32 * int(rng.choice([1, 2, 4]))
+        K = int(rng.integers(1, 40)) * 8 * int(rng.choice([1, 2, 4]))
+        x = rng.normal(0, 1, (M, K)).astype(np.float32)
+        w = rng.normal(0, 0.05, (N, K)).astype(np.float32)
+        a = zest_gpu.pack_act_x(_dev(x))
+        kind = case % 4
+        if kind == 3:
+            F = max(32, N // 64 * 32)
+            up = rng.normal(0, 0.05, (F, K)).astype(np.float32)
+            wgu = zest_gpu.convert_weight_gu(0, _dev(np.ascontiguousarray(w[:F]).view(np.uint8)),
+                                             _dev(up.view(np.uint8)), F, K)
+            c = zest_gpu.gemm(a, M, wgu, 2 * F, K).view(M, F // 32, 2, 32)
+            h_ref = zest_gpu.glu(2, c[:, :, 0, :].reshape(M, F).contiguous(), c[:, :, 1, :].reshape(M, F).contiguous(), F)
+            xo, h = zest_gpu.gemm_glu(2, a, M, wgu, F, K, h=True)
+            x_ref = zest_gpu.pack_act_x(h_ref)
+            torch.cuda.synchronize()
+            assert torch.equal(h.view(torch.int32), h_ref.view(torch.int32)), (M, F, K)
+            assert torch.equal(xo, x_ref), (M, F, K)
+            continue
+        wp = zest_gpu.convert_weight(0, _dev(w.view(np.uint8)), N, K)
+        slack = 0.0
+        if kind == 0:
+            got = zest_gpu.gemm(a, M, wp, N, K).cpu().numpy().astype(np.float64)
+        elif kind == 1:
+            res = rng.normal(0, 1, (M, N)).astype(np.float32)
+            out = zest_gpu.gemm_residual(a, M, wp, N, K, _dev(res)).cpu().numpy().astype(np.float64)
+            got, slack = out - res, np.abs(out) * 2.0 ** -24  # the add rounds once more
+        else:
+            cuts = sorted({0, N, *(int(v) // 8 * 8 for v in rng.integers(8, max(9, N - 8), 2))})
+            parts = [(lo, hi) for lo, hi in zip(cuts, cuts[1:]) if hi > lo]
+            ws = [zest_gpu.convert_weight(0, _dev(np.ascontiguousarray(w[lo:hi]).view(np.uint8)), hi - lo, K)
+                  for lo, hi in parts]
+            outs = zest_gpu.gemm_group(a, M, ws, [hi - lo for lo, hi in parts], K)
+            got = np.concatenate([o.cpu().numpy() for o in outs], axis=1).astype(np.float64)
+        rows = np.unique(np.linspace(0, M - 1, min(M, 16)).astype(int))
+        r64, ab = oracle.mul_mat_f64(decoded(zest_gpu, oracle, wp, N, K), decoded_act(zest_gpu, oracle, a, M, K)[rows])
+        sl = slack[rows] if kind == 1 else 0.0
+        err = np.abs(got[rows] - r64)
+        bound = 1e-3 * np.abs(r64) + 2.0 * K * 2.0 ** -24 * ab + sl
+        assert np.isfinite(got[rows]).all() and (err <= bound).all(), (kind, M, N, K, float((err / bound).max()))
+
