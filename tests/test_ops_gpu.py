@@ -130,3 +130,41 @@ def test_fused_packs_zero_their_padding(zest_gpu, oracle, rows, d):
     assert np.array_equal(zest_gpu.expanded_to_rows(host, rows, d).view(np.uint32),
                           oracle.decode_rows(oracle.encode_rows(_host(h))).view(np.uint32))
     del torch
+
+
+def test_expanded_writers_random_shapes(zest_gpu, oracle):
+    # every kernel that writes the expanded operand, over seeded odd shapes
+    # (rows across 32-row sub-tile groups and 256-row padding, widths in steps
+    # of 8 across 16- and 64-column boundaries), into buffers that held
+    # garbage: the values are the oracle's encoding of each kernel's fp32
+    # result and the padding is zero
+    import torch
+    rng = np.random.default_rng(31)
+    for _ in range(10):
+        rows = int(rng.choice([1, 31, 33, 95, 257, 300, 700]))
+        d = int(rng.integers(1, 200)) * 8
+        x = rng.normal(0, 1.5, (rows, d)).astype(np.float32)
+        want = oracle.decode_rows(oracle.encode_rows(x)).view(np.uint32)
+        buf = zest_gpu.empty_act(rows, d)
+        buf.fill_(0xFF)
+        zest_gpu.pack_act_x(_dev(x), out=buf)
+        host = _host(buf)
+        assert np.array_equal(zest_gpu.expanded_to_rows(host, rows, d).view(np.uint32), want), (rows, d)
+        assert _padding_is_zero(zest_gpu, host, rows, d), (rows, d)
+        ex = zest_gpu.expand_act(zest_gpu.pack_act(_dev(x)), rows, d)
+        assert np.array_equal(_host(ex), host), (rows, d)
+        buf.fill_(0xFF)
+        y = _host(zest_gpu.rms_norm(_dev(x), 1e-6, packed=buf))
+        host = _host(buf)
+        assert np.array_equal(zest_gpu.expanded_to_rows(host, rows, d).view(np.uint32),
+                              oracle.decode_rows(oracle.encode_rows(y)).view(np.uint32)), (rows, d)
+        assert _padding_is_zero(zest_gpu, host, rows, d), (rows, d)
+        u = rng.normal(0, 1.5, (rows, d)).astype(np.float32)
+        buf.fill_(0xFF)
+        h = _host(zest_gpu.glu(2, _dev(x), _dev(u), d, packed=buf))
+        host = _host(buf)
+        assert np.array_equal(zest_gpu.expanded_to_rows(host, rows, d).view(np.uint32),
+                              oracle.decode_rows(oracle.encode_rows(h)).view(np.uint32)), (rows, d)
+        assert _padding_is_zero(zest_gpu, host, rows, d), (rows, d)
+    del torch
+
