@@ -96,7 +96,9 @@ typedef __attribute__((address_space(3))) void * lds_ptr_t;
 
 // The producer side. W loads go through a buffer resource: the slab's byte
 // offset is wave-uniform (a scalar offset), the lane's place in it a fixed
-// vector offset, and a read past the operand returns zeros. Thread p takes
+// vector offset. The hardware range check covers the vector offset only, so
+// every slab offset a load is given names a K-step of the operand (callers
+// clamp the steps past the end to the last one). Thread p takes
 // two adjacent units of tile p/32 of the W slab: row p%16, column quarters 2h
 // and 2h+1 with h = p/16%2, i.e. 32 contiguous mantissa bytes (two 16-byte
 // loads) and 4 contiguous exponent bytes (one 4-byte load). 16 consecutive
@@ -163,8 +165,9 @@ struct producer {
 // Fragment i of sub-step s is sub-tile s of the 32-row group wm*WM/32 + i of
 // the tile's K-step slab: lane l takes row l%32, chunk 2s + l/32 (one block
 // as bf16, the MFMA's A operand), the 16 bytes at 32(l%32) + 16(l/32), so the
-// wave's load covers one contiguous 1 KB. A load past the operand returns
-// zeros.
+// wave's load covers one contiguous 1 KB. The K-step's offset is a scalar
+// offset, which the range check does not cover: callers pass only steps of
+// the operand.
 template <class C>
 struct a_loader {
     __amdgpu_buffer_rsrc_t ra;
@@ -253,12 +256,14 @@ __device__ inline void store_tile(const f32x16 (&acc)[C::TI][C::TJ], float * Cou
         uint8_t * region = smem + wave * (C::WM * C::WN * 4);
         const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<float *>(res), (short) 0, (int) (M * ldr * 4), 0x00020000);
-        // instruction q: rows RPI*q.. of the block, lane l taking row RPI*q + l/LPR, bytes 16(l%LPR)
+        // instruction q: rows RPI*q.. of the block, lane l taking row RPI*q + l/LPR, bytes 16(l%LPR);
+        // the whole byte offset is in the vector offset, so the range check
+        // turns rows past M into zeros instead of reads past the residual
         const int voff = (int) ((row0 + lane / LPR) * ldr * 4 + (n0 + wn * C::WN) * 4 + (lane % LPR) * 16);
 #pragma unroll
         for (int q = 0; q < C::WM / RPI; q++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_ptr_t) (region + q * 1024), 16, voff,
-                                                     (int) (RPI * q * ldr * 4), 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_ptr_t) (region + q * 1024), 16,
+                                                     voff + (int) (RPI * q * ldr * 4), 0, 0, 0);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         rl = reinterpret_cast<const float *>(region);
     }
@@ -273,9 +278,10 @@ __device__ inline void store_tile(const f32x16 (&acc)[C::TI][C::TJ], float * Cou
 #pragma unroll
                 for (int v = 0; v < 16; v++) {
                     float x = acc[i][j][v];
-                    if constexpr (RES)
-                        x += rl[(i * 32 + (v >> 2) * 8 + khalf * 4 + (v & 3)) * C::WN + j * 32 + (lane & 31)];
-                    bad |= !(__builtin_fabsf(x) <= 3.402823466e38f);
+                    const int rt = i * 32 + (v >> 2) * 8 + khalf * 4 + (v & 3);  // row in the wave's block
+                    if constexpr (RES) x += rl[rt * C::WN + j * 32 + (lane & 31)];
+                    // only rows that are stored count
+                    bad |= row0 + rt < M && !(__builtin_fabsf(x) <= 3.402823466e38f);
                     const int roff = (row0 + i * 32 + (v >> 2) * 8 + (v & 3)) * (int) ldc * 4;
                     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), rc, voff + roff, 0, 0);
                 }
@@ -525,20 +531,21 @@ __device__ inline void produce_step(const producer<C> & pr, uint8_t * smem, int 
 // registers and every LDS store is the compiler's own, so the compiler counts
 // the loads in flight and waits for exactly those whose registers a store
 // reads; before a barrier only the LDS stores are waited for. Steps 0-3 are
-// requested whether or not they exist (a load past the operand returns zeros,
-// one past this split's steps reads the next split's slab, and neither is
-// stored), so the steady state starts with an exact count; it runs without
-// conditions, and the last steps do their remaining stores one by one. The
-// barriers match the consumers', step for step.
+// requested whether or not this tile has them (a step past this split's
+// steps reads the next split's slab; one past the operand's last step, `last`
+// steps after w0, reads that last step again; neither is stored), so the
+// steady state starts with an exact count; it runs without conditions, and
+// the last steps do their remaining stores one by one. The barriers match the
+// consumers', step for step.
 template <class C>
-__device__ inline void produce(const producer<C> & pr, uint8_t * smem, int w0, int w_kstride, int ns) {
+__device__ inline void produce(const producer<C> & pr, uint8_t * smem, int w0, int w_kstride, int ns, int last) {
     stage_regs<C> r0, r1;
     pr.load_w(r0, w0);
-    pr.load_w(r1, w0 + w_kstride);
+    pr.load_w(r1, w0 + min(1, last) * w_kstride);
     pr.store_w(r0, smem, 0);
-    pr.load_w(r0, w0 + 2 * w_kstride);
+    pr.load_w(r0, w0 + min(2, last) * w_kstride);
     if (ns > 1) pr.store_w(r1, smem, C::STAGE);
-    pr.load_w(r1, w0 + 3 * w_kstride);
+    pr.load_w(r1, w0 + min(3, last) * w_kstride);
     wait_lgkm0();
     bare_barrier();
     // during step k: step k+2 stored into stage (k+2)%3, step k+4 requested
@@ -617,7 +624,7 @@ __device__ inline void run_tile(const gemm_params & p, uint8_t * smem, const gem
         // and a load's scalar offset taken from one costs a loop per load
         const int w0 =
             __builtin_amdgcn_readfirstlane((int) ((n0 / ZEST_TILE_ROWS) * ZEST_TILE_BYTES) + k0 * W.w_kstride);
-        produce<C>(pr, smem, w0, W.w_kstride, ns);
+        produce<C>(pr, smem, w0, W.w_kstride, ns, nk - 1 - k0);
         return;
     }
 
@@ -638,22 +645,26 @@ __device__ inline void run_tile(const gemm_params & p, uint8_t * smem, const gem
         const int ks = p.a_kstride;
         const int a0 =
             __builtin_amdgcn_readfirstlane((int) ((m0 / ZEST_XGROUP_ROWS) * ZEST_XGROUP_BYTES) + k0 * p.a_kstride);
+        // the operand's last K-step, counted from a0: the steps loaded past
+        // it load it again (the scalar offset is not range-checked)
+        const int last = nk - 1 - k0;
         bf16x8 a0s[4][C::TI], a1s[4][C::TI], bw[2][C::TJ];
         al.load_step(a0s, a0);
-        al.load_step(a1s, a0 + ks);
+        al.load_step(a1s, a0 + min(1, last) * ks);
         bare_barrier();
 #pragma unroll
         for (int j = 0; j < C::TJ; j++) bw[0][j] = lds_get(smem, fw[0] + j * 32 * C::ROWB);
         int cur = 0, k = 0;
         // pairs of steps without conditions (the loads of steps past the
-        // end read zeros or the next split's slab, and are never used)
+        // tile's end read the next split's slab or the operand's last step
+        // again, and are never used)
         for (; k + 1 < ns; k += 2) {
             int nxt = cur == 2 * C::STAGE ? 0 : cur + C::STAGE;
-            consume<C, true>(acc, a0s, bw, smem, fw, cur, nxt, al, a0 + (k + 2) * ks);
+            consume<C, true>(acc, a0s, bw, smem, fw, cur, nxt, al, a0 + min(k + 2, last) * ks);
             cur = nxt;
             bare_barrier();
             nxt = cur == 2 * C::STAGE ? 0 : cur + C::STAGE;
-            consume<C, true>(acc, a1s, bw, smem, fw, cur, nxt, al, a0 + (k + 3) * ks);
+            consume<C, true>(acc, a1s, bw, smem, fw, cur, nxt, al, a0 + min(k + 3, last) * ks);
             cur = nxt;
             bare_barrier();
         }
@@ -763,10 +774,10 @@ struct sk_space {
 
 int cu_count(int dev) {
     static std::mutex mu;
-    static std::map<int, int> cus;
+    static int cus[ZEST_MAX_DEVICES];
+    if (dev < 0 || dev >= ZEST_MAX_DEVICES) return 256;
     std::lock_guard<std::mutex> lock(mu);
-    auto it = cus.find(dev);
-    if (it != cus.end()) return it->second;
+    if (cus[dev] > 0) return cus[dev];
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
     cus[dev] = n;

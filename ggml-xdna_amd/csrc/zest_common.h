@@ -20,6 +20,9 @@ inline hipStream_t as_stream(void * s) { return reinterpret_cast<hipStream_t>(s)
 // Non-zero when the last launch failed (the error is recorded).
 int check_launch(const char * what);
 
+// Devices the per-device tables hold.
+#define ZEST_MAX_DEVICES 64
+
 } // namespace zest
 
 #define ZEST_REQUIRE(cond, ...)                               \

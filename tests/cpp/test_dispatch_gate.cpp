@@ -1,170 +1,197 @@
-// What the backend takes lives in supports_op, the device type and the buffer
-// type: the three things ggml's scheduler reads to decide. Checked directly,
-// as the reference's tests/test-dispatch-gate.cpp does, with
-// GGML_XDNA_MIN_BATCH and GGML_XDNA_MIN_MFLOP at their defaults. Runs on the
-// GPU, or without one under GGML_XDNA_PLAN_ONLY=1 (planning only).
+// The dispatch gate: which ops the backend takes from ggml's scheduler, read
+// through the three things the scheduler asks (the device's type and buffer
+// types, and supports_op for each node).
+//
+// Contract (reference: src/ggml-zest.cpp:56-81 thresholds and batch,
+// :1066-1072 what a weight is, :1160-1226 claim and policy; acceptance
+// criteria in specs/xdna-backend/spec.md, XDNA-BATCH-GATE, XDNA-WORK-FLOOR,
+// XDNA-SIZE-POLICY):
+//   batch    a MUL_MAT is taken only when its batch (dst ne[1]) is at least
+//            GGML_XDNA_MIN_BATCH (1024);
+//   floor    and its work 2*K*N*batch / 1e6 (integer MFLOP) is at least
+//            GGML_XDNA_MIN_MFLOP (256);
+//   weight   and its left side is a plain 2-D leaf (not a view, not computed)
+//            of a type the converter handles, the right side fp32 and 2-D,
+//            and K a whole number of 8-value blocks (this build's shape rule);
+//   block    a small op (RMS_NORM, MUL by a row, ADD, SCALE, GLU, ROPE) is
+//            taken when one input comes from a taken op, it covers the batch,
+//            its row inputs are kept leaves, and no same-shape input may sit
+//            in host memory (graph inputs, GET_ROWS results);
+//   never    MUL_MAT_ID and every other op; offload_op claims nothing.
+// Each rule is checked on both sides of its boundary, with the expected
+// answer computed here from the rule where it is arithmetic. BASELINE's
+// small-model configuration (hidden 1024, Q8_0, chunks of 256 to 4096
+// tokens) is checked launch by launch. Runs with the thresholds at their
+// defaults, on the GPU or under GGML_XDNA_PLAN_ONLY=1.
+#include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
 
 #include "mini_ggml.h"
 
-static ggml_tensor * make_mul_mat(ggml_context * ctx, ggml_type wtype, int64_t k, int64_t n, int64_t batch) {
-    ggml_tensor * a = ggml_new_tensor_2d(ctx, wtype, k, n);
-    ggml_tensor * b = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, k, batch);
-    return ggml_mul_mat(ctx, a, b);
+namespace {
+
+ggml_context * g_ctx;
+ggml_backend_dev_t g_dev;
+int g_cases;
+
+ggml_tensor * weight(ggml_type t, int64_t k, int64_t n) { return ggml_new_tensor_2d(g_ctx, t, k, n); }
+ggml_tensor * rows(int64_t k, int64_t m) { return ggml_new_tensor_2d(g_ctx, GGML_TYPE_F32, k, m); }
+ggml_tensor * matmul(ggml_type t, int64_t k, int64_t n, int64_t m) { return ggml_mul_mat(g_ctx, weight(t, k, n), rows(k, m)); }
+
+// Asks supports_op about `op` and checks the answer is `want`.
+void expect(ggml_tensor * op, bool want, const char * rule, const char * fmt, ...) __attribute__((format(printf, 4, 5)));
+void expect(ggml_tensor * op, bool want, const char * rule, const char * fmt, ...) {
+    char what[256];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(what, sizeof what, fmt, ap);
+    va_end(ap);
+    const bool got = ggml_backend_dev_supports_op(g_dev, op);
+    test_check(got == want, "[%s] %s: %s", rule, what, want ? "taken" : "left to the scheduler");
+    g_cases++;
 }
+
+// the integer MFLOP the floor compares
+int64_t mflop(int64_t k, int64_t n, int64_t m) { return 2 * k * n * m / 1000000; }
+
+void batch_rule() {
+    // below, at and above the threshold, for a 2048 x 2048 q4_K weight
+    for (int64_t m : {1, 256, 512, 1000, 1023, 1024, 1025, 1536, 2048, 4096, 8192})
+        expect(matmul(GGML_TYPE_Q4_K, 2048, 2048, m), m >= 1024, "batch", "q4_K 2048x2048 at batch %lld",
+               (long long) m);
+}
+
+void floor_rule() {
+    // at batch 1024 and K 1024, the floor of 256 MFLOP falls between N = 122 and 123
+    for (int64_t n : {32, 64, 120, 122, 123, 128, 4096}) {
+        const int64_t w = mflop(1024, n, 1024);
+        expect(matmul(GGML_TYPE_Q8_0, 1024, n, 1024), w >= 256, "floor", "q8_0 1024x%lld at batch 1024 (%lld MFLOP)",
+               (long long) n, (long long) w);
+    }
+    // a wide batch does not lift a matmul over the floor by itself: 64 rows of K 256 at 4096 tokens
+    expect(matmul(GGML_TYPE_Q8_0, 256, 64, 4096), mflop(256, 64, 4096) >= 256, "floor",
+           "q8_0 256x64 at batch 4096 (%lld MFLOP)", (long long) mflop(256, 64, 4096));
+}
+
+void weight_rule() {
+    const ggml_type convertible[] = {GGML_TYPE_F32,  GGML_TYPE_F16,  GGML_TYPE_BF16, GGML_TYPE_Q4_0, GGML_TYPE_Q4_1,
+                                     GGML_TYPE_Q5_0, GGML_TYPE_Q5_1, GGML_TYPE_Q8_0, GGML_TYPE_Q2_K, GGML_TYPE_Q3_K,
+                                     GGML_TYPE_Q4_K, GGML_TYPE_Q5_K, GGML_TYPE_Q6_K};
+    for (ggml_type t : convertible) expect(matmul(t, 2048, 2048, 2048), true, "weight", "ggml type %d", (int) t);
+    expect(matmul(GGML_TYPE_Q8_K, 2048, 2048, 2048), false, "weight", "q8_K (a dot-product intermediate, no converter)");
+    expect(matmul(GGML_TYPE_F32, 2052, 2048, 2048), false, "weight", "K = 2052, not a whole number of blocks");
+    expect(matmul(GGML_TYPE_F32, 2056, 2048, 2048), true, "weight", "K = 2056, a whole number of blocks");
+    // keys read from the cache are views; the score matrix is computed
+    ggml_tensor * cache = ggml_new_tensor_2d(g_ctx, GGML_TYPE_F16, 2048, 8192);
+    expect(ggml_mul_mat(g_ctx, ggml_view_2d(g_ctx, cache, 2048, 2048, cache->nb[1], 0), rows(2048, 2048)), false,
+           "weight", "left side a view of a larger tensor");
+    ggml_tensor * made = ggml_add(g_ctx, weight(GGML_TYPE_F32, 2048, 2048), weight(GGML_TYPE_F32, 2048, 2048));
+    expect(ggml_mul_mat(g_ctx, made, rows(2048, 2048)), false, "weight", "left side computed by another op");
+    expect(made, false, "never", "an ADD of two leaves");
+    expect(ggml_mul_mat(g_ctx, weight(GGML_TYPE_Q8_0, 2048, 2048), ggml_new_tensor_3d(g_ctx, GGML_TYPE_F32, 2048, 1024, 2)),
+           false, "weight", "a 3-D right side");
+}
+
+void block_rule() {
+    ggml_tensor * x = rows(2048, 2048);
+    ggml_tensor * up = ggml_mul_mat(g_ctx, weight(GGML_TYPE_Q4_0, 2048, 2048), x);
+    ggml_tensor * gate = ggml_mul_mat(g_ctx, weight(GGML_TYPE_Q4_0, 2048, 2048), x);
+    ggml_tensor * short_mm = matmul(GGML_TYPE_Q4_K, 2048, 2048, 512);
+    ggml_tensor * embd = ggml_get_rows(g_ctx, weight(GGML_TYPE_Q4_0, 2048, 32000), ggml_new_tensor_1d(g_ctx, GGML_TYPE_I32, 2048));
+    ggml_tensor * input = rows(2048, 2048);
+    ggml_set_input(input);
+    ggml_tensor * bias = ggml_new_tensor_1d(g_ctx, GGML_TYPE_F32, 2048);
+    ggml_tensor * made_row = ggml_scale(g_ctx, ggml_new_tensor_1d(g_ctx, GGML_TYPE_F32, 2048), 3.0f);
+
+    expect(ggml_add(g_ctx, up, gate), true, "block", "ADD of two taken matmuls");
+    expect(ggml_add(g_ctx, up, bias), true, "block", "ADD of a kept bias row to a taken matmul");
+    expect(ggml_add(g_ctx, up, made_row), false, "block", "ADD of a computed row");
+    expect(ggml_add(g_ctx, embd, up), false, "block", "ADD of the token embeddings (GET_ROWS) and a taken matmul");
+    expect(ggml_add(g_ctx, up, embd), false, "block", "the same ADD with its inputs swapped");
+    expect(ggml_add(g_ctx, input, up), false, "block", "ADD of a graph input and a taken matmul");
+    expect(ggml_scale(g_ctx, up, 0.5f), true, "block", "SCALE of a taken matmul");
+    expect(ggml_scale(g_ctx, short_mm, 0.5f), false, "block", "SCALE of a matmul the batch rule left");
+    expect(ggml_geglu_split(g_ctx, gate, up), true, "block", "GeGLU over two taken matmuls");
+    expect(ggml_swiglu_split(g_ctx, gate, up), true, "block", "SwiGLU over two taken matmuls");
+    expect(ggml_swiglu(g_ctx, ggml_mul_mat(g_ctx, weight(GGML_TYPE_Q4_0, 2048, 4096), x)), true, "block",
+           "SwiGLU over one taken matmul holding gate and up");
+    ggml_tensor * norm = ggml_rms_norm(g_ctx, up, 1e-6f);
+    expect(norm, true, "block", "RMS_NORM of a taken matmul");
+    expect(ggml_mul(g_ctx, norm, ggml_new_tensor_1d(g_ctx, GGML_TYPE_F32, 2048)), true, "block",
+           "MUL of that norm by a kept scale row");
+    // ROPE over the heads of a projection: NeoX is run, a multi-section mode is not
+    ggml_tensor * heads = ggml_new_tensor_3d(g_ctx, GGML_TYPE_F32, 128, 16, 2048);
+    heads->op = GGML_OP_RESHAPE;
+    heads->src[0] = ggml_reshape_2d(g_ctx, up, 128, 16 * 2048);
+    heads->view_src = up;
+    ggml_tensor * pos = ggml_new_tensor_1d(g_ctx, GGML_TYPE_I32, 2048);
+    expect(ggml_rope_ext(g_ctx, heads, pos, nullptr, 128, GGML_ROPE_TYPE_NEOX, 0, 1e6f, 1.0f, 0.0f, 1.0f, 32.0f, 1.0f),
+           true, "block", "NeoX ROPE of a taken projection's heads");
+    expect(ggml_rope_ext(g_ctx, heads, pos, nullptr, 128, 8, 0, 1e6f, 1.0f, 0.0f, 1.0f, 32.0f, 1.0f), false, "block",
+           "ROPE in a multi-section mode");
+}
+
+void never_rule() {
+    ggml_tensor * experts = ggml_new_tensor_3d(g_ctx, GGML_TYPE_Q4_0, 2048, 2048, 8);
+    ggml_tensor * ids = ggml_new_tensor_2d(g_ctx, GGML_TYPE_I32, 1, 2048);
+    expect(ggml_mul_mat_id(g_ctx, experts, ggml_new_tensor_3d(g_ctx, GGML_TYPE_F32, 2048, 1, 2048), ids), false, "never",
+           "an expert step (MUL_MAT_ID)");
+    expect(matmul(GGML_TYPE_Q4_0, 2048, 2048, 2048), true, "never", "a plain matmul asked after it");
+    test_check(!ggml_backend_dev_offload_op(g_dev, matmul(GGML_TYPE_Q4_K, 2048, 2048, 4096)),
+               "[never] offload_op claims nothing (the cache is built per weight, not per op)");
+}
+
+// a hidden-1024 Q8_0 layer at each chunk size
+void small_model_config() {
+    struct mm { const char * name; int64_t k, n; };
+    const mm layer[] = {{"q", 1024, 1024}, {"k", 1024, 1024}, {"v", 1024, 1024}, {"o", 1024, 1024},
+                        {"gate", 1024, 4096}, {"up", 1024, 4096}, {"down", 4096, 1024}};
+    for (int64_t m : {256, 512, 1024, 1536, 4096})
+        for (const mm & w : layer) {
+            const bool want = m >= 1024 && mflop(w.k, w.n, m) >= 256;
+            expect(matmul(GGML_TYPE_Q8_0, w.k, w.n, m), want, "config 4", "%s (%lldx%lld) at a %lld-token chunk", w.name,
+                   (long long) w.k, (long long) w.n, (long long) m);
+        }
+}
+
+}  // namespace
 
 int main() {
     ggml_backend_load_all();
-    ggml_backend_dev_t dev = ggml_backend_dev_by_name("XDNA0");
-    if (!dev) {
-        fprintf(stderr, "XDNA0 device not registered - is GGML_BACKEND_PATH set, and is there a GPU?\n");
+    g_dev = ggml_backend_dev_by_name("XDNA0");
+    if (!g_dev) {
+        fprintf(stderr, "no XDNA0 device: set GGML_BACKEND_PATH to libggml-zest.so (and run on a GPU, or planning only)\n");
         return 2;
     }
     const char * po = getenv("GGML_XDNA_PLAN_ONLY");
-    const bool plan_only = po && *po && po[0] != '0';
+    const bool planning = po && *po && po[0] != '0';
 
-    test_check(ggml_backend_dev_type(dev) == GGML_BACKEND_DEVICE_TYPE_GPU,
-               "device registers as a GPU (the model's memory is on it)");
-    ggml_backend_buffer_type_t own = ggml_backend_dev_buffer_type(dev);
-    test_check(own && !ggml_backend_buft_is_host(own), "its buffer type is its own device memory");
-    test_check(ggml_backend_dev_supports_buft(dev, own), "it reads its own buffers");
-    ggml_backend_dev_t cpu = ggml_backend_dev_by_type(GGML_BACKEND_DEVICE_TYPE_CPU);
-    test_check(cpu && ggml_backend_dev_supports_buft(dev, ggml_backend_dev_buffer_type(cpu)),
-               "it reads host buffers (graph inputs such as positions)");
-    size_t free = 1, total = 0;
-    ggml_backend_dev_memory(dev, &free, &total);
-    if (plan_only)
-        test_check(free == 0 && total == 0, "planning only: no memory reported");
-    else
-        test_check(total > 0 && free > 0 && free <= total, "reports the GPU's HBM (free %.1f of %.1f GB)", free / 1e9,
-                   total / 1e9);
+    // what the scheduler reads before any op
+    test_check(ggml_backend_dev_type(g_dev) == GGML_BACKEND_DEVICE_TYPE_GPU, "[device] a GPU device");
+    ggml_backend_buffer_type_t own = ggml_backend_dev_buffer_type(g_dev);
+    test_check(own && !ggml_backend_buft_is_host(own) && ggml_backend_dev_supports_buft(g_dev, own),
+               "[device] its buffer type is device memory it reads");
+    ggml_backend_dev_t host = ggml_backend_dev_by_type(GGML_BACKEND_DEVICE_TYPE_CPU);
+    test_check(host && ggml_backend_dev_supports_buft(g_dev, ggml_backend_dev_buffer_type(host)),
+               "[device] host buffers are readable too, so pieces never wait on copied inputs");
+    size_t free = 7, total = 7;
+    ggml_backend_dev_memory(g_dev, &free, &total);
+    test_check(planning ? free == 0 && total == 0 : total > 0 && free > 0 && free <= total,
+               "[device] memory: %zu free of %zu (none when planning only)", free, total);
     ggml_backend_dev_props props;
-    ggml_backend_dev_get_props(dev, &props);
-    test_check(!props.caps.async && !props.caps.events, "no async or events: graph_compute returns with results done");
+    ggml_backend_dev_get_props(g_dev, &props);
+    test_check(!props.caps.async && !props.caps.events, "[device] synchronous: graph_compute returns with results done");
 
-    ggml_init_params ip = {ggml_tensor_overhead() * 256, nullptr, true};
-    ggml_context * ctx = ggml_init(ip);
-    const int64_t k = 2048, n = 2048;
-
-    test_check(!ggml_backend_dev_supports_op(dev, make_mul_mat(ctx, GGML_TYPE_Q4_K, k, n, 1)),
-               "batch 1 (reply generation) is not claimed");
-    test_check(!ggml_backend_dev_supports_op(dev, make_mul_mat(ctx, GGML_TYPE_Q4_K, k, n, 512)),
-               "batch 512 (llama.cpp's default chunk) is not claimed");
-    test_check(!ggml_backend_dev_supports_op(dev, make_mul_mat(ctx, GGML_TYPE_Q4_K, k, n, 1023)),
-               "batch 1023 is not claimed (below the default threshold of 1024)");
-    test_check(ggml_backend_dev_supports_op(dev, make_mul_mat(ctx, GGML_TYPE_Q4_K, k, n, 1024)),
-               "batch 1024, q4_K 2048x2048 is claimed");
-    test_check(ggml_backend_dev_supports_op(dev, make_mul_mat(ctx, GGML_TYPE_Q4_0, k, n, 2048)),
-               "batch 2048, q4_0 is claimed");
-    test_check(ggml_backend_dev_supports_op(dev, make_mul_mat(ctx, GGML_TYPE_F32, k, n, 2048)),
-               "batch 2048, f32 is claimed");
-    // every GGUF float and block type has a converter; Q8_K (a dot-product
-    // intermediate, no weight of a model file) has none and is not claimed
-    for (ggml_type t : {GGML_TYPE_F16, GGML_TYPE_BF16, GGML_TYPE_Q4_1, GGML_TYPE_Q5_0, GGML_TYPE_Q5_1, GGML_TYPE_Q8_0,
-                        GGML_TYPE_Q2_K, GGML_TYPE_Q3_K, GGML_TYPE_Q5_K, GGML_TYPE_Q6_K}) {
-        char what[64];
-        snprintf(what, sizeof what, "batch 2048, type %d is claimed", (int) t);
-        test_check(ggml_backend_dev_supports_op(dev, make_mul_mat(ctx, t, k, n, 2048)), "%s", what);
-    }
-    test_check(!ggml_backend_dev_supports_op(dev, make_mul_mat(ctx, GGML_TYPE_Q8_K, k, n, 2048)),
-               "a type with no converter (q8_K) is not claimed");
-    // 2*1024*64*1024 = 134 MFLOP, under the 256 MFLOP floor
-    test_check(!ggml_backend_dev_supports_op(dev, make_mul_mat(ctx, GGML_TYPE_Q4_K, 1024, 64, 1024)),
-               "a tiny matmul is not claimed even at a large batch");
-    // 2*1024*128*1024 = 268 MFLOP: just over
-    test_check(ggml_backend_dev_supports_op(dev, make_mul_mat(ctx, GGML_TYPE_Q8_0, 1024, 128, 1024)),
-               "a matmul just over the floor is claimed");
-    test_check(!ggml_backend_dev_supports_op(dev, make_mul_mat(ctx, GGML_TYPE_F32, 2052, n, 2048)),
-               "K not a multiple of the 8-value block is not claimed");
-    {
-        ggml_tensor * a = ggml_new_tensor_2d(ctx, GGML_TYPE_Q8_0, k, n);
-        ggml_tensor * b = ggml_new_tensor_3d(ctx, GGML_TYPE_F32, k, 1024, 2);
-        test_check(!ggml_backend_dev_supports_op(dev, ggml_mul_mat(ctx, a, b)), "a batched (3-D) input is not claimed");
-    }
-
-    // attention's matmuls read keys from the cache through views, not weights
-    {
-        ggml_tensor * cache = ggml_new_tensor_2d(ctx, GGML_TYPE_F16, k, 4 * n);
-        ggml_tensor * view = ggml_view_2d(ctx, cache, k, n, cache->nb[1], 0);
-        ggml_tensor * b = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, k, 1024);
-        test_check(!ggml_backend_dev_supports_op(dev, ggml_mul_mat(ctx, view, b)),
-                   "a matmul whose left side is a view (a cache read, not a weight) is not claimed");
-        ggml_tensor * computed =
-            ggml_add(ctx, ggml_new_tensor_2d(ctx, GGML_TYPE_F32, k, n), ggml_new_tensor_2d(ctx, GGML_TYPE_F32, k, n));
-        test_check(!ggml_backend_dev_supports_op(dev, ggml_mul_mat(ctx, computed, b)),
-                   "a matmul whose left side is computed (not a weight) is not claimed");
-        test_check(!ggml_backend_dev_supports_op(dev, computed), "other ops (ADD) on their own are not claimed");
-    }
-
-    // small ops next to our matmuls (block claiming), except those reading a
-    // same-shape tensor that may sit in host memory
-    {
-        ggml_tensor * x = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, k, 2048);
-        ggml_tensor * mm1 = ggml_mul_mat(ctx, ggml_new_tensor_2d(ctx, GGML_TYPE_Q4_0, k, n), x);
-        ggml_tensor * mm2 = ggml_mul_mat(ctx, ggml_new_tensor_2d(ctx, GGML_TYPE_Q4_0, k, n), x);
-        test_check(ggml_backend_dev_supports_op(dev, ggml_add(ctx, mm1, mm2)),
-                   "an ADD of two claimed matmuls is claimed (block claiming)");
-        ggml_tensor * emb = ggml_get_rows(ctx, ggml_new_tensor_2d(ctx, GGML_TYPE_Q4_0, k, 32000),
-                                          ggml_new_tensor_1d(ctx, GGML_TYPE_I32, 2048));
-        test_check(!ggml_backend_dev_supports_op(dev, ggml_add(ctx, emb, mm1)),
-                   "an ADD of a claimed matmul and the token embeddings (GET_ROWS) is not claimed");
-        test_check(!ggml_backend_dev_supports_op(dev, ggml_add(ctx, mm1, emb)), "... in either order");
-        ggml_tensor * in = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, k, 2048);
-        ggml_set_input(in);
-        test_check(!ggml_backend_dev_supports_op(dev, ggml_add(ctx, in, mm1)),
-                   "an ADD of a claimed matmul and a graph input is not claimed");
-        ggml_tensor * bias = ggml_new_tensor_1d(ctx, GGML_TYPE_F32, n);
-        test_check(ggml_backend_dev_supports_op(dev, ggml_add(ctx, mm1, bias)),
-                   "an ADD of a bias row to a claimed matmul is claimed");
-        ggml_tensor * made = ggml_scale(ctx, ggml_new_tensor_1d(ctx, GGML_TYPE_F32, n), 2.0f);
-        test_check(!ggml_backend_dev_supports_op(dev, ggml_add(ctx, mm1, made)),
-                   "an ADD of a computed row (not a kept leaf) is not claimed");
-        test_check(ggml_backend_dev_supports_op(dev, ggml_scale(ctx, mm1, 0.25f)), "a SCALE of a claimed matmul is claimed");
-        test_check(ggml_backend_dev_supports_op(dev, ggml_geglu_split(ctx, mm1, mm2)),
-                   "a GeGLU of two claimed matmuls is claimed");
-        ggml_tensor * fused = ggml_mul_mat(ctx, ggml_new_tensor_2d(ctx, GGML_TYPE_Q4_0, k, 2 * n), x);
-        test_check(ggml_backend_dev_supports_op(dev, ggml_swiglu(ctx, fused)),
-                   "a SwiGLU on one claimed matmul holding gate and up is claimed");
-        ggml_tensor * norm = ggml_rms_norm(ctx, mm1, 1e-6f);
-        test_check(ggml_backend_dev_supports_op(dev, norm), "an RMS_NORM of a claimed matmul is claimed");
-        test_check(ggml_backend_dev_supports_op(dev, ggml_mul(ctx, norm, ggml_new_tensor_1d(ctx, GGML_TYPE_F32, n))),
-                   "... and its MUL by a scale row");
-        ggml_tensor * small_x = ggml_new_tensor_2d(ctx, GGML_TYPE_F32, k, 512);
-        ggml_tensor * mm_small = ggml_mul_mat(ctx, ggml_new_tensor_2d(ctx, GGML_TYPE_Q4_K, k, n), small_x);
-        test_check(!ggml_backend_dev_supports_op(dev, ggml_scale(ctx, mm_small, 0.5f)),
-                   "a small op next to an unclaimed (small-batch) matmul is not claimed");
-        // ROPE on the q projection, viewed as heads
-        ggml_tensor * q = ggml_reshape_2d(ctx, mm1, 128, 16 * 2048);
-        ggml_tensor * q3 = ggml_new_tensor_3d(ctx, GGML_TYPE_F32, 128, 16, 2048);
-        q3->op = GGML_OP_RESHAPE;
-        q3->src[0] = q;
-        q3->view_src = mm1;
-        ggml_tensor * pos = ggml_new_tensor_1d(ctx, GGML_TYPE_I32, 2048);
-        test_check(ggml_backend_dev_supports_op(dev, ggml_rope_ext(ctx, q3, pos, nullptr, 128, GGML_ROPE_TYPE_NEOX, 0,
-                                                                   1e6f, 1.0f, 0.0f, 1.0f, 32.0f, 1.0f)),
-                   "a NeoX ROPE of a claimed projection is claimed");
-        test_check(!ggml_backend_dev_supports_op(dev, ggml_rope_ext(ctx, q3, pos, nullptr, 128, 8, 0, 1e6f, 1.0f,
-                                                                    0.0f, 1.0f, 32.0f, 1.0f)),
-                   "a ROPE of another mode (multi-section) is not claimed");
-    }
-
-    // A mixture-of-experts model's expert step is a MUL_MAT_ID: not taken, but
-    // the model's ordinary matmuls still are (the backend warns instead).
-    {
-        ggml_tensor * experts = ggml_new_tensor_3d(ctx, GGML_TYPE_Q4_0, k, n, 8);
-        ggml_tensor * rows = ggml_new_tensor_3d(ctx, GGML_TYPE_F32, k, 1, 2048);
-        ggml_tensor * ids = ggml_new_tensor_2d(ctx, GGML_TYPE_I32, 1, 2048);
-        test_check(!ggml_backend_dev_supports_op(dev, ggml_mul_mat_id(ctx, experts, rows, ids)),
-                   "the expert step (MUL_MAT_ID) is not claimed");
-        test_check(ggml_backend_dev_supports_op(dev, make_mul_mat(ctx, GGML_TYPE_Q4_0, k, n, 2048)),
-                   "... and an ordinary matmul is still claimed afterwards");
-    }
-
-    test_check(!ggml_backend_dev_offload_op(dev, make_mul_mat(ctx, GGML_TYPE_Q4_K, k, n, 2048)),
-               "offload_op never claims an op (no per-op weight copies)");
-
-    ggml_free(ctx);
-    printf("%s\n", test_failures() ? "FAILED" : "ALL PASS");
+    ggml_init_params ip = {ggml_tensor_overhead() * 1024, nullptr, true};
+    g_ctx = ggml_init(ip);
+    batch_rule();
+    floor_rule();
+    weight_rule();
+    block_rule();
+    never_rule();
+    small_model_config();
+    ggml_free(g_ctx);
+    printf("%d supports_op cases\n%s\n", g_cases, test_failures() ? "FAILED" : "ALL PASS");
     return test_failures() ? 1 : 0;
 }

@@ -56,6 +56,25 @@ def test_safe_start_host_only():
     run("test_safe_start", "--host-only")
 
 
+def test_two_contexts_on_threads_planning():
+    run("test_contexts", GGML_XDNA_PLAN_ONLY="1", GGML_XDNA_MAX_COPY_GB="0.05")
+
+
+def test_host_code_under_sanitizers():
+    # the host side rebuilt with ThreadSanitizer and with AddressSanitizer +
+    # UBSan (tests/cpp/Makefile, `sanitize`), the gate, budget, safe-start and
+    # two-context programs run under each; any report or failure fails
+    if not list((ROOT / "ggml-xdna_amd" / "_build").glob("*.hip.o")):
+        pytest.fail("the kernel objects are not built (run __graft_entry__.build())")
+    env = {k: v for k, v in os.environ.items() if k not in SETTINGS}
+    r = subprocess.run(["make", "-s", "-C", str(ROOT / "tests" / "cpp"), "-j8", "sanitize-run"], env=env,
+                       capture_output=True, text=True, timeout=600)
+    out = r.stdout + r.stderr
+    print(out)
+    assert r.returncode == 0, out
+    assert out.count("ALL PASS") == 8, out
+
+
 # ---- on the GPU ---------------------------------------------------------------------------
 
 @pytest.mark.gpu

@@ -1,0 +1,124 @@
+"""Every byte the GEMM kernels read or write through a scalar offset lies
+inside its operand, for every tile, split and wave of the launches the
+planner can make. The hardware range check of a buffer access covers only its
+vector offset, so an access whose scalar offset (a K-step's slab, a row block)
+runs past the operand would read or write whatever memory follows it; the
+kernel must never form one. This restates, in integers, the offsets of
+gemm.hip's a_loader (the consumers' A fragments), producer::load_w (the W
+slab) and fixup's partial sums, with the step sequences of run_tile and
+produce, and checks the largest byte each launch touches against the
+operand's size. (store_tile's stores and residual reads keep their whole
+offset in the vector offset; test_gemm_gpu's ragged residual test covers
+them.) CPU only."""
+from __future__ import annotations
+
+import itertools
+
+import pytest
+
+XGROUP_BYTES, XSUB_BYTES = 4096, 1024
+TILE_ROWS, TILE_BYTES, TILE_MANT, TILE_K = 16, 1152, 1024, 64
+
+
+def rows_pad(r):
+    return (r + 255) // 256 * 256
+
+
+def k_steps(k):
+    return (k + 63) // 64
+
+
+# (BM, BN, consumer waves) of cfg_big, cfg_small and cfg_glu
+CONFIGS = [(256, 128, 4), (128, 128, 4), (256, 128, 8)]
+
+
+def consumer_steps(ns, last):
+    """run_tile's A loads, as K-step indices from the tile's first step:
+    steps 0 and 1 before the loop, steps k+2 and k+3 in each pair of the loop,
+    each clamped to the operand's last step."""
+    steps = [0, min(1, last)]
+    k = 0
+    while k + 1 < ns:
+        steps += [min(k + 2, last), min(k + 3, last)]
+        k += 2
+    return steps
+
+
+def producer_steps(ns, last):
+    """produce()'s W loads: steps 0-3 in the prologue (clamped), k+4 and k+5
+    in the steady state, then the guarded tail loads."""
+    steps = [0, min(1, last), min(2, last), min(3, last)]
+    k = 0
+    while k + 5 < ns:
+        steps += [k + 4, k + 5]
+        k += 2
+    while k < ns:
+        if k + 2 < ns and k + 4 < ns:
+            steps.append(k + 4)
+        if k + 1 < ns and k + 3 < ns and k + 5 < ns:
+            steps.append(k + 5)
+        k += 2
+    return steps
+
+
+def check_launch(M, N, K, BM, BN, CWM, S):
+    nk = k_steps(K)
+    Mp, Np = rows_pad(M), rows_pad(N)
+    ks = Mp // 32 * XGROUP_BYTES             # p.a_kstride
+    wks = Np // TILE_ROWS * TILE_BYTES       # W.w_kstride
+    a_size, w_size = ks * nk, wks * nk       # the buffer resources' sizes
+    WM, TI = BM // CWM, BM // CWM // 32
+    mt, nt = (M + BM - 1) // BM, (N + BN - 1) // BN
+    # the A fragment of the highest vector offset: wave's last 32-row group,
+    # lane 63 (row 31, K-half 1), sub-step 3, 16 bytes
+    a_vmax = lambda wm: (wm * WM // 32 + TI - 1) * XGROUP_BYTES + 31 * 32 + 16 + 3 * XSUB_BYTES + 16
+    # the producer thread of the highest offset: tile BN/16-1, row 15, h 1, second 16 bytes
+    w_vmax = (BN // 16 - 1) * TILE_BYTES + 15 * TILE_K + 32 + 16 + 16
+    w_emax = (BN // 16 - 1) * TILE_BYTES + TILE_MANT + 15 * 8 + 4 + 4
+    for split in range(S):
+        k0 = split * nk // S
+        ns = (split + 1) * nk // S - k0
+        last = nk - 1 - k0
+        a_hi = max(consumer_steps(ns, last))
+        w_hi = max(producer_steps(ns, last))
+        assert k0 + a_hi <= nk - 1 and k0 + w_hi <= nk - 1, (M, N, K, BM, S, split)
+        for tm in range(mt):
+            m0 = tm * BM
+            a0 = m0 // 32 * XGROUP_BYTES + k0 * ks
+            for wm in range(CWM):
+                assert a0 + a_hi * ks + a_vmax(wm) <= a_size, ("A", M, N, K, BM, S, split, tm, wm)
+        for tn in range(nt):
+            w0 = (tn * BN) // TILE_ROWS * TILE_BYTES + k0 * wks
+            assert w0 + w_hi * wks + max(w_vmax, w_emax) <= w_size, ("W", M, N, K, BN, S, split, tn)
+    if S > 1:
+        # fixup: unit (u*T + t), wave, 1 KB pieces, all inside T*S*BM*BN*4
+        T = mt * nt
+        unit_bytes = BM * BN * 4
+        top = ((S - 1) * T + T - 1) * unit_bytes + (CWM - 1) * WM * BN * 4 + WM * BN * 4
+        assert top <= T * S * unit_bytes
+
+
+SHAPES = [
+    (1, 256, 64), (7, 200, 200), (100, 96, 8), (129, 1000, 520), (300, 200, 256), (600, 1000, 8192),
+    (1024, 2560, 2560), (2048, 2560, 4096), (2048, 2560, 9728), (2048, 6144, 2560), (2048, 19456, 2560),
+    (4096, 5120, 17408), (4096, 34816, 5120), (1536, 1024, 4096), (256, 4096, 1024),
+]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_scalar_offsets_stay_inside_operands(M, N, K):
+    nk = k_steps(K)
+    for (BM, BN, CWM), S in itertools.product(CONFIGS, range(1, 17)):
+        if S > 1 and nk // S < 4:
+            continue  # the planner never splits below four steps a split
+        check_launch(M, N, K, BM, BN, CWM, S)
+
+
+def test_unclamped_prefetch_would_leave_the_operand():
+    # the check above has teeth: the step sequence without the clamp (the
+    # kernel before it was added) reads past A's last step
+    nk, ns, last = 40, 40, 39
+    steps = [0, 1] + [s for k in range(0, ns - 1, 2) for s in (k + 2, k + 3)]
+    assert max(steps) > last
+    assert max(consumer_steps(ns, last)) == last
+
