@@ -52,6 +52,7 @@ SIGNATURES = {
     "zest_gemm": (_c_i, [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_p]),
     "zest_gemm_residual": (_c_i, [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p]),
     "zest_gemm_group": (_c_i, [_c_p, _c_i64, _c_i64, _c_i, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p]),
+    "zest_gemm_group_noalloc": (_c_i, [_c_p, _c_i64, _c_i64, _c_i, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p]),
     "zest_convert_weight_gu": (_c_i, [_c_i, _c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "zest_gemm_glu": (_c_i, [_c_i, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_p]),
     "zest_rms_norm": (_c_i, [_c_p, _c_i64, _c_i64, _c_f, _c_p, _c_p, _c_p, _c_p]),
@@ -229,17 +230,20 @@ def gemm_residual(a_packed, m: int, w_packed, n: int, k: int, res, out=None, non
     return out
 
 
-def gemm_group(a_packed, m: int, weights, ns, k: int, outs=None, nonfinite=None):
+def gemm_group(a_packed, m: int, weights, ns, k: int, outs=None, nonfinite=None, noalloc=False):
     """Several weights sharing one activation operand in one launch:
-    outs[i][m][ns[i]] = A . W_i^T. Returns the outputs."""
+    outs[i][m][ns[i]] = A . W_i^T. Returns the outputs. noalloc: through
+    zest_gemm_group_noalloc (split-K workspace from the library's static
+    array; the outputs must then be given)."""
     torch = _torch()
     n = len(weights)
     outs = [torch.empty((m, ni), dtype=torch.float32, device=a_packed.device) for ni in ns] if outs is None else outs
     P, I64 = ctypes.c_void_p * n, ctypes.c_int64 * n
     w = P(*[t.data_ptr() for t in weights])
     c = P(*[t.data_ptr() for t in outs])
-    check(lib().zest_gemm_group(_ptr(a_packed), m, k, n, w, I64(*ns), c, I64(*[t.stride(0) for t in outs]),
-                                _ptr(nonfinite), _stream()), "zest_gemm_group")
+    name = "zest_gemm_group_noalloc" if noalloc else "zest_gemm_group"
+    check(getattr(lib(), name)(_ptr(a_packed), m, k, n, w, I64(*ns), c, I64(*[t.stride(0) for t in outs]),
+                               _ptr(nonfinite), _stream()), name)
     return outs
 
 

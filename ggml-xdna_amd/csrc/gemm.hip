@@ -36,6 +36,14 @@
 #define ZEST_GEMM_GROUP_M 4  // tile rows per group of the tile order
 #endif
 
+// The split-K workspace of zest_gemm_group_noalloc: one static array per GPU
+// (the code object's own copy on each device, held until the process ends),
+// ZEST_NOALLOC_PARTIAL_BYTES of fp32 partial sums, then
+// ZEST_NOALLOC_COUNTERS counters. Host code never passes `scratch` itself to
+// a kernel (on the host it names a stand-in, not device memory): it uses the
+// device address that scratch_address() looks up per device.
+static __device__ __align__(256) uint8_t scratch[ZEST_NOALLOC_PARTIAL_BYTES + ZEST_NOALLOC_COUNTERS * 4];
+
 namespace {
 
 // Epilogues other than the GLU kinds (which are >= 0)
@@ -772,6 +780,30 @@ struct sk_space {
     size_t n_counters = 0;
 };
 
+// Clears n counters (a kernel, not a memset, so a captured graph replays it).
+__global__ void clear_counters(uint32_t * c, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) c[i] = 0;
+}
+
+// The device address of `scratch` on device `dev`, looked up once per device
+// with that device current.
+int scratch_address(int dev, uint8_t ** out) {
+    static std::mutex mu;
+    static uint8_t * addr[ZEST_MAX_DEVICES];  // no heap: the no-alloc entry point comes here on every call
+    if (dev < 0 || dev >= ZEST_MAX_DEVICES) return zest::fail(ZEST_E_ARG, "device %d: at most %d", dev, ZEST_MAX_DEVICES);
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void * p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return zest::fail(ZEST_E_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+        addr[dev] = (uint8_t *) p;
+    }
+    *out = addr[dev];
+    return ZEST_OK;
+}
+
 int cu_count(int dev) {
     static std::mutex mu;
     static int cus[ZEST_MAX_DEVICES];
@@ -870,9 +902,13 @@ gemm_plan plan_splits(int64_t T, int nk, int64_t P, double tile_bytes, double st
     return best;
 }
 
-// Plans and launches one GEMM (a group of weights, or the fused GLU).
+// Plans and launches one GEMM (a group of weights, or the fused GLU). A
+// split-K plan takes its workspace from `fixed` when given (no allocation:
+// a plan that does not fit is rejected, and the counters it uses are cleared
+// first), else from the per-stream workspace.
 template <class C, int EPI>
-int launch(gemm_params p, const int64_t * N, int splits, hipStream_t s, const char * name) {
+int launch(gemm_params p, const int64_t * N, int splits, hipStream_t s, const char * name,
+           const sk_space * fixed = nullptr) {
     p.mt = (int) ((p.M + C::BM - 1) / C::BM);
     int nt = 0;
     for (int i = 0; i < p.nw; i++) {
@@ -886,9 +922,21 @@ int launch(gemm_params p, const int64_t * N, int splits, hipStream_t s, const ch
     if (grid >= (1ll << 31) || (p.splits > 1 && grid * C::BM * C::BN * 4 >= (1ll << 31)))
         return zest::fail(ZEST_E_ARG, "%s: %lld tiles is too many", name, (long long) T);
     if (p.splits > 1) {
+        const size_t partial_bytes = (size_t) grid * C::BM * C::BN * 4, n_counters = (size_t) T * (C::NC / 64);
         sk_space sp;
-        const int st = sk_reserve(s, (size_t) grid * C::BM * C::BN * 4, (size_t) T * (C::NC / 64), sp, name);
-        if (st != ZEST_OK) return st;
+        if (fixed) {
+            if (partial_bytes > fixed->partial_bytes || n_counters > fixed->n_counters)
+                return zest::fail(ZEST_E_ARG,
+                                  "%s: this shape's split-K plan needs %zu bytes of partial sums and %zu counters; "
+                                  "the static workspace holds %zu bytes and %zu counters",
+                                  name, partial_bytes, n_counters, fixed->partial_bytes, fixed->n_counters);
+            sp = *fixed;
+            hipLaunchKernelGGL(clear_counters, dim3((unsigned) ((n_counters + 255) / 256)), dim3(256), 0, s,
+                               sp.counters, (int) n_counters);
+        } else {
+            const int st = sk_reserve(s, partial_bytes, n_counters, sp, name);
+            if (st != ZEST_OK) return st;
+        }
         p.partial = sp.partial;
         p.counters = sp.counters;
     }
@@ -924,9 +972,11 @@ int launch_mixed(gemm_params p, const int64_t * N, int64_t nbig, hipStream_t s, 
     return zest::check_launch(name);
 }
 
-// The tile shape and K splits of a launch (the cost model above).
+// The tile shape and K splits of a launch (the cost model above); `fixed` as
+// for launch().
 template <int EPI>
-int launch_any(gemm_params p, const int64_t * N, hipStream_t s, const char * name) {
+int launch_any(gemm_params p, const int64_t * N, hipStream_t s, const char * name,
+               const sk_space * fixed = nullptr) {
     int dev = 0;
     (void) hipGetDevice(&dev);
     const int64_t P = cu_count(dev);
@@ -944,8 +994,8 @@ int launch_any(gemm_params p, const int64_t * N, hipStream_t s, const char * nam
             if (mixed < big.cost && mixed < small.cost) return launch_mixed<EPI>(p, N, R * P, s, name);
         }
     }
-    if (small.cost < big.cost) return launch<cfg_small, EPI>(p, N, small.splits, s, name);
-    return launch<CB, EPI>(p, N, big.splits, s, name);
+    if (small.cost < big.cost) return launch<cfg_small, EPI>(p, N, small.splits, s, name, fixed);
+    return launch<CB, EPI>(p, N, big.splits, s, name, fixed);
 }
 
 // The parts of a launch's parameters common to every kind.
@@ -969,27 +1019,59 @@ gemm_weight weight_of(const void * w, int64_t N, float * c, int64_t ldc) {
     return g;
 }
 
-} // namespace
-
-extern "C" int zest_gemm_group(const void * a, int64_t M, int64_t K, int n, const void * const * w, const int64_t * N,
-                               float * const * c, const int64_t * ldc, uint32_t * nonfinite, void * stream) {
-    ZEST_REQUIRE(a && w && N && c && ldc, "zest_gemm_group: null pointer");
-    ZEST_REQUIRE(n >= 1 && n <= ZEST_GEMM_MAX_GROUP, "zest_gemm_group: %d weights (1..%d)", n, ZEST_GEMM_MAX_GROUP);
-    ZEST_REQUIRE(M > 0 && K > 0 && K % 8 == 0, "zest_gemm_group: M=%lld K=%lld", (long long) M, (long long) K);
-    ZEST_REQUIRE(zest_act_bytes(M, K) < (1ull << 31), "zest_gemm_group: activations must be under 2 GiB");
+// zest_gemm_group's checks and launch; `fixed` as for launch().
+int gemm_group(const void * a, int64_t M, int64_t K, int n, const void * const * w, const int64_t * N,
+               float * const * c, const int64_t * ldc, uint32_t * nonfinite, void * stream, const char * name,
+               const sk_space * fixed) {
+    ZEST_REQUIRE(a && w && N && c && ldc, "%s: null pointer", name);
+    ZEST_REQUIRE(n >= 1 && n <= ZEST_GEMM_MAX_GROUP, "%s: %d weights (1..%d)", name, n, ZEST_GEMM_MAX_GROUP);
+    ZEST_REQUIRE(M > 0 && K > 0 && K % 8 == 0, "%s: M=%lld K=%lld", name, (long long) M, (long long) K);
+    ZEST_REQUIRE(zest_act_bytes(M, K) < (1ull << 31), "%s: activations must be under 2 GiB", name);
     gemm_params p = base_params(a, M, K, nonfinite);
     p.nw = n;
     for (int i = 0; i < n; i++) {
-        ZEST_REQUIRE(w[i] && c[i], "zest_gemm_group: null weight or output %d", i);
-        ZEST_REQUIRE(N[i] > 0 && ldc[i] >= N[i], "zest_gemm_group: weight %d: N=%lld ldc=%lld", i, (long long) N[i],
+        ZEST_REQUIRE(w[i] && c[i], "%s: null weight or output %d", name, i);
+        ZEST_REQUIRE(N[i] > 0 && ldc[i] >= N[i], "%s: weight %d: N=%lld ldc=%lld", name, i, (long long) N[i],
                      (long long) ldc[i]);
         ZEST_REQUIRE(zest_bfp16_bytes(N[i], K) < (1ull << 31) &&
                          (uint64_t) zest_rows_padded(M) * (uint64_t) ldc[i] * 4 < (1ull << 31),
-                     "zest_gemm_group: weight %d and its output must be under 2 GiB (N=%lld ldc=%lld)", i,
+                     "%s: weight %d and its output must be under 2 GiB (N=%lld ldc=%lld)", name, i,
                      (long long) N[i], (long long) ldc[i]);
         p.wt[i] = weight_of(w[i], N[i], c[i], ldc[i]);
     }
-    return launch_any<EPI_PLAIN>(p, N, zest::as_stream(stream), "zest_gemm");
+    return launch_any<EPI_PLAIN>(p, N, zest::as_stream(stream), name, fixed);
+}
+
+} // namespace
+
+namespace zest {
+
+int scratch_setup(int dev) {
+    uint8_t * p = nullptr;
+    return scratch_address(dev, &p);
+}
+
+} // namespace zest
+
+extern "C" int zest_gemm_group(const void * a, int64_t M, int64_t K, int n, const void * const * w, const int64_t * N,
+                               float * const * c, const int64_t * ldc, uint32_t * nonfinite, void * stream) {
+    return gemm_group(a, M, K, n, w, N, c, ldc, nonfinite, stream, "zest_gemm", nullptr);
+}
+
+extern "C" int zest_gemm_group_noalloc(const void * a, int64_t M, int64_t K, int n, const void * const * w,
+                                       const int64_t * N, float * const * c, const int64_t * ldc,
+                                       uint32_t * nonfinite, void * stream) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return zest::fail(ZEST_E_HIP, "zest_gemm_group_noalloc: hipGetDevice failed");
+    uint8_t * base = nullptr;
+    const int st = scratch_address(dev, &base);
+    if (st != ZEST_OK) return st;
+    sk_space ws;
+    ws.partial = reinterpret_cast<float *>(base);
+    ws.partial_bytes = ZEST_NOALLOC_PARTIAL_BYTES;
+    ws.counters = reinterpret_cast<uint32_t *>(base + ZEST_NOALLOC_PARTIAL_BYTES);
+    ws.n_counters = ZEST_NOALLOC_COUNTERS;
+    return gemm_group(a, M, K, n, w, N, c, ldc, nonfinite, stream, "zest_gemm_group_noalloc", &ws);
 }
 
 extern "C" int zest_gemm(const void * a, int64_t M, const void * w, int64_t N, int64_t K, float * c, int64_t ldc,

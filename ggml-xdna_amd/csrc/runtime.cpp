@@ -63,7 +63,7 @@ int zest_init(int device) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return zest::fail(ZEST_E_UNSUPPORTED, "zest_init: device %d is %s; the kernels are built for gfx950", device,
                           prop.gcnArchName);
-    return ZEST_OK;
+    return zest::scratch_setup(device);
 }
 
 // npu_self_test (src/xdna-npu.cpp:142-184): small whole numbers, which the

@@ -20,6 +20,10 @@ inline hipStream_t as_stream(void * s) { return reinterpret_cast<hipStream_t>(s)
 // Non-zero when the last launch failed (the error is recorded).
 int check_launch(const char * what);
 
+// Looks up, with `dev` current, the device address of the no-alloc entry
+// point's static workspace on that device (once per device; zest_init calls it).
+int scratch_setup(int dev);
+
 // Devices the per-device tables hold.
 #define ZEST_MAX_DEVICES 64
 

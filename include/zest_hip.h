@@ -146,6 +146,27 @@ ZEST_API int zest_gemm_residual(const void *a, int64_t M, const void *w, int64_t
 ZEST_API int zest_gemm_group(const void *a, int64_t M, int64_t K, int n, const void *const *w, const int64_t *N,
                              float *const *c, const int64_t *ldc, uint32_t *nonfinite, void *stream);
 
+/* zest_gemm_group for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops and harnesses that forbid hipMalloc). It
+ * has no counterpart in the reference. It runs the launch zest_gemm_group
+ * plans for the same arguments (the same tiles, K splits and summation order,
+ * so the same results), but a split-K plan takes its workspace from a static
+ * device array the library holds on each GPU (ZEST_NOALLOC_PARTIAL_BYTES of
+ * partial sums and ZEST_NOALLOC_COUNTERS counters, kept until the process
+ * ends) instead of allocating one. A call whose plan needs more than that
+ * fails with ZEST_E_ARG and runs nothing; plans without split-K need none.
+ * It allocates nothing: no hipMalloc, no hipFree, no library allocation. The
+ * device address of the array is looked up once per device, by zest_init or
+ * else by the first call on that device (which should then not be under
+ * capture). Every call on one GPU shares that GPU's array, whose counters
+ * each call clears (with a kernel on `stream`) before use: calls that overlap
+ * on one GPU, on any streams, race. */
+#define ZEST_NOALLOC_PARTIAL_BYTES (64u << 20)
+#define ZEST_NOALLOC_COUNTERS 16384
+ZEST_API int zest_gemm_group_noalloc(const void *a, int64_t M, int64_t K, int n, const void *const *w,
+                                     const int64_t *N, float *const *c, const int64_t *ldc, uint32_t *nonfinite,
+                                     void *stream);
+
 /* A GLU's gate[F][K] and up[F][K] weights (GGUF rows of `type`, the same for
  * both; for a weight holding the gate and then the up, up = gate + F rows)
  * -> one packed weight of 2F rows for zest_gemm_glu (zest_bfp16_bytes(2F, K)
