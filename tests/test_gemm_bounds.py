@@ -122,3 +122,23 @@ def test_unclamped_prefetch_would_leave_the_operand():
     assert max(steps) > last
     assert max(consumer_steps(ns, last)) == last
 
+
+
+# (tile columns BN, wave columns WN, waves across) of the GLU launch (cfg_glu)
+GLU_CONFIGS = [(128, 128, 1)]
+
+
+@pytest.mark.parametrize("F", [32, 64, 96, 128, 160, 4096, 9728, 17408])
+def test_glu_epilogue_columns_stay_inside_the_operand(F):
+    # store_glu: the wave of tile column n0 (over the interleaved 2F rows)
+    # holds h columns c0 = n0/2 + wn*HW .. c0+HW-1, HW = WN/2; it writes the
+    # operand only when c0 < k_pad(F), and then every column it writes is
+    # inside the operand's padded width
+    Fp = (F + 63) // 64 * 64
+    for BN, WN, waves_n in GLU_CONFIGS:
+        HW = WN // 2
+        for n0 in range(0, (2 * F + BN - 1) // BN * BN, BN):
+            for wn in range(waves_n):
+                c0 = n0 // 2 + wn * HW
+                if c0 < Fp:
+                    assert c0 + HW <= Fp, (F, BN, WN, n0, wn)
