@@ -268,6 +268,95 @@ def traffic_summary(fetch_dir: str, write_dir: str) -> int:
     return 0
 
 
+# The stack's GEMM launch kinds, told apart by the kernel's template arguments
+# (demangled names): the q/k/v group runs as a mixed launch, O as a residual
+# launch, gate/up as the fused GLU launch (epilogue kind 2, SwiGLU), down as a
+# split-K residual launch.
+def gemm_kind(name: str):
+    if "gemm_kernel_mixed" in name:
+        return "qkv"
+    if "gemm_kernel<" not in name:
+        return None
+    if ", -2, true>" in name:
+        return "down"
+    if ", -2, false>" in name:
+        return "o"
+    if ", 2, false>" in name or ", 2, true>" in name:
+        return "gate_up"
+    return "other"
+
+
+def kind_flops(cfg, m: int) -> dict:
+    return {"qkv": 2.0 * m * (cfg.q + 2 * cfg.kv) * cfg.hidden, "o": 2.0 * m * cfg.hidden * cfg.q,
+            "gate_up": 4.0 * m * cfg.ffn * cfg.hidden, "down": 2.0 * m * cfg.hidden * cfg.ffn}
+
+
+def counter_summary(args) -> int:
+    """Per GEMM launch kind of one prompt step (bench.py --traffic-probe under
+    rocprofv3): average duration (--kernel-trace --stats), TFLOP/s and
+    fraction of bf16 peak, MFMA-busy share of the SIMD cycles and the clock
+    the kernel ran at (SQ_VALU_MFMA_BUSY_CYCLES, GRBM_GUI_ACTIVE; the latter
+    is summed over the 8 XCDs), and HBM bytes (FETCH_SIZE, WRITE_SIZE, scaled
+    by the calibration kernel as in --traffic-summary)."""
+    import csv
+    import glob
+    from collections import defaultdict
+    load_pkg()
+    from ggml_xdna_amd.stack import CONFIGS
+    cfg = CONFIGS[args.workload]
+    m = args.chunk or cfg.chunk
+    mfma_dir, fetch_dir, write_dir, trace_dir = args.counter_summary
+    sums = defaultdict(lambda: defaultdict(list))
+    calib = defaultdict(list)
+    for d in (mfma_dir, fetch_dir, write_dir):
+        per = defaultdict(float)
+        for r in _counter_rows(d):
+            per[(r["Dispatch_Id"], r["Kernel_Name"], r["Counter_Name"])] += float(r["Counter_Value"])
+        for (_, name, counter), v in per.items():
+            k = gemm_kind(name)
+            if k:
+                sums[k][counter].append(v)
+            elif "scale_kernel" in name:
+                calib[counter].append(v)
+    durs = defaultdict(list)
+    for f in glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            k = gemm_kind(r["Kernel_Name"])
+            if k:
+                durs[k].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3)
+    if not durs or not sums:
+        print("no GEMM rows in the given directories", file=sys.stderr)
+        return 1
+    fl = kind_flops(cfg, m)
+    out = {"workload": cfg.name, "chunk": m, "peak_tflops": BF16_PEAK, "simds": 1024, "kinds": {}}
+    total_us, total_flops = 0.0, 0.0
+    for k in ("qkv", "o", "gate_up", "down"):
+        if k not in durs:
+            continue
+        us = sum(durs[k]) / len(durs[k])
+        c = {n: sum(v) / len(v) for n, v in sums[k].items()}
+        xcd_cycles = c.get("GRBM_GUI_ACTIVE", 0.0) / 8.0
+        row = {"launches": len(durs[k]), "us": round(us, 2), "tflops": round(fl[k] / (us * 1e-6) / 1e12, 1),
+               "frac_of_peak": round(fl[k] / (us * 1e-6) / 1e12 / BF16_PEAK, 4)}
+        if xcd_cycles > 0 and "SQ_VALU_MFMA_BUSY_CYCLES" in c:
+            row["clock_ghz"] = round(xcd_cycles / (us * 1e3), 3)
+            row["mfma_busy_pct"] = round(100.0 * c["SQ_VALU_MFMA_BUSY_CYCLES"] / (xcd_cycles * 1024), 1)
+            if "SQ_INSTS_MFMA" in c:
+                row["mfma_insts"] = int(c["SQ_INSTS_MFMA"])
+        for counter, key in (("FETCH_SIZE", "fetch_bytes"), ("WRITE_SIZE", "write_bytes")):
+            if counter in c and calib.get(counter):
+                factor = CALIB_FLOATS * 4.0 / (max(calib[counter]) * 1024.0)
+                row[key] = int(c[counter] * 1024.0 * factor)
+        out["kinds"][k] = row
+        n_per_step = len(durs[k])
+        total_us += us * n_per_step
+        total_flops += fl[k] * n_per_step
+    out["all_gemm"] = {"us_per_step": round(total_us, 1), "tflops": round(total_flops / (total_us * 1e-6) / 1e12, 1),
+                       "frac_of_peak": round(total_flops / (total_us * 1e-6) / 1e12 / BF16_PEAK, 4)}
+    print(json.dumps(out, indent=1))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -281,9 +370,13 @@ def main() -> int:
     ap.add_argument("--traffic-probe", action="store_true", help="one step and the calibration kernel, for rocprofv3")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
     ap.add_argument("--hbm", action="store_true", help="HBM rates of the converter (every type) and the pack")
+    ap.add_argument("--counter-summary", nargs=4, metavar=("MFMA_DIR", "FETCH_DIR", "WRITE_DIR", "TRACE_DIR"),
+                    help="per GEMM launch kind: time, MFMA busy, clock, HBM bytes from rocprofv3 runs of --traffic-probe")
     args = ap.parse_args()
     if args.hbm:
         return hbm_kernels(args)
+    if args.counter_summary:
+        return counter_summary(args)
     if args.traffic_summary:
         return traffic_summary(*args.traffic_summary)
     if args.traffic_probe:
@@ -345,6 +438,16 @@ def main() -> int:
     if tf.exists() and stack.chunk == cfg.chunk and not args.unfused:
         traffic = round(json.loads(tf.read_text())["traffic_bytes_per_launch"])
         traffic_src = str(tf.relative_to(ROOT))
+    # MFMA-busy share and clock of the GEMM launches, from the committed counter runs
+    counters = None
+    cf = ROOT / "profiles" / f"gemm_counters_{cfg.name}.json"
+    if cf.exists() and stack.chunk == cfg.chunk and not args.unfused:
+        kinds = json.loads(cf.read_text())["kinds"]
+        wt = sum(k["us"] * k["launches"] for k in kinds.values())
+        counters = {"source": str(cf.relative_to(ROOT)),
+                    "mfma_busy_pct": round(sum(k["mfma_busy_pct"] * k["us"] * k["launches"] for k in kinds.values()) / wt, 1),
+                    "clock_ghz": round(sum(k["clock_ghz"] * k["us"] * k["launches"] for k in kinds.values()) / wt, 3),
+                    "per_kind_frac": {n: k["frac_of_peak"] for n, k in kinds.items()}}
     convert = [convert_bandwidth(z, cfg.ffn_type, cfg.ffn, cfg.hidden),
                convert_bandwidth(z, cfg.down_type, cfg.hidden, cfg.ffn)]
     line = {
@@ -373,7 +476,8 @@ def main() -> int:
                      "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK, 4), "traffic": traffic,
                      "traffic_source": traffic_src,
                      "launches": launches, "avg_launch_us": round(gemm_ms * 1e3 / launches, 2),
-                     "timed": "the step's GEMM launches back to back between two HIP events"},
+                     "timed": "the step's GEMM launches back to back between two HIP events",
+                     "counters": counters},
         "convert": convert,
         "pack": pack,
     }
