@@ -103,48 +103,6 @@ def orc_p():
     return ctypes.c_void_p
 
 
-def pack_bandwidth(z, m: int, k: int, reps: int = 20) -> list:
-    """The activation pack, as bfp16 bytes (4 + 1.125 B/value) and as the
-    GEMM's expanded operand (4 + 2 B/value, the form the stack uses)."""
-    import torch
-    x = torch.randn((m, k), device="cuda")
-    res = []
-    for name, fn, out, per in (("bfp16", z.pack_act, z.empty_packed(m, k), 5.125),
-                               ("expanded", z.pack_act_x, z.empty_act(m, k), 6.0)):
-        fn(x, out=out)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            fn(x, out=out)
-        e1.record()
-        e1.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / reps
-        gbs = per * m * k / (us * 1e-6) / 1e9
-        res.append({"output": name, "shape": [m, k], "us": round(us, 2), "GB/s": round(gbs, 1),
-                    "frac": round(gbs / HBM_PEAK, 3)})
-    return res
-
-
-def convert_bandwidth(z, wtype: int, n: int, k: int, reps: int = 10) -> dict:
-    """One-time weight conversion of one [n][k] GGUF weight, repeated."""
-    import torch
-    from ggml_xdna_amd import quant
-    raw = quant.quantize(wtype, torch.randn((n, k), device="cuda") * 0.02)
-    out = z.empty_packed(n, k)
-    z.convert_weight(wtype, raw, n, k, out=out)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        z.convert_weight(wtype, raw, n, k, out=out)
-    e1.record()
-    e1.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / reps
-    nbytes = raw.numel() + n * k * 9 / 8
-    gbs = nbytes / (us * 1e-6) / 1e9
-    return {"type": {8: "Q8_0", 12: "Q4_K"}[wtype], "shape": [n, k], "us": round(us, 2), "GB/s": round(gbs, 1),
-            "frac": round(gbs / HBM_PEAK, 3)}
-
-
 # GGUF block types: (values per block, bytes per block, byte ranges of the
 # block's fp16 scale fields)
 GGUF_BLOCKS = {"F16": (1, 1, 2, []), "BF16": (30, 1, 2, []), "Q4_0": (2, 32, 18, [(0, 2)]),
@@ -170,45 +128,116 @@ def random_gguf(name: str, n: int, k: int, seed: int):
     return raw.view(n, -1)
 
 
+# The HBM-rate measurements: every launch takes the next of several input and
+# output sets, at least 4 and enough that their footprint is three times the
+# 256 MB MALL, so each launch reads its input from HBM rather than from the
+# cache the previous launch filled.
+HBM_REPS = 5
+HBM_W = (17408, 5120)  # converter: one weight of the 27B-class FFN
+HBM_X = (8192, 5120)   # pack and RMSNorm: 8192 activation rows of 5120
+
+
+def _sets(set_bytes: float) -> int:
+    return max(4, int(768e6 // set_bytes) + 1)
+
+
+def _timed(fn, count: int) -> float:
+    """Average microseconds per call over `count` calls after one warm call,
+    between HIP events on the current stream."""
+    import torch
+    fn(0)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(count):
+        fn(i)
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / count
+
+
+def _rate(kernel: str, nbytes: float, us: float, **kw) -> dict:
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"kernel": kernel, **kw, "bytes": int(nbytes), "us": round(us, 2), "GB/s": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK, 3)}
+
+
+def convert_rate(z, name: str, n: int = HBM_W[0], k: int = HBM_W[1]) -> dict:
+    """One-time weight conversion of an [n][k] GGUF weight of type `name`:
+    GGUF bytes read + 1.125 B/value written."""
+    wtype, blk, bb, _ = GGUF_BLOCKS[name]
+    nbytes = n * (k // blk) * bb + n * k * 9 / 8
+    sets = _sets(nbytes)
+    raws = [random_gguf(name, n, k, s) for s in range(sets)]
+    outs = [z.empty_packed(n, k) for _ in range(sets)]
+    us = _timed(lambda i: z.convert_weight(wtype, raws[i % sets], n, k, out=outs[i % sets]), sets * HBM_REPS)
+    return _rate("convert", nbytes, us, type=name, shape=[n, k])
+
+
+def pack_rates(z, m: int = HBM_X[0], k: int = HBM_X[1], bfp16: bool = True) -> list:
+    """The activation pack, to bfp16 bytes (4 + 1.125 B/value) and to the
+    GEMM's expanded operand (4 + 2 B/value, the form the stack uses)."""
+    import torch
+    sets = _sets(6.0 * m * k)
+    xs = [torch.randn((m, k), device="cuda") for _ in range(sets)]
+    res = []
+    for label, fn, mk, per in (("pack", z.pack_act, z.empty_packed, 5.125), ("pack_x", z.pack_act_x, z.empty_act, 6.0)):
+        if label == "pack" and not bfp16:
+            continue
+        outs = [mk(m, k) for _ in range(sets)]
+        us = _timed(lambda i: fn(xs[i % sets], out=outs[i % sets]), sets * HBM_REPS)
+        res.append(_rate(label, per * m * k, us, shape=[m, k]))
+        del outs
+    return res
+
+
+def norm_rate(z, m: int = HBM_X[0], d: int = HBM_X[1]) -> dict:
+    """RMSNorm with its scale row, writing only the next matmul's expanded
+    operand (the stack's form): 4 + 2 B/value."""
+    import torch
+    sets = _sets(6.0 * m * d)
+    xs = [torch.randn((m, d), device="cuda") for _ in range(sets)]
+    w = torch.randn(d, device="cuda")
+    outs = [z.empty_act(m, d) for _ in range(sets)]
+    us = _timed(lambda i: z.rms_norm(xs[i % sets], 1e-6, w, y=None, packed=outs[i % sets]), sets * HBM_REPS)
+    return _rate("rms_norm+pack_x", 6.0 * m * d, us, shape=[m, d])
+
+
+def copy_rate(nbytes: float) -> dict:
+    """The ceiling the HBM-bound kernels are held against: torch's device
+    copy of a float32 tensor, `nbytes` moved in all (half read, half
+    written), on rotating sets as above."""
+    import torch
+    n = int(nbytes / 8)
+    sets = _sets(nbytes)
+    xs = [torch.randn(n, device="cuda") for _ in range(sets)]
+    ys = [torch.empty_like(xs[0]) for _ in range(sets)]
+    us = _timed(lambda i: ys[i % sets].copy_(xs[i % sets]), sets * HBM_REPS)
+    return _rate("copy", 8.0 * n, us, floats=n)
+
+
 def hbm_kernels(args) -> int:
-    """HBM rates of the converter (every GGUF type) and the activation pack,
-    on shapes whose footprint (four rotating sets) exceeds the 256 MB
-    Infinity Cache. One JSON line per kernel."""
+    """HBM rates of the converter (every GGUF type), the activation pack and
+    the fused RMSNorm+pack, on rotating sets, at the large shapes and at the
+    qwen3-4b stack's own, beside a plain copy of the same bytes. One JSON
+    line per kernel."""
     import torch
     z = load_pkg()
     torch.cuda.set_device(0)
     z.init(0)
-    n, k, sets, reps = 17408, 5120, 4, 5
-
-    def timed(fn, count):
-        fn(0)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for i in range(count):
-            fn(i)
-        e1.record()
-        e1.synchronize()
-        return e0.elapsed_time(e1) * 1e3 / count
-
-    for name, (wtype, blk, bb, _) in GGUF_BLOCKS.items():
-        raws = [random_gguf(name, n, k, s) for s in range(sets)]
-        outs = [z.empty_packed(n, k) for _ in range(sets)]
-        us = timed(lambda i: z.convert_weight(wtype, raws[i % sets], n, k, out=outs[i % sets]), sets * reps)
-        nbytes = raws[0].numel() + n * k * 9 / 8
-        gbs = nbytes / (us * 1e-6) / 1e9
-        print(json.dumps({"kernel": "convert", "type": name, "shape": [n, k], "bytes": int(nbytes), "us": round(us, 2),
-                          "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK, 3)}), flush=True)
-        del raws, outs
-    m, kk = 8192, 5120
-    xs = [torch.randn((m, kk), device="cuda") for _ in range(sets)]
-    for label, fn, mk, per in (("pack", z.pack_act, z.empty_packed, 5.125), ("pack_x", z.pack_act_x, z.empty_act, 6.0)):
-        outs = [mk(m, kk) for _ in range(sets)]
-        us = timed(lambda i: fn(xs[i % sets], out=outs[i % sets]), sets * reps)
-        gbs = per * m * kk / (us * 1e-6) / 1e9
-        print(json.dumps({"kernel": label, "shape": [m, kk], "bytes": int(per * m * kk), "us": round(us, 2),
-                          "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK, 3)}), flush=True)
-        del outs
+    for name in GGUF_BLOCKS:
+        print(json.dumps(convert_rate(z, name)), flush=True)
+    for r in pack_rates(z):
+        print(json.dumps(r), flush=True)
+    print(json.dumps(norm_rate(z)), flush=True)
+    # the stack's own sizes: qwen3-4b's attention output (2048 x 4096) and hidden rows (2048 x 2560)
+    for r in pack_rates(z, 2048, 4096, bfp16=False):
+        print(json.dumps(r), flush=True)
+    print(json.dumps(norm_rate(z, 2048, 2560)), flush=True)
+    # a plain copy moving the same bytes as each of the above
+    for nbytes in (6.0 * 2048 * 2560, 6.0 * 2048 * 4096, 6.0 * HBM_X[0] * HBM_X[1],
+                   HBM_W[0] * HBM_W[1] * (34 / 32 + 9 / 8)):
+        print(json.dumps(copy_rate(nbytes)), flush=True)
     return 0
 
 
@@ -431,7 +460,6 @@ def main() -> int:
     print(f"[bench] {args.steps} steps: {ms_step:.2f} ms/step; the GEMMs alone {gemm_ms / args.steps:.2f} ms/step over "
           f"{launches // args.steps} launches", file=sys.stderr, flush=True)
 
-    pack = pack_bandwidth(z, stack.chunk, cfg.q)
     # HBM bytes per GEMM launch, from the committed counter runs of this workload
     traffic, traffic_src = None, None
     tf = ROOT / "profiles" / f"gemm_traffic_{cfg.name}.json"
@@ -448,8 +476,10 @@ def main() -> int:
                     "mfma_busy_pct": round(sum(k["mfma_busy_pct"] * k["us"] * k["launches"] for k in kinds.values()) / wt, 1),
                     "clock_ghz": round(sum(k["clock_ghz"] * k["us"] * k["launches"] for k in kinds.values()) / wt, 3),
                     "per_kind_frac": {n: k["frac_of_peak"] for n, k in kinds.items()}}
-    convert = [convert_bandwidth(z, cfg.ffn_type, cfg.ffn, cfg.hidden),
-               convert_bandwidth(z, cfg.down_type, cfg.hidden, cfg.ffn)]
+    # the HBM-bound kernels on rotating sets, as `--hbm` measures them
+    names = {v[0]: k for k, v in GGUF_BLOCKS.items()}
+    convert = [convert_rate(z, names[t]) for t in dict.fromkeys((cfg.ffn_type, cfg.down_type))]
+    pack = pack_rates(z) + [norm_rate(z)]
     line = {
         "metric": METRIC,
         "value": round(value, 2),

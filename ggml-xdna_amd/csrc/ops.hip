@@ -158,6 +158,14 @@ __global__ __launch_bounds__(NORM_ROWS * 64) void rms_norm_kernel(const float * 
 // loaded at once; the sum of squares is a wave reduction and then a sum of
 // the four waves' partials through LDS. Four times the waves of
 // rms_norm_kernel for the same rows, so more loads are in flight.
+//
+// Row order: workgroups are dealt to the eight XCDs in turn (workgroup b to
+// XCD b % 8), and a row writes only 32 bytes of each 128-byte line of the
+// expanded operand (the other 96 are rows r^1..r^3 of its 4-row quartet).
+// With a grid of 8k workgroups, workgroup b takes row (b % 8) * k + b / 8,
+// so each XCD owns a contiguous run of k rows, every line is completed
+// inside one XCD's L2, and no line leaves an L2 partly written
+// (2048 x 2560 with the pack: 9.5 -> 7.3 us).
 template <int NCH>
 __global__ __launch_bounds__(256) void rms_norm_row_kernel(const float * __restrict__ x, int64_t rows, int64_t d,
                                                            float eps, const float * __restrict__ w,
@@ -165,7 +173,8 @@ __global__ __launch_bounds__(256) void rms_norm_row_kernel(const float * __restr
                                                            int64_t R_pad) {
     __shared__ float part[4];
     const int t = threadIdx.x, lane = t & 63;
-    const int64_t r = blockIdx.x;
+    const int64_t G = gridDim.x, b = blockIdx.x;
+    const int64_t r = G % 8 == 0 ? (b % 8) * (G / 8) + b / 8 : b;
     const int64_t d_pad = zest_k_padded(d);
     if (r >= rows) {  // a padding row of the packed operand (the whole workgroup takes this branch)
         for (int64_t c = t * 4; c < d_pad; c += 1024)
