@@ -15,6 +15,7 @@
 #include <atomic>
 #include <chrono>
 #include <cmath>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -149,6 +150,8 @@ int64_t nan_after() {
 }
 std::atomic<int64_t> g_submissions{0};
 
+struct piece_plan;
+
 struct context {
     hipStream_t stream = nullptr;  // compute
     hipStream_t loader = nullptr;  // weight conversion at load
@@ -172,6 +175,12 @@ struct context {
     // trace
     double compute_ms = 0;
     int64_t matmuls = 0, pieces = 0;
+
+    // the plans of the graphs computed lately, by graph (reused while the
+    // graph is unchanged; at most PLAN_CACHE of them)
+    static constexpr size_t PLAN_CACHE = 256;
+    std::unordered_map<const ggml_cgraph *, std::shared_ptr<const piece_plan>> plans;
+    std::shared_ptr<const piece_plan> plan_for(const ggml_cgraph * g);
 
     context();
     ~context();
@@ -406,6 +415,30 @@ bool gemm_matmul(const ggml_tensor * n) {
            is_contiguous(n->src[1]) && n->src[0]->ne[0] % 8 == 0;
 }
 
+// Readers of each tensor among a piece's nodes, owner(src) -> (node, source
+// slot), built once per piece so that each reader question is one lookup
+// rather than a pass over every node (a prompt graph of a whole model has
+// hundreds of nodes, and the questions are asked per node).
+using reader_list = std::vector<std::pair<const ggml_tensor *, int>>;
+using reader_map = std::unordered_map<const ggml_tensor *, reader_list>;
+
+reader_map index_readers(const std::vector<ggml_tensor *> & nodes) {
+    reader_map r;
+    for (const ggml_tensor * n : nodes)
+        for (int j = 0; j < GGML_MAX_SRC; j++)
+            if (n->src[j]) r[owner(n->src[j])].emplace_back(n, j);
+    return r;
+}
+
+// whether a node of the piece other than `except` reads t
+bool read_by_other(const reader_map & r, const ggml_tensor * t, const ggml_tensor * except) {
+    const auto it = r.find(t);
+    if (it == r.end()) return false;
+    for (const auto & e : it->second)
+        if (e.first != except) return true;
+    return false;
+}
+
 // The fusions of a piece (src/xdna-exec.cpp:399-431): a GLU whose gate and up
 // are matmuls of the piece on the same input, with weights of one type and
 // shape, read by nothing but the GLU, inside the piece or out; or a GLU over
@@ -413,7 +446,7 @@ bool gemm_matmul(const ggml_tensor * n) {
 // interleave). The reference fuses SwiGLU only; every GLU kind is fused here,
 // the epilogue computing the same GLU the GLU kernel does.
 std::vector<fusion> find_fusions(const std::vector<ggml_tensor *> & nodes,
-                                 const std::unordered_set<const ggml_tensor *> & in_piece) {
+                                 const std::unordered_set<const ggml_tensor *> & in_piece, const reader_map & rd) {
     std::vector<fusion> out;
     for (ggml_tensor * n : nodes) {
         if (n->op != GGML_OP_GLU || glu_kind_of(param_i32(n, 0)) < 0 || !is_contiguous(n)) continue;
@@ -435,11 +468,8 @@ std::vector<fusion> find_fusions(const std::vector<ggml_tensor *> & nodes,
             f.swapped = param_i32(n, 1) != 0;
         }
         if (f.F % 32 || n->ne[0] != f.F || nrows(n) != gm->src[1]->ne[1]) continue;
-        bool other = false;  // another reader of the gate's or up's result
-        for (const ggml_tensor * m : nodes)
-            for (int j = 0; j < GGML_MAX_SRC && m != n; j++)
-                if (m->src[j] && (owner(m->src[j]) == gm || (um && owner(m->src[j]) == um))) other = true;
-        if (!other) out.push_back(f);
+        // another reader of the gate's or up's result
+        if (!read_by_other(rd, gm, n) && !(um && read_by_other(rd, um, n))) out.push_back(f);
     }
     return out;
 }
@@ -450,7 +480,7 @@ std::vector<fusion> find_fusions(const std::vector<ggml_tensor *> & nodes,
 // Returns ADD -> its matmul.
 std::unordered_map<const ggml_tensor *, const ggml_tensor *> find_residuals(
     const std::vector<ggml_tensor *> & nodes, const std::unordered_set<const ggml_tensor *> & in_piece,
-    const std::unordered_set<const ggml_tensor *> & fused) {
+    const std::unordered_set<const ggml_tensor *> & fused, const reader_map & rd) {
     std::unordered_map<const ggml_tensor *, const ggml_tensor *> out;
     for (ggml_tensor * a : nodes) {
         if (a->op != GGML_OP_ADD || !is_contiguous(a) || a->type != GGML_TYPE_F32) continue;
@@ -460,11 +490,7 @@ std::unordered_map<const ggml_tensor *, const ggml_tensor *> find_residuals(
                 !same_shape(a, n) || !same_shape(a, r) || r->type != GGML_TYPE_F32 || r->nb[0] != 4 ||
                 r->nb[1] % 16 != 0 || nrows(a) != a->ne[1])
                 continue;
-            bool other = false;  // another reader of the matmul's result
-            for (const ggml_tensor * m : nodes)
-                for (int j = 0; j < GGML_MAX_SRC && m != a; j++)
-                    if (m->src[j] && owner(m->src[j]) == n) other = true;
-            if (other) continue;
+            if (read_by_other(rd, n, a)) continue;  // another reader of the matmul's result
             out[a] = n;
             break;
         }
@@ -472,11 +498,97 @@ std::unordered_map<const ggml_tensor *, const ggml_tensor *> find_residuals(
     return out;
 }
 
+// What graph_compute works out about a piece before launching anything: its
+// nodes, their readers, the gate/up fusions and the residual adds. It depends
+// only on the graph's structure (ops, sources, shapes, strides, data
+// addresses, flags, op parameters) and on the readers recorded by
+// supports_op, so a graph computed again unchanged (llama.cpp reuses its
+// prompt graph from one batch to the next) reuses it.
+struct piece_plan {
+    std::vector<ggml_tensor *> nodes;
+    std::unordered_set<const ggml_tensor *> in_piece;
+    reader_map readers;                                     // owner -> its readers in the piece
+    std::unordered_set<const ggml_tensor *> matmul_inputs;  // packed_key of every MUL_MAT's input
+    std::vector<fusion> fusions;
+    std::unordered_map<const ggml_tensor *, const fusion *> fused_mm;      // gate/up matmul -> its fusion
+    std::unordered_map<const ggml_tensor *, const fusion *> fused_glu;     // GLU -> its fusion
+    std::unordered_map<const ggml_tensor *, const ggml_tensor *> res_add;  // ADD -> its matmul
+    std::unordered_set<const ggml_tensor *> res_mm;                        // matmuls run by their ADD
+    uint64_t key = 0, epoch = 0;  // graph_key and readers_epoch it was made at
+
+    explicit piece_plan(const ggml_cgraph * g) {
+        for (int i = 0; i < g->n_nodes; i++) {
+            nodes.push_back(g->nodes[i]);
+            in_piece.insert(g->nodes[i]);
+            if (g->nodes[i]->op == GGML_OP_MUL_MAT) matmul_inputs.insert(packed_key(g->nodes[i]->src[1]));
+        }
+        readers = index_readers(nodes);
+        fusions = find_fusions(nodes, in_piece, readers);
+        std::unordered_set<const ggml_tensor *> fused;
+        for (const fusion & f : fusions) {
+            fused_mm[f.gate_mm] = &f;
+            if (f.up_mm) fused_mm[f.up_mm] = &f;
+            fused_glu[f.glu] = &f;
+            fused.insert(f.gate_mm);
+            if (f.up_mm) fused.insert(f.up_mm);
+        }
+        res_add = find_residuals(nodes, in_piece, fused, readers);
+        for (const auto & kv : res_add) res_mm.insert(kv.second);
+    }
+};
+
+// A 64-bit digest of everything a piece_plan reads from a graph.
+uint64_t graph_key(const ggml_cgraph * g) {
+    uint64_t h = 0x9E3779B97F4A7C15ull ^ (uint64_t) g->n_nodes;
+    auto mix = [&h](uint64_t v) {
+        h ^= v + 0x9E3779B97F4A7C15ull + (h << 6) + (h >> 2);
+        h *= 0xBF58476D1CE4E5B9ull;
+    };
+    auto tensor = [&mix](const ggml_tensor * t) {
+        mix((uint64_t) (uintptr_t) t);
+        mix(((uint64_t) t->op << 32) | ((uint64_t) t->type << 8) | (uint64_t) (uint32_t) t->flags);
+        for (int d = 0; d < GGML_MAX_DIMS; d++) {
+            mix((uint64_t) t->ne[d]);
+            mix((uint64_t) t->nb[d]);
+        }
+        mix((uint64_t) (uintptr_t) t->data);
+        mix((uint64_t) (uintptr_t) t->view_src);
+        mix((uint64_t) (uintptr_t) t->buffer);
+        mix(t->buffer ? (uint64_t) t->buffer->usage : 0);
+    };
+    for (int i = 0; i < g->n_nodes; i++) {
+        const ggml_tensor * n = g->nodes[i];
+        tensor(n);
+        for (int j = 0; j < GGML_MAX_OP_PARAMS / 4; j += 2)
+            mix(((uint64_t) (uint32_t) n->op_params[j] << 32) | (uint32_t) n->op_params[j + 1]);
+        for (int j = 0; j < GGML_MAX_SRC; j++)
+            if (n->src[j]) tensor(n->src[j]);
+            else mix(j);
+    }
+    return h;
+}
+
+std::shared_ptr<const piece_plan> context::plan_for(const ggml_cgraph * g) {
+    const uint64_t key = graph_key(g), epoch = readers_epoch();
+    auto it = plans.find(g);
+    if (it != plans.end() && it->second->key == key && it->second->epoch == epoch &&
+        it->second->nodes.size() == (size_t) g->n_nodes &&
+        std::equal(it->second->nodes.begin(), it->second->nodes.end(), g->nodes))
+        return it->second;
+    auto pl = std::make_shared<piece_plan>(g);
+    pl->key = key;
+    pl->epoch = epoch;
+    if (plans.size() >= PLAN_CACHE) plans.clear();
+    plans[g] = pl;
+    return pl;
+}
+
 struct piece {
     context & ctx;
     const ggml_cgraph * g;
-    std::vector<ggml_tensor *> nodes;
-    std::unordered_set<const ggml_tensor *> in_piece;
+    std::shared_ptr<const piece_plan> plan;
+    const std::vector<ggml_tensor *> & nodes;
+    const std::unordered_set<const ggml_tensor *> & in_piece;
     std::unordered_map<const ggml_tensor *, void *> staged;   // host inputs copied up
     std::unordered_map<const ggml_tensor *, void *> packed;   // owner -> packed bfp16 activations
     struct pending_out {
@@ -486,31 +598,19 @@ struct piece {
     std::vector<pending_out> host_outs;  // results of nodes whose memory is on the host
     std::string err;
 
-    std::vector<fusion> fusions;
+    const std::unordered_map<const ggml_tensor *, const fusion *> & fused_mm;
+    const std::unordered_map<const ggml_tensor *, const fusion *> & fused_glu;
+    const std::unordered_map<const ggml_tensor *, const ggml_tensor *> & res_add;
+    const std::unordered_set<const ggml_tensor *> & res_mm;
+    const reader_map & readers;
+    const std::unordered_set<const ggml_tensor *> & matmul_inputs;
     int launches = 0, fused_launches = 0, grouped_launches = 0;  // GEMM launches of the piece
-    std::unordered_map<const ggml_tensor *, const fusion *> fused_mm;   // gate/up matmul -> its fusion
-    std::unordered_map<const ggml_tensor *, const fusion *> fused_glu;  // GLU -> its fusion
-    std::unordered_map<const ggml_tensor *, const ggml_tensor *> res_add;  // ADD -> its matmul
-    std::unordered_set<const ggml_tensor *> res_mm;                       // matmuls run by their ADD
     int residual_launches = 0;
 
-    piece(context & c, const ggml_cgraph * graph) : ctx(c), g(graph) {
-        for (int i = 0; i < g->n_nodes; i++) {
-            nodes.push_back(g->nodes[i]);
-            in_piece.insert(g->nodes[i]);
-        }
-        fusions = find_fusions(nodes, in_piece);
-        std::unordered_set<const ggml_tensor *> fused;
-        for (const fusion & f : fusions) {
-            fused_mm[f.gate_mm] = &f;
-            if (f.up_mm) fused_mm[f.up_mm] = &f;
-            fused_glu[f.glu] = &f;
-            fused.insert(f.gate_mm);
-            if (f.up_mm) fused.insert(f.up_mm);
-        }
-        res_add = find_residuals(nodes, in_piece, fused);
-        for (const auto & kv : res_add) res_mm.insert(kv.second);
-    }
+    piece(context & c, const ggml_cgraph * graph, std::shared_ptr<const piece_plan> pl)
+        : ctx(c), g(graph), plan(std::move(pl)), nodes(plan->nodes), in_piece(plan->in_piece),
+          fused_mm(plan->fused_mm), fused_glu(plan->fused_glu), res_add(plan->res_add), res_mm(plan->res_mm),
+          readers(plan->readers), matmul_inputs(plan->matmul_inputs) {}
 
     bool fail(const std::string & e) {
         err = e;
@@ -540,32 +640,24 @@ struct piece {
     }
 
     // whether some MUL_MAT of this piece reads t's rows as its input
-    bool feeds_matmul(const ggml_tensor * t) const {
-        for (const ggml_tensor * n : nodes)
-            if (n->op == GGML_OP_MUL_MAT && packed_key(n->src[1]) == t) return true;
-        return false;
-    }
+    bool feeds_matmul(const ggml_tensor * t) const { return matmul_inputs.count(t) != 0; }
     // the only reader of t, inside the piece and out, is `only`
     bool only_reader(const ggml_tensor * t, const ggml_tensor * only) const {
-        for (const ggml_tensor * n : nodes)
-            for (int j = 0; j < GGML_MAX_SRC; j++)
-                if (n != only && n->src[j] && owner(n->src[j]) == t) return false;
-        return !read_outside(t, in_piece);
+        return !read_by_other(readers, t, only) && !read_outside(t, in_piece);
     }
     // Every reader of t is a matmul of this piece taking t's rows as its
     // input (views in between are free): its packed copy then serves them
     // all and its fp32 values need not be written (src/ggml-zest.cpp:1100-1109).
     bool only_matmuls_read(const ggml_tensor * t) const {
         bool any = false;
-        for (const ggml_tensor * n : nodes) {
-            if (is_noop(n)) continue;
-            for (int j = 0; j < GGML_MAX_SRC; j++) {
-                const ggml_tensor * s = n->src[j];
-                if (!s || owner(s) != t) continue;
-                if (n->op != GGML_OP_MUL_MAT || j != 1 || packed_key(s) != t) return false;
+        const auto it = readers.find(t);
+        if (it != readers.end())
+            for (const auto & e : it->second) {
+                const ggml_tensor * n = e.first;
+                if (is_noop(n)) continue;
+                if (n->op != GGML_OP_MUL_MAT || e.second != 1 || packed_key(n->src[1]) != t) return false;
                 any = true;
             }
-        }
         return any && !read_outside(t, in_piece);
     }
     // packed bfp16 space for a matmul input produced in this piece
@@ -864,12 +956,19 @@ ggml_status graph_compute(ggml_backend_t backend, ggml_cgraph * cgraph) {
         log(LOG_ERROR, "graph_compute after the GPU path failed\n");
         return GGML_STATUS_FAILED;
     }
-    const auto t0 = std::chrono::steady_clock::now();
+    using clock = std::chrono::steady_clock;
+    const auto ms = [](clock::time_point a, clock::time_point b) {
+        return std::chrono::duration<double, std::milli>(b - a).count();
+    };
+    const auto t0 = clock::now();
     ctx.ws_reset();
     (void) hipMemsetAsync(ctx.nonfinite, 0, sizeof(uint32_t), ctx.stream);
-    piece p(ctx, cgraph);
-    bool ok = p.run();
+    piece p(ctx, cgraph, ctx.plan_for(cgraph));  // the piece's fusions, residual adds and readers
+    const auto t1 = clock::now();
+    bool ok = p.run();     // its launches
+    const auto t2 = clock::now();
     const hipError_t se = hipStreamSynchronize(ctx.stream);
+    const auto t3 = clock::now();
     if (ok && se != hipSuccess) ok = p.fail(std::string("the GPU reported ") + hipGetErrorString(se));
     if (ok) {
         uint32_t nf = 0;
@@ -880,8 +979,11 @@ ggml_status graph_compute(ggml_backend_t backend, ggml_cgraph * cgraph) {
     ctx.pieces++;
     static const int64_t trace_level = env_int("GGML_XDNA_TRACE", 0);
     if (trace_level >= 2)
-        fprintf(stderr, "xdna piece: %d GEMM launches (%d fused gate/up, %d grouped, %d with a residual add)\n",
-                p.launches, p.fused_launches, p.grouped_launches, p.residual_launches);
+        fprintf(stderr,
+                "xdna piece: %d nodes, %d GEMM launches (%d fused gate/up, %d grouped, %d with a residual add); "
+                "host ms: plan %.3f, launch %.3f, wait %.3f\n",
+                (int) p.nodes.size(), p.launches, p.fused_launches, p.grouped_launches, p.residual_launches,
+                ms(t0, t1), ms(t1, t2), ms(t2, t3));
     if (trace() && ctx.matmuls >= 196) {
         fprintf(stderr, "xdna times, %lld matmuls in %lld pieces: all %.1f ms; weight copies %lld at load, %lld in pieces\n",
                 (long long) ctx.matmuls, (long long) ctx.pieces, ctx.compute_ms, (long long) ctx.built_at_load,
@@ -910,7 +1012,7 @@ void graph_optimize(ggml_backend_t backend, ggml_cgraph * cgraph, ggml_backend_g
     const std::unordered_set<const ggml_tensor *> in_piece(nodes.begin(), nodes.end());
     std::unordered_set<const ggml_tensor *> fused;
     std::string err;
-    for (const fusion & f : find_fusions(nodes, in_piece)) {
+    for (const fusion & f : find_fusions(nodes, in_piece, index_readers(nodes))) {
         const ggml_tensor * gw = f.gate_mm->src[0], * uw = f.up_mm ? f.up_mm->src[0] : nullptr;
         if (!gw->data || !in_weight_buffer(gw) || (uw && (!uw->data || !in_weight_buffer(uw)))) continue;
         if (!ctx.ensure_fused(f, ctx.loader, true, err)) {

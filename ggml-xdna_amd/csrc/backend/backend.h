@@ -43,6 +43,8 @@ const ggml_tensor * exec_param(const ggml_tensor * op);
 // when a reader outside it exists, it is a graph output, or it was never seen.
 void note_readers(const ggml_tensor * op);
 bool read_outside(const ggml_tensor * t, const std::unordered_set<const ggml_tensor *> & in_piece);
+// Changes whenever a new reader is recorded (what read_outside answers may change with it).
+uint64_t readers_epoch();
 
 // The HBM budget for weight-cache entries (src/ggml-zest.cpp:429-564).
 double copy_bytes(int64_t K, int64_t N);

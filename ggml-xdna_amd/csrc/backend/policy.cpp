@@ -168,15 +168,20 @@ bool exec_supports(const ggml_tensor * op) {
 
 static std::mutex g_read_mu;
 static std::unordered_map<const ggml_tensor *, std::unordered_set<const ggml_tensor *>> g_readers;
+static std::atomic<uint64_t> g_read_epoch{0};  // counts the readers recorded
 
 void note_readers(const ggml_tensor * op) {
     std::lock_guard<std::mutex> lk(g_read_mu);
+    bool added = false;
     for (int j = 0; j < GGML_MAX_SRC; j++)
         if (const ggml_tensor * s = op->src[j]) {
-            g_readers[s].insert(op);
-            for (const ggml_tensor * v = s->view_src; v; v = v->view_src) g_readers[v].insert(op);
+            added |= g_readers[s].insert(op).second;
+            for (const ggml_tensor * v = s->view_src; v; v = v->view_src) added |= g_readers[v].insert(op).second;
         }
+    if (added) g_read_epoch.fetch_add(1, std::memory_order_relaxed);
 }
+
+uint64_t readers_epoch() { return g_read_epoch.load(std::memory_order_relaxed); }
 
 bool read_outside(const ggml_tensor * t, const std::unordered_set<const ggml_tensor *> & in_piece) {
     static const bool all = env_int("GGML_XDNA_WRITE_ALL", 0) != 0;
