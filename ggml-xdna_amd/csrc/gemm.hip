@@ -56,10 +56,10 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // BM x BN tile; CWM consumer waves, each a WM x BN block of 32x32 MFMA tiles
 // (TI x TJ of them); NP/64 producer waves (as many by default). LDS holds the expanded W ring;
 // after the K loop each consumer wave uses WM x BN floats of it for its
-// epilogue.
-template <int BM_, int BN_, int CWM_, int NP_ = 64 * CWM_>
+// epilogue. MINB workgroups a CU at least (the launch bound).
+template <int BM_, int BN_, int CWM_, int NP_ = 64 * CWM_, int MINB_ = 1>
 struct gemm_cfg {
-    static constexpr int BM = BM_, BN = BN_, CWM = CWM_, CWN = 1;
+    static constexpr int BM = BM_, BN = BN_, CWM = CWM_, CWN = 1, MINB = MINB_;
     static constexpr int NC = 64 * CWM;  // consumer threads
     static constexpr int NP = NP_;       // producer threads
     static constexpr int NT = NC + NP;
@@ -697,7 +697,7 @@ __device__ inline void run_tile(const gemm_params & p, uint8_t * smem, const gem
 // >= 0 the fused GLU of that kind.
 // SPLIT: split-K (p.splits > 1), else one whole tile per workgroup.
 template <class C, int EPI, bool SPLIT>
-__global__ __launch_bounds__(C::NT, 1) void gemm_kernel(const gemm_params p) {
+__global__ __launch_bounds__(C::NT, C::MINB) void gemm_kernel(const gemm_params p) {
     extern __shared__ uint4 smem_u4[];
     uint8_t * smem = reinterpret_cast<uint8_t *>(smem_u4);
     const int v = xcd_order((int) blockIdx.x, (int) gridDim.x), nk = p.nk;
@@ -747,8 +747,11 @@ __global__ __launch_bounds__(CB::NT, 1) void gemm_kernel_mixed(const gemm_params
 // steps per round to fill the pipeline. S K-splits take ceil(T*S/P) rounds of
 // nk/S steps, plus the fixup: every split writes its fp32 tile and the last
 // reads all S back through HBM, 2*T*S*BM*BN*4 bytes at about FIX_BW bytes
-// per step. A 128x128 step costs SMALL_STEP of a 256x128 one (half the MFMA
-// work, not half the waiting). The cheapest plan wins.
+// per step, and FIX_LAT steps more: the fixup's round trips (store and
+// acknowledge, count in, read back) that follow the K loop of every split
+// launch, however little data they move. A 128x128 step costs SMALL_STEP of
+// a 256x128 one (half the MFMA work, not half the waiting). The cheapest plan
+// wins.
 #ifndef ZEST_GEMM_MAX_SPLIT
 #define ZEST_GEMM_MAX_SPLIT 16
 #endif
@@ -758,8 +761,20 @@ __global__ __launch_bounds__(CB::NT, 1) void gemm_kernel_mixed(const gemm_params
 #ifndef ZEST_GEMM_FIX_BW
 #define ZEST_GEMM_FIX_BW 4.25e6  // bytes per step: ~5 TB/s x 0.85 us
 #endif
+#ifndef ZEST_GEMM_FIX_LAT
+#define ZEST_GEMM_FIX_LAT 5.0  // ~4 us
+#endif
 #ifndef ZEST_GEMM_SMALL_STEP
 #define ZEST_GEMM_SMALL_STEP 0.8
+#endif
+// 64x64 tiles (2 consumer waves of 32x64, 2 producers; two workgroups a CU)
+// for launches too small to fill the GPU with bigger tiles: a step of one
+// costs TINY_STEP of a 256x128 one, and two run on a CU side by side.
+#ifndef ZEST_GEMM_TINY
+#define ZEST_GEMM_TINY 64, 64, 2, 128, 2
+#endif
+#ifndef ZEST_GEMM_TINY_STEP
+#define ZEST_GEMM_TINY_STEP 0.6
 #endif
 // The fused GLU's 256x128 tiles: 8 consumer waves of 32x128 and 4 producer
 // waves, two consumers on each SIMD (the GLU's long launches gain ~3% from
@@ -770,6 +785,7 @@ __global__ __launch_bounds__(CB::NT, 1) void gemm_kernel_mixed(const gemm_params
 using cfg_big = gemm_cfg<ZEST_GEMM_BIG>;
 using cfg_small = gemm_cfg<ZEST_GEMM_SMALL>;
 using cfg_glu = gemm_cfg<ZEST_GEMM_GLU>;
+using cfg_tiny = gemm_cfg<ZEST_GEMM_TINY>;
 
 // Per device and stream: the split-K workspace (grown as needed; counters
 // zeroed when allocated, and zero again after every launch).
@@ -893,7 +909,7 @@ gemm_plan plan_splits(int64_t T, int nk, int64_t P, double tile_bytes, double st
     best.cost = (double) ((T + P - 1) / P) * (nk + ZEST_GEMM_PROLOGUE) * step;
     for (int S = 2; S <= ZEST_GEMM_MAX_SPLIT && nk / S >= 4; S++) {
         const double cost = (double) ((T * S + P - 1) / P) * ((double) nk / S + ZEST_GEMM_PROLOGUE) * step +
-                            2.0 * T * S * tile_bytes / ZEST_GEMM_FIX_BW;
+                            2.0 * T * S * tile_bytes / ZEST_GEMM_FIX_BW + ZEST_GEMM_FIX_LAT;
         if (cost < best.cost) {
             best.splits = S;
             best.cost = cost;
@@ -993,6 +1009,13 @@ int launch_any(gemm_params p, const int64_t * N, hipStream_t s, const char * nam
                 ((double) R + (double) ((2 * rem + P - 1) / P) * ZEST_GEMM_SMALL_STEP) * (p.nk + ZEST_GEMM_PROLOGUE);
             if (mixed < big.cost && mixed < small.cost) return launch_mixed<EPI>(p, N, R * P, s, name);
         }
+    }
+    if constexpr (EPI < 0) {
+        // tiny tiles, cfg_tiny::MINB of them a CU
+        const gemm_plan tiny = plan_splits(tiles_of(p, N, cfg_tiny::BM, cfg_tiny::BN), p.nk, P * cfg_tiny::MINB,
+                                           (double) cfg_tiny::BM * cfg_tiny::BN * 4, ZEST_GEMM_TINY_STEP);
+        if (tiny.cost < big.cost && tiny.cost < small.cost)
+            return launch<cfg_tiny, EPI>(p, N, tiny.splits, s, name, fixed);
     }
     if (small.cost < big.cost) return launch<cfg_small, EPI>(p, N, small.splits, s, name, fixed);
     return launch<CB, EPI>(p, N, big.splits, s, name, fixed);

@@ -28,8 +28,8 @@ def k_steps(k):
     return (k + 63) // 64
 
 
-# (BM, BN, consumer waves) of cfg_big, cfg_small and cfg_glu
-CONFIGS = [(256, 128, 4), (128, 128, 4), (256, 128, 8)]
+# (BM, BN, consumer waves) of cfg_big, cfg_small, cfg_glu and cfg_tiny
+CONFIGS = [(256, 128, 4), (128, 128, 4), (256, 128, 8), (64, 64, 2)]
 
 
 def consumer_steps(ns, last):
@@ -102,6 +102,7 @@ SHAPES = [
     (1, 256, 64), (7, 200, 200), (100, 96, 8), (129, 1000, 520), (300, 200, 256), (600, 1000, 8192),
     (1024, 2560, 2560), (2048, 2560, 4096), (2048, 2560, 9728), (2048, 6144, 2560), (2048, 19456, 2560),
     (4096, 5120, 17408), (4096, 34816, 5120), (1536, 1024, 4096), (256, 4096, 1024),
+    (1024, 1024, 1024), (1024, 3072, 1024), (1024, 1024, 4096), (65, 64, 64), (64, 65, 128),
 ]
 
 
