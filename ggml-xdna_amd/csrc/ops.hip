@@ -4,6 +4,8 @@
 // bfp16 pack, stored expanded) directly, so a normalised or gated row goes
 // HBM -> registers -> matmul operand without a round trip through an fp32
 // tensor.
+#include <algorithm>
+
 #include "zest_common.h"
 #include "zest_device.h"
 
@@ -274,53 +276,84 @@ __global__ __launch_bounds__(256) void glu_kernel(const float * __restrict__ g, 
     }
 }
 
-__global__ __launch_bounds__(256) void add_kernel(const float * __restrict__ a, const float * __restrict__ b,
-                                                  int64_t n, int64_t d, int b_row, float * __restrict__ y) {
-    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    y[i] = a[i] + (b_row ? b[i % d] : b[i]);
+// Row-wise binary ops over rows x d (row-major, contiguous): y = a OP b,
+// with b either the same shape or one row broadcast to every row (b_row).
+// Thread t of column block x takes columns 4t + 1024x of rows y, y + Y, ...
+// (a 2-D grid: no division per element), four at a time with 16-byte loads
+// and stores when VEC (d % 4 == 0 and every pointer 16-byte aligned).
+template <int OP, bool VEC>  // OP 0: add, 1: mul
+__global__ __launch_bounds__(256) void binary_rows_kernel(const float * __restrict__ a, const float * __restrict__ b,
+                                                          int64_t rows, int64_t d, int b_row, float * __restrict__ y) {
+    const int64_t c = ((int64_t) blockIdx.x * 256 + threadIdx.x) * 4;
+    if (c >= d) return;
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+        const float * ar = a + r * d;
+        const float * br = b_row ? b : b + r * d;
+        float * yr = y + r * d;
+        if (VEC) {
+            const float4 u = *reinterpret_cast<const float4 *>(ar + c), v = *reinterpret_cast<const float4 *>(br + c);
+            *reinterpret_cast<float4 *>(yr + c) = OP == 0 ? make_float4(u.x + v.x, u.y + v.y, u.z + v.z, u.w + v.w)
+                                                          : make_float4(u.x * v.x, u.y * v.y, u.z * v.z, u.w * v.w);
+        } else {
+            for (int64_t i = c; i < c + 4 && i < d; i++) yr[i] = OP == 0 ? ar[i] + br[i] : ar[i] * br[i];
+        }
+    }
 }
 
-__global__ __launch_bounds__(256) void mul_row_kernel(const float * __restrict__ x, const float * __restrict__ w,
-                                                      int64_t n, int64_t d, float * __restrict__ y) {
-    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    y[i] = x[i] * w[i % d];
-}
-
+// y = x * s + b over n floats, four a thread (16-byte accesses when VEC).
+template <bool VEC>
 __global__ __launch_bounds__(256) void scale_kernel(const float * __restrict__ x, int64_t n, float s, float b,
                                                     float * __restrict__ y) {
-    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t i = ((int64_t) blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= n) return;
-    y[i] = x[i] * s + b;
+    if (VEC && i + 4 <= n) {
+        const float4 u = *reinterpret_cast<const float4 *>(x + i);
+        *reinterpret_cast<float4 *>(y + i) = make_float4(u.x * s + b, u.y * s + b, u.z * s + b, u.w * s + b);
+    } else {
+        for (int64_t k = i; k < i + 4 && k < n; k++) y[k] = x[k] * s + b;
+    }
 }
 
 // NaN or infinity anywhere in rows x cols (row stride ld) sets *flag. The test
 // is on the bits (exponent field all ones), so no fast-math can fold it away.
-__global__ __launch_bounds__(256) void check_finite_kernel(const float * __restrict__ y, int64_t cols, int64_t ld,
-                                                           int64_t n, uint32_t * flag) {
-    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const uint32_t bits = __float_as_uint(y[(i / cols) * ld + i % cols]);
-    if ((bits & 0x7f800000u) == 0x7f800000u) atomicOr(flag, 1u);
+// 2-D grid as binary_rows_kernel, four columns a thread.
+__global__ __launch_bounds__(256) void check_finite_kernel(const float * __restrict__ y, int64_t rows, int64_t cols,
+                                                           int64_t ld, uint32_t * flag) {
+    const int64_t c = ((int64_t) blockIdx.x * 256 + threadIdx.x) * 4;
+    if (c >= cols) return;
+    bool bad = false;
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y)
+        for (int64_t i = c; i < c + 4 && i < cols; i++)
+            bad |= (__float_as_uint(y[r * ld + i]) & 0x7f800000u) == 0x7f800000u;
+    if (bad) atomicOr(flag, 1u);
 }
 
-// ROPE: one workgroup per (token, head); thread p < n_dims/2 owns pair p.
-// theta for pair p is pos * theta_scale^p built by p float multiplications,
-// as the reference's table loop does (src/xdna-exec.cpp:225-233); the
-// rotation of :326-339; dimensions past n_dims copied.
+// ROPE: one workgroup per token. Thread 0 walks θ through the pairs as the
+// reference's table loop does (src/xdna-exec.cpp:225-233): θ_0 = pos, and
+// θ_{p+1} = θ_p * theta_scale, one float multiplication a pair; each thread
+// then forms the cos and sin of its pairs (rope_yarn), and the token's heads
+// are rotated from that table (the rotation of :326-339); dimensions past
+// n_dims are copied. Shared memory: n_dims/2 angles, then n_dims/2 (cos, sin).
 __global__ __launch_bounds__(256) void rope_kernel(const float * __restrict__ x, int64_t heads, int64_t d,
                                                    const int32_t * __restrict__ pos, const float * __restrict__ ff,
                                                    int n_dims, int neox, float theta_scale, float freq_scale,
                                                    float ext_factor, float attn_factor, float corr0, float corr1,
                                                    float * __restrict__ y) {
-    const int64_t t = blockIdx.x / heads, h = blockIdx.x % heads;
-    const float * src = x + (t * heads + h) * d;
-    float * dst = y + (t * heads + h) * d;
-    for (int p = threadIdx.x; p < n_dims / 2; p += blockDim.x) {
-        float theta = (float) pos[t];
-        for (int i = 0; i < p; i++) theta *= theta_scale;
-        const float theta_extrap = ff ? theta / ff[p] : theta;
+    extern __shared__ float rope_sh[];
+    const int half = n_dims / 2;
+    float * theta = rope_sh;
+    float2 * cs = reinterpret_cast<float2 *>(rope_sh + ((half + 1) & ~1));
+    const int64_t t = blockIdx.x;
+    if (threadIdx.x == 0) {
+        float th = (float) pos[t];
+        for (int p = 0; p < half; p++) {
+            theta[p] = th;
+            th *= theta_scale;
+        }
+    }
+    __syncthreads();
+    for (int p = threadIdx.x; p < half; p += blockDim.x) {
+        const float theta_extrap = ff ? theta[p] / ff[p] : theta[p];
         float th = freq_scale * theta_extrap, mscale = attn_factor;
         if (ext_factor != 0.0f) {
             const float yv = ((float) p - corr0) / fmaxf(0.001f, corr1 - corr0);
@@ -328,16 +361,46 @@ __global__ __launch_bounds__(256) void rope_kernel(const float * __restrict__ x,
             th = th * (1.0f - ramp_mix) + theta_extrap * ramp_mix;
             mscale *= 1.0f + 0.1f * logf(1.0f / freq_scale);
         }
-        const float c = cosf(th) * mscale, sn = sinf(th) * mscale;
-        const int64_t ic = neox ? p : 2 * p, off = neox ? n_dims / 2 : 1;
-        const float x0 = src[ic], x1 = src[ic + off];
-        dst[ic] = x0 * c - x1 * sn;
-        dst[ic + off] = x0 * sn + x1 * c;
+        cs[p] = make_float2(cosf(th) * mscale, sinf(th) * mscale);
     }
-    for (int64_t i = n_dims + threadIdx.x; i < d; i += blockDim.x) dst[i] = src[i];
+    __syncthreads();
+    const int64_t off = neox ? half : 1;
+    for (int64_t k = threadIdx.x; k < heads * half; k += blockDim.x) {
+        const int64_t h = k / half, p = k - h * half;
+        const float * src = x + (t * heads + h) * d;
+        float * dst = y + (t * heads + h) * d;
+        const int64_t ic = neox ? p : 2 * p;
+        const float2 r = cs[p];
+        const float x0 = src[ic], x1 = src[ic + off];
+        dst[ic] = x0 * r.x - x1 * r.y;
+        dst[ic + off] = x0 * r.y + x1 * r.x;
+    }
+    const int64_t rest = d - n_dims;
+    if (rest > 0)
+        for (int64_t k = threadIdx.x; k < heads * rest; k += blockDim.x) {
+            const int64_t h = k / rest, i = n_dims + (k - h * rest);
+            y[(t * heads + h) * d + i] = x[(t * heads + h) * d + i];
+        }
 }
 
 unsigned blocks_for(int64_t n, int per) { return (unsigned) ((n + per - 1) / per); }
+
+// rows x d as (column blocks of 1024, up to 65535 row slots)
+dim3 row_grid(int64_t rows, int64_t d) {
+    return dim3(blocks_for(d, 1024), (unsigned) std::min<int64_t>(rows, 65535));
+}
+
+bool aligned16(const void * p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+template <int OP>
+void binary_rows(const float * a, const float * b, int64_t rows, int64_t d, int b_row, float * y,
+                        hipStream_t s) {
+    if (d % 4 == 0 && aligned16(a) && aligned16(b) && aligned16(y))
+        hipLaunchKernelGGL((binary_rows_kernel<OP, true>), row_grid(rows, d), dim3(256), 0, s, a, b, rows, d, b_row, y);
+    else
+        hipLaunchKernelGGL((binary_rows_kernel<OP, false>), row_grid(rows, d), dim3(256), 0, s, a, b, rows, d, b_row, y);
+}
+
 
 } // namespace
 
@@ -391,22 +454,23 @@ int zest_glu(int kind, const float * g, int64_t sg, const float * u, int64_t su,
 
 int zest_add(const float * a, const float * b, int64_t rows, int64_t d, int b_is_row, float * y, void * stream) {
     ZEST_REQUIRE(a && b && y && rows > 0 && d > 0, "zest_add: bad arguments");
-    const int64_t n = rows * d;
-    hipLaunchKernelGGL(add_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, zest::as_stream(stream), a, b, n, d, b_is_row,
-                       y);
+    binary_rows<0>(a, b, rows, d, b_is_row != 0, y, zest::as_stream(stream));
     return zest::check_launch("zest_add");
 }
 
 int zest_mul_row(const float * x, const float * w, int64_t rows, int64_t d, float * y, void * stream) {
     ZEST_REQUIRE(x && w && y && rows > 0 && d > 0, "zest_mul_row: bad arguments");
-    const int64_t n = rows * d;
-    hipLaunchKernelGGL(mul_row_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, zest::as_stream(stream), x, w, n, d, y);
+    binary_rows<1>(x, w, rows, d, 1, y, zest::as_stream(stream));
     return zest::check_launch("zest_mul_row");
 }
 
 int zest_scale(const float * x, int64_t n, float s, float b, float * y, void * stream) {
     ZEST_REQUIRE(x && y && n > 0, "zest_scale: bad arguments");
-    hipLaunchKernelGGL(scale_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, zest::as_stream(stream), x, n, s, b, y);
+    const dim3 grid(blocks_for(n, 1024));
+    if (aligned16(x) && aligned16(y))
+        hipLaunchKernelGGL((scale_kernel<true>), grid, dim3(256), 0, zest::as_stream(stream), x, n, s, b, y);
+    else
+        hipLaunchKernelGGL((scale_kernel<false>), grid, dim3(256), 0, zest::as_stream(stream), x, n, s, b, y);
     return zest::check_launch("zest_scale");
 }
 
@@ -416,17 +480,19 @@ int zest_rope(const float * x, int64_t T, int64_t heads, int64_t d, const int32_
     ZEST_REQUIRE(x && pos && y && T > 0 && heads > 0 && d > 0, "zest_rope: bad arguments");
     ZEST_REQUIRE(n_dims > 0 && n_dims % 2 == 0 && n_dims <= d, "zest_rope: n_dims=%d d=%lld", n_dims, (long long) d);
     ZEST_REQUIRE(mode == 0 || mode == 2, "zest_rope: mode %d (normal 0 or neox 2)", mode);
+    ZEST_REQUIRE(T <= 0x7fffffff, "zest_rope: %lld tokens", (long long) T);
     const float theta_scale = powf(freq_base, -2.0f / (float) n_dims);
-    hipLaunchKernelGGL(rope_kernel, dim3((unsigned) (T * heads)), dim3(64), 0, zest::as_stream(stream), x, heads, d, pos,
-                       ff, n_dims, mode == 2, theta_scale, freq_scale, ext_factor, attn_factor, corr0, corr1, y);
+    const int half = n_dims / 2;
+    const size_t lds = (size_t) (((half + 1) & ~1) + 2 * half) * sizeof(float);
+    hipLaunchKernelGGL(rope_kernel, dim3((unsigned) T), dim3(256), lds, zest::as_stream(stream), x, heads, d, pos, ff,
+                       n_dims, mode == 2, theta_scale, freq_scale, ext_factor, attn_factor, corr0, corr1, y);
     return zest::check_launch("zest_rope");
 }
 
 int zest_check_finite(const float * y, int64_t rows, int64_t cols, int64_t ld, uint32_t * flag, void * stream) {
     ZEST_REQUIRE(y && flag && rows > 0 && cols > 0 && ld >= cols, "zest_check_finite: bad arguments");
-    const int64_t n = rows * cols;
-    hipLaunchKernelGGL(check_finite_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, zest::as_stream(stream), y, cols,
-                       ld, n, flag);
+    hipLaunchKernelGGL(check_finite_kernel, row_grid(rows, cols), dim3(256), 0, zest::as_stream(stream), y, rows, cols,
+                       ld, flag);
     return zest::check_launch("zest_check_finite");
 }
 

@@ -80,6 +80,30 @@ def test_add_mul_scale(zest_gpu, oracle):
     assert nrmse(_host(zest_gpu.scale(_dev(a), 0.37, 0.25)), oracle.scale(a, np.float32(0.37), np.float32(0.25))) <= EXACT
 
 
+@pytest.mark.parametrize("rows,d,off", [(3, 7, 0), (5, 1030, 1), (70000, 8, 0), (2, 4096, 3), (4, 1028, 2)])
+def test_add_mul_scale_odd_shapes(zest_gpu, oracle, rows, d, off):
+    # widths that are not a multiple of 4, and operands starting `off` floats
+    # past 16-byte alignment, take the scalar path; more rows than one grid
+    # dimension holds (70000) are walked in a loop
+    import torch
+    n = rows * d
+    a, b = Rng(83).normal(n + off, 0, 1.5), Rng(84).normal(n + off, 0, 1.5)
+    r = Rng(85).normal(d + off, 0, 1.5)
+    ta, tb, tr = (_dev(v)[off:] for v in (a, b, r))
+    a2, b2, r2 = a[off:].reshape(rows, d), b[off:].reshape(rows, d), r[off:]
+    assert np.array_equal(_host(zest_gpu.add(ta.view(rows, d), tb.view(rows, d))), oracle.add(a2, b2))
+    assert np.array_equal(_host(zest_gpu.add(ta.view(rows, d), tr, b_is_row=True)), oracle.add_row(a2, r2))
+    assert np.array_equal(_host(zest_gpu.mul_row(ta.view(rows, d), tr)), oracle.mul_row(a2, r2))
+    assert nrmse(_host(zest_gpu.scale(ta, 0.37, 0.25)), oracle.scale(a[off:], np.float32(0.37), np.float32(0.25))) <= EXACT
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    zest_gpu.check_finite(ta.view(rows, d), flag)
+    assert int(flag.item()) == 0
+    bad = ta.clone().view(rows, d)
+    bad[rows - 1, d - 1] = float("inf")
+    zest_gpu.check_finite(bad, flag)
+    assert int(flag.item()) == 1
+
+
 ROPE_CASES = [  # (n_dims, mode, n_ctx_orig, freq_scale, ext_factor, factors): tests/test-host-ops.cpp:146-152
     (64, 0, 0, 1.0, 0.0, False), (64, 2, 0, 1.0, 0.0, False), (32, 0, 0, 1.0, 0.0, False),
     (48, 2, 0, 1.0, 0.0, False), (64, 2, 4096, 0.25, 1.0, False), (64, 2, 4096, 1.0, 0.0, True),
