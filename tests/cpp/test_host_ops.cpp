@@ -223,6 +223,34 @@ static void piece_tests(ggml_backend_t be) {
             test_check(err <= e.tol, "pieces: %-20s nrmse %.2e (allowed %.0e) cos %.7f vs the CPU chain", e.name, err,
                        e.tol, cs);
         }
+
+        // The same graph again: the backend reuses what it worked out about it,
+        // and the results are the same bits.
+        auto read = [](ggml_tensor * t) {
+            fvec v((size_t) ggml_nelements(t));
+            ggml_backend_tensor_get(t, v.data(), 0, ggml_nbytes(t));
+            return v;
+        };
+        const fvec q1 = read(q), o1 = read(o);
+        bool again = ggml_backend_graph_compute(be, gf) == GGML_STATUS_SUCCESS;
+        test_check(again && read(q) == q1 && read(o) == o1, "pieces: computed again, the same results bit for bit");
+
+        // The gate's result made a graph output: it is now read outside the
+        // piece, so gate and up may no longer run fused (the fused GEMM never
+        // writes them). A plan kept from before would leave g unwritten.
+        ggml_set_output(g);
+        std::vector<float> poison((size_t) ggml_nelements(g), -12345.0f);
+        ggml_backend_tensor_set(g, poison.data(), 0, ggml_nbytes(g));
+        again = ggml_backend_graph_compute(be, gf) == GGML_STATUS_SUCCESS;
+        if (again) {
+            double eg, cg, eo, co;
+            cos_nrmse(read(g), gw, eg, cg);
+            cos_nrmse(read(o), ow, eo, co);
+            test_check(eg <= 1e-3 && eo <= 1e-3,
+                       "pieces: with the gate an output, planned again: gate nrmse %.2e, ffn out nrmse %.2e", eg, eo);
+        } else {
+            test_check(false, "pieces: compute with the gate an output");
+        }
     }
     ggml_backend_buffer_free(abuf);
     ggml_backend_buffer_free(wbuf);
