@@ -432,13 +432,16 @@ __device__ inline int partial_off(int unit, int wave, int i, int j, int q, int l
 // Split-K fixup of one consumer wave's block of tile t, split `split` of
 // p.splits. Writes this wave's sums to its unit's partial (sc1 stores), waits
 // for them to be acknowledged, and counts itself in. The wave that arrives
-// last adds the splits' partials in order 0, 1, ... (its own read back like
-// the others), so the result does not depend on arrival order, and resets
-// the counter. Each partial comes into the wave's own LDS region by LDS DMA
-// (all of its loads in flight at once, no registers held), then is added
-// from there. LDS is free: the K loop is over, and this workgroup has no
-// other tile. Returns true for the last wave, whose acc then holds the
-// tile's sums. No wave waits for another.
+// last forms ((p[S-1] + p[S-2]) + p[S-3]) + ... + p[0] and resets the
+// counter. The order is fixed, so the result does not depend on arrival
+// order; since a + b == b + a exactly, a last wave of split S-1 or S-2 (the
+// usual case: splits run in that order) starts from its own sums in acc and
+// reads one partial fewer, others read their own back like the rest. Each
+// partial comes into the wave's own LDS region by LDS DMA (all of its loads
+// in flight at once, no registers held), then is added from there. LDS is
+// free: the K loop is over, and this workgroup has no other tile. Returns
+// true for the last wave, whose acc then holds the tile's sums. No wave
+// waits for another.
 template <class C>
 __device__ inline bool fixup(f32x16 (&acc)[C::TI][C::TJ], const gemm_params & p, uint8_t * smem, int t, int split,
                              int wave, int lane) {
@@ -467,7 +470,15 @@ __device__ inline bool fixup(f32x16 (&acc)[C::TI][C::TJ], const gemm_params & p,
     asm volatile("" ::: "memory");
     if (old != (uint32_t) (S - 1)) return false;
     uint8_t * region = smem + wave * (C::WM * C::WN * 4);
-    for (int u = 0; u < S; u++) {
+    // acc already holds p[S-1] (split S-1) or its commuted first sum's other
+    // operand (split S-2)
+    const bool own = split >= S - 2;
+    for (int v = own ? 1 : 0; v < S; v++) {
+        // p[S-1] first; for split S-2, its own sums stand in for p[S-2]
+        // uniform, but derived from the split, which the tile arithmetic can
+        // leave in a vector register; a DMA's scalar offset taken from one
+        // costs a loop per load
+        const int u = __builtin_amdgcn_readfirstlane(own && v == 1 ? (split == S - 1 ? S - 2 : S - 1) : S - 1 - v);
         const int base = partial_off<C>(u * T + t, wave, 0, 0, 0, 0);
 #pragma unroll
         for (int x = 0; x < PARTS; x++)
@@ -482,7 +493,7 @@ __device__ inline bool fixup(f32x16 (&acc)[C::TI][C::TJ], const gemm_params & p,
                 for (int q = 0; q < 4; q++) {
                     const float4 x =
                         *reinterpret_cast<const float4 *>(region + ((i * C::TJ + j) * 4 + q) * 1024 + lane * 16);
-                    if (u == 0) {
+                    if (v == 0) {
                         acc[i][j][4 * q] = x.x;
                         acc[i][j][4 * q + 1] = x.y;
                         acc[i][j][4 * q + 2] = x.z;
@@ -776,9 +787,12 @@ __global__ __launch_bounds__(CB::NT, 1) void gemm_kernel_mixed(const gemm_params
 #ifndef ZEST_GEMM_TINY_STEP
 #define ZEST_GEMM_TINY_STEP 0.45  // measured: ~0.38 us a step in a launch of 16 or 64 steps
 #endif
-// The fused GLU's 256x128 tiles: 8 consumer waves of 32x128 and 4 producer
-// waves, two consumers on each SIMD (the GLU's long launches gain ~3% from
-// the second consumer; the others lose it to the doubled W fragment reads).
+// 256x128 tiles with 8 consumer waves of 32x128 and 4 producer waves, two
+// consumers on each SIMD: for the fused GLU (its long launches gain ~3% from
+// the second consumer) and for launches of at most one round of whole tiles
+// (each CU has one tile to hide its latencies in: the O projection at 2048
+// tokens, 160 tiles, 57.9 -> 55.7 us); other launches of several rounds lose
+// what the second consumer gains to its doubled W fragment reads.
 #ifndef ZEST_GEMM_GLU
 #define ZEST_GEMM_GLU 256, 128, 8, 256
 #endif
@@ -1018,6 +1032,8 @@ int launch_any(gemm_params p, const int64_t * N, hipStream_t s, const char * nam
             return launch<cfg_tiny, EPI>(p, N, tiny.splits, s, name, fixed);
     }
     if (small.cost < big.cost) return launch<cfg_small, EPI>(p, N, small.splits, s, name, fixed);
+    if constexpr (EPI < 0)
+        if (big.splits == 1 && tiles_of(p, N, CB::BM, CB::BN) <= P) return launch<cfg_glu, EPI>(p, N, 1, s, name, fixed);
     return launch<CB, EPI>(p, N, big.splits, s, name, fixed);
 }
 
