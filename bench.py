@@ -108,7 +108,8 @@ def orc_p():
 GGUF_BLOCKS = {"F16": (1, 1, 2, []), "BF16": (30, 1, 2, []), "Q4_0": (2, 32, 18, [(0, 2)]),
                "Q4_1": (3, 32, 20, [(0, 4)]), "Q5_0": (6, 32, 22, [(0, 2)]), "Q5_1": (7, 32, 24, [(0, 4)]),
                "Q8_0": (8, 32, 34, [(0, 2)]), "Q2_K": (10, 256, 84, [(80, 84)]), "Q3_K": (11, 256, 110, [(108, 110)]),
-               "Q4_K": (12, 256, 144, [(0, 4)]), "Q5_K": (13, 256, 176, [(0, 4)]), "Q6_K": (14, 256, 210, [(208, 210)])}
+               "Q4_K": (12, 256, 144, [(0, 4)]), "Q5_K": (13, 256, 176, [(0, 4)]), "Q6_K": (14, 256, 210, [(208, 210)]),
+               "IQ4_NL": (20, 32, 18, [(0, 2)]), "IQ4_XS": (23, 256, 136, [(0, 2)])}
 
 
 def random_gguf(name: str, n: int, k: int, seed: int):

@@ -49,6 +49,15 @@ inline type_traits traits_of(int type) {
         case GGML_TYPE_Q5_K: return {256, 176};
         case GGML_TYPE_Q6_K: return {256, 210};
         case GGML_TYPE_Q8_K: return {256, 292};
+        case GGML_TYPE_IQ4_NL: return {32, 18};
+        case GGML_TYPE_IQ4_XS: return {256, 136};
+        case GGML_TYPE_IQ2_XXS: return {256, 66};
+        case GGML_TYPE_IQ2_XS: return {256, 74};
+        case GGML_TYPE_IQ2_S: return {256, 82};
+        case GGML_TYPE_IQ3_XXS: return {256, 98};
+        case GGML_TYPE_IQ3_S: return {256, 110};
+        case GGML_TYPE_IQ1_S: return {256, 50};
+        case GGML_TYPE_IQ1_M: return {256, 56};
         case GGML_TYPE_I8: return {1, 1};
         case GGML_TYPE_I16: return {1, 2};
         case GGML_TYPE_I32: return {1, 4};
@@ -60,7 +69,9 @@ inline type_traits traits_of(int type) {
 
 // weight types the converter turns into bfp16 (zest_convert_weight): the
 // reference takes any type with a to_float (src/ggml-zest.cpp:1066-1072);
-// these are GGUF's float and block types (not the IQ family, Q8_1 or Q8_K)
+// these are GGUF's float and block types and the two 4-bit non-uniform grid
+// types (not the codebook IQ types, whose grids are ggml-base tables, Q8_1 or
+// Q8_K)
 inline bool convertible(int type) {
     switch (type) {
         case GGML_TYPE_F32:
@@ -75,7 +86,9 @@ inline bool convertible(int type) {
         case GGML_TYPE_Q3_K:
         case GGML_TYPE_Q4_K:
         case GGML_TYPE_Q5_K:
-        case GGML_TYPE_Q6_K: return true;
+        case GGML_TYPE_Q6_K:
+        case GGML_TYPE_IQ4_NL:
+        case GGML_TYPE_IQ4_XS: return true;
         default: return false;
     }
 }

@@ -3,7 +3,7 @@
 //   zest_pack_act_x      fp32 activations -> the GEMM's expanded operand: the
 //                        same bfp16 blocks, stored decoded as bf16
 //   zest_expand_act      packed bfp16 -> expanded operand
-//   zest_convert_weight  GGUF weights (F32, F16, BF16, Q4_0..Q8_0, Q2_K..Q6_K)
+//   zest_convert_weight  GGUF weights (F32, F16, BF16, Q4_0..Q8_0, Q2_K..Q6_K, IQ4_NL, IQ4_XS)
 //                        -> packed bfp16 (once, into the resident weight cache)
 // All write the layouts of zest_layout.h with 16-byte stores.
 #include "zest_common.h"
@@ -167,6 +167,20 @@ __device__ inline uint32_t spread4(uint32_t x) { return ((x & 0xFu) * 0x00204081
 
 __device__ inline bool finite(float x) { return __builtin_isfinite(x); }
 
+// IQ4_NL / IQ4_XS: four codes (0..15, one a byte) -> their levels + 128 as
+// unsigned bytes. The sixteen levels are GGUF's non-uniform 4-bit grid
+// (ggml-common.h kvalues_iq4nl): -127 -104 -83 -65 -49 -35 -22 -10 1 13 25
+// 38 53 69 89 113. Two byte permutes look up the low and the high eight, and
+// bit 3 of each code picks between them.
+__device__ inline uint32_t iq4_levels(uint32_t n) {
+    constexpr uint32_t T0 = 1u | 24u << 8 | 45u << 16 | 63u << 24, T1 = 79u | 93u << 8 | 106u << 16 | 118u << 24;
+    constexpr uint32_t T2 = 129u | 141u << 8 | 153u << 16 | 166u << 24, T3 = 181u | 197u << 8 | 217u << 16 | 241u << 24;
+    const uint32_t sel = n & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(T1, T0, sel), hi = __builtin_amdgcn_perm(T3, T2, sel);
+    const uint32_t m = ((n >> 3) & 0x01010101u) * 0xffu;
+    return (hi & m) | (lo & ~m);
+}
+
 // 32-value blocks: byte j of qs holds value j (low nibble) and j + 16 (high);
 // bit j of the little-endian 32-bit qh is value j's fifth bit.
 template <int TYPE>
@@ -239,6 +253,46 @@ __device__ inline bool dq_half(const uint8_t * row, int64_t col, int64_t K, floa
                TYPE == ZEST_TYPE_Q5_1) {
         constexpr int B = TYPE == ZEST_TYPE_Q4_0 ? 18 : TYPE == ZEST_TYPE_Q4_1 ? 20 : TYPE == ZEST_TYPE_Q5_0 ? 22 : 24;
         return dq_32<TYPE>(row + (col / 32) * B, v);
+    } else if (TYPE == ZEST_TYPE_IQ4_NL || TYPE == ZEST_TYPE_IQ4_XS) {
+        // IQ4_NL: d, qs[16] (18 bytes), y = d*level[q]. IQ4_XS: d,
+        // scales_h, scales_l[4], qs[128] (136 bytes); sub-block s (32
+        // values) has the 6-bit scale ls = nibble s%2 of scales_l[s/2] |
+        // bits 2s..2s+1 of scales_h << 4, dl = d*(ls - 32), y = dl*level[q].
+        // Byte j of a block's (sub-block's) 16 qs holds value j (low nibble)
+        // and j + 16 (high). d*(ls - 32) has at most 17 significant bits and
+        // its product with a level at most 24, so both are exact, and
+        // fma(level + 128, dl, -128*dl) is the reference's product.
+        float d;
+        bool ok;
+        uint32_t qs[4];
+        if (TYPE == ZEST_TYPE_IQ4_NL) {
+            const uint8_t * p = row + (col / 32) * 18;
+            d = half_to_float((uint16_t) ld16(p));
+            ok = finite(d);
+#pragma unroll
+            for (int i = 0; i < 4; i++) qs[i] = ld32h(p + 2 + 4 * i);
+        } else {
+            const int s = (int) ((col % 256) / 32);
+            const uint8_t * p = row + (col / 256) * 136;  // rows 8-byte aligned
+            const uint2 hdr = *reinterpret_cast<const uint2 *>(p);
+            const uint2 qa = *reinterpret_cast<const uint2 *>(p + 8 + 16 * s);
+            const uint2 qb = *reinterpret_cast<const uint2 *>(p + 16 + 16 * s);
+            const float d0 = half_to_float((uint16_t) (hdr.x & 0xffff));
+            const uint32_t ls = ((hdr.y >> (4 * s)) & 0xFu) | (((hdr.x >> (16 + 2 * s)) & 3u) << 4);
+            d = d0 * (float) ((int) ls - 32);
+            ok = finite(d0);
+            qs[0] = qa.x;
+            qs[1] = qa.y;
+            qs[2] = qb.x;
+            qs[3] = qb.y;
+        }
+        const float c = -128.0f * d;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            fma_bytes(iq4_levels(qs[i] & 0x0F0F0F0Fu), d, c, v + 4 * i);
+            fma_bytes(iq4_levels((qs[i] >> 4) & 0x0F0F0F0Fu), d, c, v + 16 + 4 * i);
+        }
+        return ok;
     } else if (TYPE == ZEST_TYPE_Q8_0) {
         // d, qs[32]: 34 bytes; y = d*q = d*(u - 128) with u = q ^ 0x80
         const uint8_t * p = row + (col / 32) * 34;
@@ -471,6 +525,8 @@ size_t zest_raw_row_bytes(int type, int64_t K) {
         case ZEST_TYPE_Q4_K: return K % 256 ? 0 : (size_t) (K / 256) * 144;
         case ZEST_TYPE_Q5_K: return K % 256 ? 0 : (size_t) (K / 256) * 176;
         case ZEST_TYPE_Q6_K: return K % 256 ? 0 : (size_t) (K / 256) * 210;
+        case ZEST_TYPE_IQ4_NL: return K % 32 ? 0 : (size_t) (K / 32) * 18;
+        case ZEST_TYPE_IQ4_XS: return K % 256 ? 0 : (size_t) (K / 256) * 136;
         default: return 0;
     }
 }
@@ -483,6 +539,7 @@ static size_t row_align(int type) {
         case ZEST_TYPE_BF16:
         case ZEST_TYPE_Q4_K:
         case ZEST_TYPE_Q5_K: return 16;
+        case ZEST_TYPE_IQ4_XS: return 8;
         case ZEST_TYPE_Q4_1:
         case ZEST_TYPE_Q5_1:
         case ZEST_TYPE_Q2_K: return 4;
@@ -587,6 +644,8 @@ static int convert(int type, const void * raw, int64_t N, int64_t K, void * dst,
         ZEST_CONVERT(ZEST_TYPE_Q4_K);
         ZEST_CONVERT(ZEST_TYPE_Q5_K);
         ZEST_CONVERT(ZEST_TYPE_Q6_K);
+        ZEST_CONVERT(ZEST_TYPE_IQ4_NL);
+        ZEST_CONVERT(ZEST_TYPE_IQ4_XS);
         default: return zest::fail(ZEST_E_UNSUPPORTED, "%s: weight type %d has no converter", name, type);
     }
 #undef ZEST_CONVERT

@@ -45,6 +45,8 @@ enum zest_type {
     ZEST_TYPE_Q4_K = 12,
     ZEST_TYPE_Q5_K = 13,
     ZEST_TYPE_Q6_K = 14,
+    ZEST_TYPE_IQ4_NL = 20,
+    ZEST_TYPE_IQ4_XS = 23,
     ZEST_TYPE_BF16 = 30
 };
 
@@ -102,9 +104,9 @@ ZEST_API int zest_expand_act(const void *src, int64_t M, int64_t K, void *dst, v
 /* A GGUF weight raw[N][K] of `type` (any zest_type, rows as ggml stores
  * them) -> packed bfp16 weight cache entry (zest_bfp16_bytes(N, K) bytes).
  * Dequantisation as ggml's to_float, then the same encoder. K must be a
- * multiple of the type's block (32 for Q4_0..Q8_0, 256 for the K-quants).
- * Row alignment: 16 bytes for F32, F16, BF16, Q4_K and Q5_K, 4 for Q4_1,
- * Q5_1 and Q2_K, 2 for the rest. Replaces xdna_npu::add_weight's unpack +
+ * multiple of the type's block (32 for Q4_0..Q8_0 and IQ4_NL, 256 for the
+ * K-quants and IQ4_XS). Row alignment: 16 bytes for F32, F16, BF16, Q4_K and
+ * Q5_K, 8 for IQ4_XS, 4 for Q4_1, Q5_1 and Q2_K, 2 for the rest. Replaces xdna_npu::add_weight's unpack +
  * bfp16_pack_b (src/xdna-npu.cpp:339-378), which converts any type with a
  * to_float (src/ggml-zest.cpp:1066-1072). */
 ZEST_API int zest_convert_weight(int type, const void *raw, int64_t N, int64_t K, void *dst, void *stream);

@@ -126,6 +126,8 @@ size_t orc_row_bytes(int type, int64_t K) {
         case ORC_TYPE_Q4_K: return (size_t) (K / 256) * 144; /* d, dmin, scales[12], qs[128] */
         case ORC_TYPE_Q5_K: return (size_t) (K / 256) * 176; /* d, dmin, scales[12], qh[32], qs[128] */
         case ORC_TYPE_Q6_K: return (size_t) (K / 256) * 210; /* ql[128], qh[64], scales[16], d */
+        case ORC_TYPE_IQ4_NL: return (size_t) (K / 32) * 18;   /* d, qs[16] */
+        case ORC_TYPE_IQ4_XS: return (size_t) (K / 256) * 136; /* d, scales_h, scales_l[4], qs[128] */
         default: return 0;
     }
 }
@@ -341,6 +343,41 @@ static void dequant_q6_k(const uint8_t *src, float *y, int64_t K) {
     }
 }
 
+/* IQ4_NL and IQ4_XS code into GGUF's sixteen non-uniform levels
+ * (ggml-common.h kvalues_iq4nl). */
+static const int8_t iq4_grid[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+/* IQ4_NL (ggml-quants.c dequantize_row_iq4_nl): blocks of 32, byte j of qs
+ * holds value j (low nibble) and j + 16 (high); y = d * grid[code]. */
+static void dequant_iq4_nl(const uint8_t *src, float *y, int64_t K) {
+    for (int64_t b = 0; b < K / 32; b++, src += 18, y += 32) {
+        const float d = f16_at(src);
+        for (int j = 0; j < 16; j++) {
+            y[j] = d * (float) iq4_grid[src[2 + j] & 0xF];
+            y[j + 16] = d * (float) iq4_grid[src[2 + j] >> 4];
+        }
+    }
+}
+
+/* IQ4_XS (dequantize_row_iq4_xs): super-blocks of 256 = 8 sub-blocks of 32.
+ * Sub-block s: ls = nibble s%2 of scales_l[s/2] | bits 2s..2s+1 of scales_h
+ * << 4, dl = d * (ls - 32), y = dl * grid[code], its 16 qs bytes as IQ4_NL's. */
+static void dequant_iq4_xs(const uint8_t *src, float *y, int64_t K) {
+    for (int64_t b = 0; b < K / 256; b++, src += 136) {
+        const float d = f16_at(src);
+        const uint16_t sh = (uint16_t) (src[2] | (src[3] << 8));
+        const uint8_t *sl = src + 4, *qs = src + 8;
+        for (int s = 0; s < 8; s++, qs += 16, y += 32) {
+            const int ls = ((sl[s / 2] >> (4 * (s % 2))) & 0xF) | (((sh >> (2 * s)) & 3) << 4);
+            const float dl = d * (float) (ls - 32);
+            for (int j = 0; j < 16; j++) {
+                y[j] = dl * (float) iq4_grid[qs[j] & 0xF];
+                y[j + 16] = dl * (float) iq4_grid[qs[j] >> 4];
+            }
+        }
+    }
+}
+
 void orc_dequant_row(int type, const void *raw, float *y, int64_t K) {
     const uint8_t *r = (const uint8_t *) raw;
     switch (type) {
@@ -357,6 +394,8 @@ void orc_dequant_row(int type, const void *raw, float *y, int64_t K) {
         case ORC_TYPE_Q4_K: dequant_q4_k(r, y, K); break;
         case ORC_TYPE_Q5_K: dequant_q5_k(r, y, K); break;
         case ORC_TYPE_Q6_K: dequant_q6_k(r, y, K); break;
+        case ORC_TYPE_IQ4_NL: dequant_iq4_nl(r, y, K); break;
+        case ORC_TYPE_IQ4_XS: dequant_iq4_xs(r, y, K); break;
         default: memset(y, 0, (size_t) K * 4); break;
     }
 }
@@ -571,6 +610,47 @@ static void quant_q6_k(const float *x, uint8_t *o) {
             }
 }
 
+/* the grid level nearest x */
+static int iq4_nearest(float x) {
+    int best = 0;
+    for (int i = 1; i < 16; i++)
+        if (fabsf(x - (float) iq4_grid[i]) < fabsf(x - (float) iq4_grid[best])) best = i;
+    return best;
+}
+
+/* IQ4_NL: d = v / -127 (v the signed absmax, so it lands on level -127) */
+static void quant_iq4_nl(const float *x, uint8_t *o) {
+    float d;
+    put_f16(o, signed_absmax(x, 32) / -127.0f, &d);
+    const float id = inv_or_zero(d);
+    for (int j = 0; j < 16; j++)
+        o[2 + j] = (uint8_t) (iq4_nearest(x[j] * id) | (iq4_nearest(x[j + 16] * id) << 4));
+}
+
+/* IQ4_XS: each sub-block's own d_s = v_s / -127 against d = max|d_s| / 32,
+ * ls - 32 = round(d_s / d) in [-32, 31] */
+static void quant_iq4_xs(const float *x, uint8_t *o) {
+    float ds[8], amax = 0.0f, d;
+    for (int s = 0; s < 8; s++) {
+        ds[s] = signed_absmax(x + 32 * s, 32) / -127.0f;
+        amax = fmaxf(amax, fabsf(ds[s]));
+    }
+    put_f16(o, amax / 32.0f, &d);
+    const float id = inv_or_zero(d);
+    uint16_t sh = 0;
+    memset(o + 4, 0, 4);
+    for (int s = 0; s < 8; s++) {
+        const int ls = clampi(ds[s] * id, -32, 31) + 32;
+        o[4 + s / 2] |= (uint8_t) ((ls & 0xF) << (4 * (s % 2)));
+        sh |= (uint16_t) ((ls >> 4) << (2 * s));
+        const float il = inv_or_zero(d * (float) (ls - 32));
+        for (int j = 0; j < 16; j++)
+            o[8 + 16 * s + j] =
+                (uint8_t) (iq4_nearest(x[32 * s + j] * il) | (iq4_nearest(x[32 * s + j + 16] * il) << 4));
+    }
+    memcpy(o + 2, &sh, 2);
+}
+
 int orc_quantize_row(int type, const float *x, void *out, int64_t K) {
     uint8_t *o = (uint8_t *) out;
     const size_t rb = orc_row_bytes(type, K);
@@ -591,7 +671,7 @@ int orc_quantize_row(int type, const float *x, void *out, int64_t K) {
         default: break;
     }
     const int blk = type == ORC_TYPE_Q2_K || type == ORC_TYPE_Q3_K || type == ORC_TYPE_Q4_K || type == ORC_TYPE_Q5_K ||
-                            type == ORC_TYPE_Q6_K
+                            type == ORC_TYPE_Q6_K || type == ORC_TYPE_IQ4_XS
                         ? 256
                         : 32;
     if (K % blk) return -1;
@@ -607,6 +687,8 @@ int orc_quantize_row(int type, const float *x, void *out, int64_t K) {
             case ORC_TYPE_Q4_K: quant_q4_k(x, o); break;
             case ORC_TYPE_Q5_K: quant_q5_k(x, o); break;
             case ORC_TYPE_Q6_K: quant_q6_k(x, o); break;
+            case ORC_TYPE_IQ4_NL: quant_iq4_nl(x, o); break;
+            case ORC_TYPE_IQ4_XS: quant_iq4_xs(x, o); break;
             default: return -1;
         }
     return 0;

@@ -21,6 +21,10 @@
  *                                ...) and quantise/dequantise error bounds;
  *                                ggml's own to_float is absent (third-party,
  *                                not vendored)
+ *   GGUF dequant (IQ4_NL, IQ4_XS) closed form over the published 16-level grid,
+ *                                hand-built blocks, IQ4_XS with every scale
+ *                                32 + 1 is IQ4_NL; the grid itself is parity
+ *                                unpinned (ggml absent)
  *   ref_mul_mat ................ pinned: integer KAT (exact under any order),
  *                                fp64 recomputation bound
  *   host ops ................... RMS_NORM/MUL/ADD/SCALE/GLU pinned by closed forms
@@ -55,7 +59,7 @@ void orc_pack_b(const float *w, int64_t N, int64_t K, int n, int k, int cols, ui
 enum {
     ORC_TYPE_F32 = 0, ORC_TYPE_F16 = 1, ORC_TYPE_Q4_0 = 2, ORC_TYPE_Q4_1 = 3, ORC_TYPE_Q5_0 = 6, ORC_TYPE_Q5_1 = 7,
     ORC_TYPE_Q8_0 = 8, ORC_TYPE_Q2_K = 10, ORC_TYPE_Q3_K = 11, ORC_TYPE_Q4_K = 12, ORC_TYPE_Q5_K = 13,
-    ORC_TYPE_Q6_K = 14, ORC_TYPE_BF16 = 30
+    ORC_TYPE_Q6_K = 14, ORC_TYPE_IQ4_NL = 20, ORC_TYPE_IQ4_XS = 23, ORC_TYPE_BF16 = 30
 };
 size_t orc_row_bytes(int type, int64_t K);
 void orc_dequant_row(int type, const void *raw, float *y, int64_t K);

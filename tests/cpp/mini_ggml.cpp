@@ -41,6 +41,15 @@ blk blk_of(ggml_type t) {
         case GGML_TYPE_Q5_K: return {256, 176};
         case GGML_TYPE_Q6_K: return {256, 210};
         case GGML_TYPE_Q8_K: return {256, 292};
+        case GGML_TYPE_IQ4_NL: return {32, 18};
+        case GGML_TYPE_IQ4_XS: return {256, 136};
+        case GGML_TYPE_IQ2_XXS: return {256, 66};
+        case GGML_TYPE_IQ2_XS: return {256, 74};
+        case GGML_TYPE_IQ2_S: return {256, 82};
+        case GGML_TYPE_IQ3_XXS: return {256, 98};
+        case GGML_TYPE_IQ3_S: return {256, 110};
+        case GGML_TYPE_IQ1_S: return {256, 50};
+        case GGML_TYPE_IQ1_M: return {256, 56};
         case GGML_TYPE_I32: return {1, 4};
         default: fprintf(stderr, "mini_ggml: type %d not known\n", (int) t); abort();
     }

@@ -77,9 +77,14 @@ void floor_rule() {
 void weight_rule() {
     const ggml_type convertible[] = {GGML_TYPE_F32,  GGML_TYPE_F16,  GGML_TYPE_BF16, GGML_TYPE_Q4_0, GGML_TYPE_Q4_1,
                                      GGML_TYPE_Q5_0, GGML_TYPE_Q5_1, GGML_TYPE_Q8_0, GGML_TYPE_Q2_K, GGML_TYPE_Q3_K,
-                                     GGML_TYPE_Q4_K, GGML_TYPE_Q5_K, GGML_TYPE_Q6_K};
+                                     GGML_TYPE_Q4_K, GGML_TYPE_Q5_K, GGML_TYPE_Q6_K, GGML_TYPE_IQ4_NL,
+                                     GGML_TYPE_IQ4_XS};
     for (ggml_type t : convertible) expect(matmul(t, 2048, 2048, 2048), true, "weight", "ggml type %d", (int) t);
     expect(matmul(GGML_TYPE_Q8_K, 2048, 2048, 2048), false, "weight", "q8_K (a dot-product intermediate, no converter)");
+    // the codebook IQ types (their grids are ggml-base tables): left to the next backend
+    const ggml_type codebook[] = {GGML_TYPE_IQ2_XXS, GGML_TYPE_IQ2_XS, GGML_TYPE_IQ3_XXS, GGML_TYPE_IQ1_S,
+                                  GGML_TYPE_IQ3_S,   GGML_TYPE_IQ2_S,  GGML_TYPE_IQ1_M};
+    for (ggml_type t : codebook) expect(matmul(t, 2048, 2048, 2048), false, "weight", "codebook type %d", (int) t);
     expect(matmul(GGML_TYPE_F32, 2052, 2048, 2048), false, "weight", "K = 2052, not a whole number of blocks");
     expect(matmul(GGML_TYPE_F32, 2056, 2048, 2048), true, "weight", "K = 2056, a whole number of blocks");
     // keys read from the cache are views; the score matrix is computed

@@ -144,6 +144,8 @@ int main() {
         {"q2_K  512x256 x 64", GGML_TYPE_Q2_K, 512, 256, 64, false, false, false},
         {"q3_K  512x256 x 64", GGML_TYPE_Q3_K, 512, 256, 64, false, false, false},
         {"q5_K  512x256 x 64", GGML_TYPE_Q5_K, 512, 256, 64, false, false, false},
+        {"iq4_nl 512x256 x 64", GGML_TYPE_IQ4_NL, 512, 256, 64, false, false, false},
+        {"iq4_xs 512x256 x 64", GGML_TYPE_IQ4_XS, 512, 256, 64, false, false, false},
         // held in a weight buffer, as llama.cpp loads a model; one weight type
         // each: the cache is keyed by where a weight lives, and a freed
         // buffer's address comes back

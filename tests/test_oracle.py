@@ -175,7 +175,8 @@ def test_quantize_dequantize_round_trip_bound(oracle, wtype):
 # value at a known position.
 
 F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, BF16 = 1, 2, 3, 6, 7, 8, 10, 11, 12, 13, 14, 30
-ALL_TYPES = [0, F16, BF16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K]
+IQ4_NL, IQ4_XS = 20, 23
+ALL_TYPES = [0, F16, BF16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS]
 
 
 def _u32le(v):
@@ -366,9 +367,60 @@ def test_q6_k_hand_built_blocks(oracle):
         assert np.flatnonzero(y).tolist() == [pos] and y[pos] == 31.0
 
 
+# IQ4_NL and IQ4_XS code into GGUF's published 16-level non-uniform grid
+# (ggml-common.h kvalues_iq4nl; ggml itself is absent, so the grid is taken
+# as published). IQ4_NL: d, qs[16]; IQ4_XS: d, scales_h, scales_l[4],
+# qs[128] with a 6-bit scale per 32-value sub-block, dl = d*(ls - 32).
+IQ4_GRID = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113])
+
+
+def _iq4xs_block(d, ls, q):
+    """One IQ4_XS super-block from d, 8 six-bit scales and 256 codes."""
+    ls = np.asarray(ls, dtype=np.int64)
+    sh = sum(int(ls[s] >> 4) << (2 * s) for s in range(8))
+    sl = np.array([(ls[2 * i] & 0xF) | ((ls[2 * i + 1] & 0xF) << 4) for i in range(4)], dtype=np.uint8)
+    qs = np.concatenate([_nibbles32(q[32 * s:32 * s + 32])[0] for s in range(8)])
+    return np.concatenate([_fp16(d), np.array([sh], dtype="<u2").view(np.uint8), sl, qs])
+
+
+def test_iq4_nl_hand_built_blocks(oracle):
+    rng = np.random.default_rng(11)
+    for d in (0.5, 3.0e-4, -2.0):
+        q = rng.integers(0, 16, 32)
+        qs, _ = _nibbles32(q)
+        y = oracle.dequant(IQ4_NL, np.concatenate([_fp16(d), qs]), 1, 32).reshape(-1)
+        assert np.array_equal(y, (IQ4_GRID[q] * np.float64(np.float16(d))).astype(np.float32))
+    # each code once, in order, then reversed: the grid's own order
+    q = np.concatenate([np.arange(16), np.arange(16)[::-1]])
+    y = oracle.dequant(IQ4_NL, np.concatenate([_fp16(1.0), _nibbles32(q)[0]]), 1, 32).reshape(-1)
+    assert y[:16].tolist() == IQ4_GRID.tolist() and y[16:].tolist() == IQ4_GRID[::-1].tolist()
+
+
+def test_iq4_xs_hand_built_blocks(oracle):
+    rng = np.random.default_rng(12)
+    g = np.arange(256) // 32
+    for d in (0.01, -1.5):
+        ls, q = rng.integers(0, 64, 8), rng.integers(0, 16, 256)
+        y = oracle.dequant(IQ4_XS, _iq4xs_block(d, ls, q), 1, 256).reshape(-1)
+        dl = np.float32(np.float16(d)) * (ls - 32).astype(np.float32)
+        assert np.array_equal(y, dl[g] * IQ4_GRID[q].astype(np.float32))
+    # each sub-block's scale alone: scale 63 in sub-block s, 32 (dl = 0) elsewhere
+    q = rng.integers(0, 16, 256)
+    for s in range(8):
+        ls = np.full(8, 32)
+        ls[s] = 63
+        y = oracle.dequant(IQ4_XS, _iq4xs_block(1.0, ls, q), 1, 256).reshape(-1)
+        assert not y[g != s].any() and np.array_equal(y[g == s], 31.0 * IQ4_GRID[q[g == s]])
+    # with every scale 33 (dl = d) a super-block is eight IQ4_NL blocks
+    d = 0.0625
+    nl = np.concatenate([np.concatenate([_fp16(d), _nibbles32(q[32 * s:32 * s + 32])[0]]) for s in range(8)])
+    assert np.array_equal(oracle.dequant(IQ4_XS, _iq4xs_block(d, np.full(8, 33), q), 1, 256),
+                          oracle.dequant(IQ4_NL, nl, 1, 256))
+
+
 @pytest.mark.parametrize("wtype,bound", [
     (F16, 5e-4), (BF16, 4e-3), (Q4_0, 0.1), (Q4_1, 0.09), (Q5_0, 0.05), (Q5_1, 0.045), (Q8_0, 0.006),
-    (Q2_K, 0.45), (Q3_K, 0.2), (Q4_K, 0.09), (Q5_K, 0.045), (Q6_K, 0.025)])
+    (Q2_K, 0.45), (Q3_K, 0.2), (Q4_K, 0.09), (Q5_K, 0.045), (Q6_K, 0.025), (IQ4_NL, 0.1), (IQ4_XS, 0.1)])
 def test_oracle_quantiser_round_trip(oracle, wtype, bound):
     # the synthetic rows decode to the weights they came from, within the
     # type's resolution (nrmse over normal weights)

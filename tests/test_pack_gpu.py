@@ -170,11 +170,11 @@ def test_convert_extreme_quant_blocks(zest_gpu, oracle):
 # quantised normal weights and on random bytes (every code, bit and scale).
 
 GGUF = {"f16": 1, "bf16": 30, "q4_0": 2, "q4_1": 3, "q5_0": 6, "q5_1": 7, "q8_0": 8,
-        "q2_K": 10, "q3_K": 11, "q4_K": 12, "q5_K": 13, "q6_K": 14}
-K_QUANTS = {10, 11, 12, 13, 14}
+        "q2_K": 10, "q3_K": 11, "q4_K": 12, "q5_K": 13, "q6_K": 14, "iq4_nl": 20, "iq4_xs": 23}
+K_QUANTS = {10, 11, 12, 13, 14, 23}  # 256-value super-blocks
 # byte ranges of each block's fp16 fields (kept finite in the random blocks)
 F16_FIELDS = {2: [(0, 2)], 3: [(0, 4)], 6: [(0, 2)], 7: [(0, 4)], 8: [(0, 2)], 10: [(80, 84)],
-              11: [(108, 110)], 12: [(0, 4)], 13: [(0, 4)], 14: [(208, 210)]}
+              11: [(108, 110)], 12: [(0, 4)], 13: [(0, 4)], 14: [(208, 210)], 20: [(0, 2)], 23: [(0, 2)]}
 
 
 def random_gguf(oracle, wtype: int, n: int, k: int, seed: int) -> np.ndarray:
@@ -231,7 +231,7 @@ def test_convert_gu_every_type_is_the_interleaved_pair(zest_gpu, oracle, name):
     assert np.array_equal(bp[dst], bg) and np.array_equal(bp[dst + 32], bu)
 
 
-@pytest.mark.parametrize("name", ["q8_0", "q4_0", "q5_0", "q3_K", "q6_K"])
+@pytest.mark.parametrize("name", ["q8_0", "q4_0", "q5_0", "q3_K", "q6_K", "iq4_nl"])
 def test_convert_two_byte_aligned_rows(zest_gpu, oracle, name):
     # the types whose rows need only 2-byte alignment, from a buffer that
     # starts 2 bytes past a 4-byte boundary: the converter's aligned loads
@@ -258,6 +258,8 @@ def test_convert_rejects_bad_rows(zest_gpu, oracle):
         zest_gpu.convert_weight(13, raw[4:], 16, 256)    # Q5_K rows need 16
     with pytest.raises(RuntimeError):
         zest_gpu.convert_weight(14, raw, 4, 128)         # Q6_K: K % 256 != 0
+    with pytest.raises(RuntimeError):
+        zest_gpu.convert_weight(23, raw[4:], 16, 256)    # IQ4_XS rows need 8
     with pytest.raises(RuntimeError):
         zest_gpu.convert_weight(2, raw, 4, 48)           # Q4_0: K % 32 != 0
     with pytest.raises(RuntimeError):
