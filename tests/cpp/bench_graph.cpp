@@ -16,9 +16,11 @@
 //          q/k/v in the next), as the scheduler splits a model whose
 //          attention stays on the CPU: 37 graph_compute calls per chunk,
 //          each ending in a stream synchronize.
-// Weights are random GGUF blocks with finite scales, one set per layer,
-// converted into the weight cache at load (graph_optimize); the input rows
-// are resident on the GPU before the clock starts.
+// Weights are N(0, 0.02) values quantised to Q4_K / Q8_0, as the C-ABI
+// stack's: one set of GGUF bytes per weight shape, shared by the layers,
+// each layer still its own tensor and cache entry. They are converted into
+// the weight cache at load (graph_optimize); the input rows are resident on
+// the GPU before the clock starts.
 //
 // Prints one JSON line per mode: tokens per second and the MUL_MAT TFLOP/s
 // of the whole prompt, host time per graph_compute included. With
@@ -43,30 +45,6 @@ constexpr int64_t HIDDEN = 2560, QDIM = 4096, KVDIM = 1024, FFN = 9728, TOKENS =
 struct layer_w {
     ggml_tensor * q, * k, * v, * o, * gate, * up, * down, * attn_norm, * ffn_norm;
 };
-
-// random GGUF blocks: bytes from a xorshift stream, then each block's fp16
-// scale fields set to small finite values
-void fill_gguf(std::vector<uint8_t> & buf, ggml_type type, uint64_t seed) {
-    uint64_t s = seed * 0x9E3779B97F4A7C15ull + 1;
-    for (size_t i = 0; i + 8 <= buf.size(); i += 8) {
-        s ^= s << 13;
-        s ^= s >> 7;
-        s ^= s << 17;
-        memcpy(&buf[i], &s, 8);
-    }
-    if (type == GGML_TYPE_Q4_K) {  // d, dmin at bytes 0..3 of each 144-byte block
-        for (size_t b = 0; b + 144 <= buf.size(); b += 144) {
-            const uint16_t d = 0x0C00, dmin = 0x0800;  // 2^-12, 2^-13
-            memcpy(&buf[b], &d, 2);
-            memcpy(&buf[b + 2], &dmin, 2);
-        }
-    } else {  // Q8_0: d at bytes 0..1 of each 34-byte block
-        for (size_t b = 0; b + 34 <= buf.size(); b += 34) {
-            const uint16_t d = 0x1000;  // 2^-11
-            memcpy(&buf[b], &d, 2);
-        }
-    }
-}
 
 ggml_tensor * new_weight(ggml_context * c, ggml_type t, int64_t k, int64_t n, int layer, const char * name) {
     ggml_tensor * w = ggml_new_tensor_2d(c, t, k, n);
@@ -156,16 +134,23 @@ int main(int argc, char ** argv) {
     }
     ggml_backend_buffer_set_usage(wbuf, GGML_BACKEND_BUFFER_USAGE_WEIGHTS);
     {
-        std::vector<uint8_t> bytes;
+        // the GGUF bytes of each weight shape: N(0, 0.02) rows quantised
+        std::vector<std::vector<uint8_t>> src;
+        test_rng wrng(7);
+        for (ggml_tensor * t : {L[0].q, L[0].k, L[0].v, L[0].o, L[0].gate, L[0].up, L[0].down}) {
+            std::vector<float> wf((size_t) (t->ne[0] * t->ne[1]));
+            for (float & f : wf) f = wrng.normal(0.0f, 0.02f);
+            src.emplace_back(ggml_nbytes(t));
+            ggml_quantize_chunk(t->type, wf.data(), src.back().data(), 0, t->ne[1], t->ne[0], nullptr);
+        }
         std::vector<float> row((size_t) HIDDEN);
         test_rng rng(11);
         for (int l = 0; l < layers; l++) {
             const layer_w & w = L[(size_t) l];
-            int i = 0;
+            size_t i = 0;
             for (ggml_tensor * t : {w.q, w.k, w.v, w.o, w.gate, w.up, w.down}) {
-                bytes.resize(ggml_nbytes(t));
-                fill_gguf(bytes, t->type, (uint64_t) (l * 16 + i++));
-                ggml_backend_tensor_set(t, bytes.data(), 0, bytes.size());
+                ggml_backend_tensor_set(t, src[i].data(), 0, src[i].size());
+                i++;
             }
             for (ggml_tensor * t : {w.attn_norm, w.ffn_norm}) {
                 for (float & f : row) f = 1.0f + 0.1f * rng.normal(0.0f, 1.0f);
