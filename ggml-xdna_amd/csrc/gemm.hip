@@ -474,10 +474,11 @@ __device__ inline bool fixup(f32x16 (&acc)[C::TI][C::TJ], const gemm_params & p,
     // operand (split S-2)
     const bool own = split >= S - 2;
     for (int v = own ? 1 : 0; v < S; v++) {
-        // p[S-1] first; for split S-2, its own sums stand in for p[S-2]
-        // uniform, but derived from the split, which the tile arithmetic can
-        // leave in a vector register; a DMA's scalar offset taken from one
-        // costs a loop per load
+        // operand v of the sum is p[S-1-v], except that a split-S-2 wave's
+        // second operand is p[S-1] (its own sums stand in for p[S-2]). u is
+        // uniform but derived from the split, which the tile arithmetic can
+        // leave in a vector register, and a DMA's scalar offset taken from
+        // one costs a loop per load
         const int u = __builtin_amdgcn_readfirstlane(own && v == 1 ? (split == S - 1 ? S - 2 : S - 1) : S - 1 - v);
         const int base = partial_off<C>(u * T + t, wave, 0, 0, 0, 0);
 #pragma unroll
