@@ -217,7 +217,7 @@ def test_convert_every_type_matches_oracle(zest_gpu, oracle, name):
         assert np.array_equal(gpu_convert(zest_gpu, wtype, raw, N, K), want), (name, N, K, "random")
 
 
-@pytest.mark.parametrize("name", ["q4_0", "q5_1", "q3_K", "q6_K", "f16"])
+@pytest.mark.parametrize("name", ["q4_0", "q5_1", "q3_K", "q6_K", "f16", "iq4_xs"])
 def test_convert_gu_every_type_is_the_interleaved_pair(zest_gpu, oracle, name):
     import torch
     wtype, F, K = GGUF[name], 96, 512
