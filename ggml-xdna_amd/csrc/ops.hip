@@ -484,6 +484,7 @@ int zest_rope(const float * x, int64_t T, int64_t heads, int64_t d, const int32_
     const float theta_scale = powf(freq_base, -2.0f / (float) n_dims);
     const int half = n_dims / 2;
     const size_t lds = (size_t) (((half + 1) & ~1) + 2 * half) * sizeof(float);
+    ZEST_REQUIRE(lds <= 65536, "zest_rope: n_dims=%d needs %zu bytes of shared memory (at most 65536)", n_dims, lds);
     hipLaunchKernelGGL(rope_kernel, dim3((unsigned) T), dim3(256), lds, zest::as_stream(stream), x, heads, d, pos, ff,
                        n_dims, mode == 2, theta_scale, freq_scale, ext_factor, attn_factor, corr0, corr1, y);
     return zest::check_launch("zest_rope");
