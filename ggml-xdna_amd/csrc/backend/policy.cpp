@@ -157,8 +157,9 @@ bool exec_supports(const ggml_tensor * op) {
             const int n_dims = param_i32(op, 1), mode = param_i32(op, 2), n_offs = param_i32(op, 15);
             const ggml_tensor * ff = op->src[2];
             if (ff && (!f32_contig(ff) || ff->ne[0] < n_dims / 2)) return false;
+            // n_dims <= 8192: the kernel's angle table (1.5 n_dims floats) fits 64 KiB of shared memory
             return (mode == GGML_ROPE_TYPE_NEOX || mode == GGML_ROPE_TYPE_NORMAL) && n_dims > 0 && n_dims % 2 == 0 &&
-                   n_dims <= a->ne[0] && n_offs == 0 && a->ne[3] == 1 && b->ne[0] == a->ne[2];
+                   n_dims <= a->ne[0] && n_dims <= 8192 && n_offs == 0 && a->ne[3] == 1 && b->ne[0] == a->ne[2];
         }
         default: return false;
     }
