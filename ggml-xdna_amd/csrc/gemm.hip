@@ -258,20 +258,22 @@ __device__ inline void store_tile(const f32x16 (&acc)[C::TI][C::TJ], float * Cou
     const int row0 = (int) m0 + wm * C::WM;
     const float * rl = nullptr;  // the residual block in LDS: WM rows of WN floats
     if constexpr (RES) {
-        // a row of the block is LPR lanes of 16 bytes; an instruction takes RPI rows
-        constexpr int LPR = C::WN / 4, RPI = 64 / LPR;
-        static_assert(64 % LPR == 0 && C::WM % RPI == 0, "whole residual rows per instruction");
+        // the block row-major in the region: instruction q fills bytes
+        // [1024q, 1024q + 1024), lane l the 16 at 1024q + 16l, i.e. floats
+        // f = 256q + 4l, row f / WN and column f % WN (a lane's 4 floats never
+        // straddle rows: WN % 4 == 0); the whole byte offset is in the vector
+        // offset, so the range check turns rows past M into zeros instead of
+        // reads past the residual
+        static_assert(C::WM * C::WN % 256 == 0 && C::WN % 4 == 0, "whole DMA instructions");
         uint8_t * region = smem + wave * (C::WM * C::WN * 4);
         const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<float *>(res), (short) 0, (int) (M * ldr * 4), 0x00020000);
-        // instruction q: rows RPI*q.. of the block, lane l taking row RPI*q + l/LPR, bytes 16(l%LPR);
-        // the whole byte offset is in the vector offset, so the range check
-        // turns rows past M into zeros instead of reads past the residual
-        const int voff = (int) ((row0 + lane / LPR) * ldr * 4 + (n0 + wn * C::WN) * 4 + (lane % LPR) * 16);
 #pragma unroll
-        for (int q = 0; q < C::WM / RPI; q++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_ptr_t) (region + q * 1024), 16,
-                                                     voff + (int) (RPI * q * ldr * 4), 0, 0, 0);
+        for (int q = 0; q < C::WM * C::WN / 256; q++) {
+            const int f = 256 * q + 4 * lane, r = f / C::WN, c = f - r * C::WN;
+            const int voff = (int) ((row0 + r) * ldr * 4 + (n0 + wn * C::WN + c) * 4);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_ptr_t) (region + q * 1024), 16, voff, 0, 0, 0);
+        }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         rl = reinterpret_cast<const float *>(region);
     }
@@ -791,13 +793,25 @@ __global__ __launch_bounds__(CB::NT, 1) void gemm_kernel_mixed(const gemm_params
 // 256x128 tiles with 8 consumer waves of 32x128 and 4 producer waves, two
 // consumers on each SIMD: for the fused GLU (its long launches gain ~3% from
 // the second consumer) and for launches of at most one round of whole tiles
-// (each CU has one tile to hide its latencies in: the O projection at 2048
-// tokens, 160 tiles, 57.9 -> 55.7 us); other launches of several rounds lose
-// what the second consumer gains to its doubled W fragment reads.
+// that 128x160 tiles cannot take (each CU has one tile to hide its latencies
+// in: the O projection at 2048 tokens as 160 of these, 57.9 -> 55.7 us);
+// other launches of several rounds lose what the second consumer gains to
+// its doubled W fragment reads.
 #ifndef ZEST_GEMM_GLU
 #define ZEST_GEMM_GLU 256, 128, 8, 256
 #endif
+// 128x160 tiles (4 consumer waves of 32x160, 5 producer waves) for a launch
+// that 256x128 tiles would run in one round, unsplit, when its weights are
+// whole 160-row tiles and these fit one round too: the O projection at 2048
+// tokens (2048 x 2560) is 256 of them, one per CU, where 160 256x128 tiles
+// leave 96 CUs idle (55.5 -> ~49 us). A split launch keeps its plan: the
+// down projection (K 9728) as 256 of these unsplit takes ~115 us against
+// 107 us in three splits.
+#ifndef ZEST_GEMM_O
+#define ZEST_GEMM_O 128, 160, 4, 320
+#endif
 using cfg_big = gemm_cfg<ZEST_GEMM_BIG>;
+using cfg_o = gemm_cfg<ZEST_GEMM_O>;
 using cfg_small = gemm_cfg<ZEST_GEMM_SMALL>;
 using cfg_glu = gemm_cfg<ZEST_GEMM_GLU>;
 using cfg_tiny = gemm_cfg<ZEST_GEMM_TINY>;
@@ -1034,7 +1048,16 @@ int launch_any(gemm_params p, const int64_t * N, hipStream_t s, const char * nam
     }
     if (small.cost < big.cost) return launch<cfg_small, EPI>(p, N, small.splits, s, name, fixed);
     if constexpr (EPI < 0)
-        if (big.splits == 1 && tiles_of(p, N, CB::BM, CB::BN) <= P) return launch<cfg_glu, EPI>(p, N, 1, s, name, fixed);
+        if (big.splits == 1 && tiles_of(p, N, CB::BM, CB::BN) <= P) {
+            // one round of whole tiles: as 128x160 tiles where the weights
+            // are whole 160-row tiles (the tiles then read only rows each
+            // packed weight holds) and they fit one round too, else with two
+            // consumers per SIMD
+            bool whole = true;
+            for (int i = 0; i < p.nw; i++) whole &= N[i] % cfg_o::BN == 0;
+            if (whole && tiles_of(p, N, cfg_o::BM, cfg_o::BN) <= P) return launch<cfg_o, EPI>(p, N, 1, s, name, fixed);
+            return launch<cfg_glu, EPI>(p, N, 1, s, name, fixed);
+        }
     return launch<CB, EPI>(p, N, big.splits, s, name, fixed);
 }
 

@@ -113,6 +113,16 @@ def test_scalar_offsets_stay_inside_operands(M, N, K):
         if S > 1 and nk // S < 4:
             continue  # the planner never splits below four steps a split
         check_launch(M, N, K, BM, BN, CWM, S)
+    # the 128x160 tiles (cfg_o): unsplit, and only for weights of whole 160-row tiles
+    if N % 160 == 0:
+        check_launch(M, N, K, 128, 160, 4, 1)
+
+
+def test_o_tiles_need_whole_160_row_weights():
+    # the launch rule has teeth: 160-row tiles over a weight of 200 rows
+    # would read rows its packed operand (256 rows) does not hold
+    with pytest.raises(AssertionError):
+        check_launch(1024, 200, 1024, 128, 160, 4, 1)
 
 
 def test_unclamped_prefetch_would_leave_the_operand():

@@ -215,6 +215,44 @@ def test_gemm_group(zest_gpu, oracle, M, K, ns, wtype):
         assert worst <= 1.0, i
 
 
+@pytest.mark.parametrize("M,ns,K", [
+    (2000, [2560], 4096),         # config 3's O projection with ragged rows: 256 tiles of 128 x 160
+    (1024, [5120], 1024),
+    (1500, [1600, 1760], 1024),   # a group of two weights, 252 tiles
+])
+def test_gemm_160_row_tiles(zest_gpu, oracle, M, ns, K):
+    # a launch that 256 x 128 tiles run in one round, unsplit, while 128 x 128
+    # tiles would take two, runs as 128 x 160 tiles when every weight is whole
+    # 160-row tiles: against the oracle; with the residual epilogue (rows past
+    # M of the residual holding NaN), bit for bit the GEMM followed by the ADD
+    import torch
+    x = Rng(M + 7).normal(M * K).reshape(M, K)
+    a = zest_gpu.pack_act_x(_dev(x))
+    ws = []
+    for i, n in enumerate(ns):
+        w = Rng(n + 7 + i).normal(n * K, 0, 0.02).reshape(n, K)
+        ws.append(zest_gpu.convert_weight(0, _dev(w.view(np.uint8)), n, K))
+    nf = torch.zeros(1, dtype=torch.int32, device="cuda")
+    outs = zest_gpu.gemm_group(a, M, ws, ns, K, nonfinite=nf)
+    torch.cuda.synchronize()
+    assert int(nf.item()) == 0
+    rows = np.unique(np.concatenate([np.linspace(0, M - 1, 40).astype(int), [127, 128, M - 1]]))
+    ad = decoded_act(zest_gpu, oracle, a, M, K)[rows]
+    for i, n in enumerate(ns):
+        r64, ab = oracle.mul_mat_f64(decoded(zest_gpu, oracle, ws[i], n, K), ad)
+        worst, maxrel = gemm_check(outs[i].cpu().numpy()[rows], r64, ab, K)
+        assert worst <= 1.0 and maxrel <= 1e-3, i
+    if len(ns) == 1:
+        N = ns[0]
+        big = torch.full((M + 64, N), float("nan"), device="cuda")
+        big[:M] = torch.from_numpy(Rng(M * 5).normal(M * N).reshape(M, N)).cuda()
+        want = zest_gpu.add(outs[0], big[:M].contiguous())
+        got = zest_gpu.gemm_residual(a, M, ws[0], N, K, big[:M], nonfinite=nf)
+        torch.cuda.synchronize()
+        assert int(nf.item()) == 0
+        assert torch.equal(got.view(torch.int32), want.view(torch.int32))
+
+
 def test_gemm_part_round_as_half_tiles(zest_gpu, oracle):
     # M = 2048, N = 6144: 384 tiles of 256 x 128, one round of the GPU's 256
     # CUs and half of another; the launch runs the last 128 tiles as 256 of
