@@ -21,6 +21,7 @@
 // K-step. The store is fp32 row-major, as the reference's output mode 0
 // (kernels/bfp16_gemm/aie_kernels/aie2p/mm_bfp_acc.cc:106-116, 258-278).
 #include <algorithm>
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <type_traits>
@@ -895,26 +896,28 @@ int sk_reserve(hipStream_t s, size_t partial_bytes, size_t n_counters, sk_space 
 
 template <class C, int EPI, bool SPLIT>
 int set_lds(const char * name) {
-    static bool attr_set = false;
-    if (!attr_set) {
+    // threads that launch a kernel for the first time at once may both set
+    // the attribute: the same value, harmless
+    static std::atomic<bool> attr_set{false};
+    if (!attr_set.load(std::memory_order_acquire)) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_kernel<C, EPI, SPLIT>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int) C::LDS_BYTES);
         if (e != hipSuccess) return zest::fail(ZEST_E_HIP, "%s: LDS attribute: %s", name, hipGetErrorString(e));
-        attr_set = true;
+        attr_set.store(true, std::memory_order_release);
     }
     return ZEST_OK;
 }
 
 template <int EPI>
 int set_lds_mixed(const char * name) {
-    static bool attr_set = false;
-    if (!attr_set) {
+    static std::atomic<bool> attr_set{false};
+    if (!attr_set.load(std::memory_order_acquire)) {
         const size_t bytes = std::max(cfg_big::LDS_BYTES, cfg_small::LDS_BYTES);
         const hipError_t e =
             hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_kernel_mixed<cfg_big, cfg_small, EPI>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int) bytes);
         if (e != hipSuccess) return zest::fail(ZEST_E_HIP, "%s: LDS attribute: %s", name, hipGetErrorString(e));
-        attr_set = true;
+        attr_set.store(true, std::memory_order_release);
     }
     return ZEST_OK;
 }
