@@ -54,17 +54,19 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// BM x BN tile; CWM consumer waves, each a WM x BN block of 32x32 MFMA tiles
-// (TI x TJ of them); NP/64 producer waves (as many by default). LDS holds the expanded W ring;
-// after the K loop each consumer wave uses WM x BN floats of it for its
-// epilogue. MINB workgroups a CU at least (the launch bound).
-template <int BM_, int BN_, int CWM_, int NP_ = 64 * CWM_, int MINB_ = 1>
+// BM x BN tile; CWM x CWN consumer waves, each a WM x WN block of 32x32 MFMA
+// tiles (TI x TJ of them; consumer w takes row block w % CWM, column block
+// w / CWM); NP/64 producer waves (as many as the consumers' row blocks by
+// default). LDS holds the expanded W ring; after the K loop each consumer
+// wave uses WM x WN floats of it for its epilogue. MINB workgroups a CU at
+// least (the launch bound).
+template <int BM_, int BN_, int CWM_, int NP_ = 64 * CWM_, int MINB_ = 1, int CWN_ = 1>
 struct gemm_cfg {
-    static constexpr int BM = BM_, BN = BN_, CWM = CWM_, CWN = 1, MINB = MINB_;
-    static constexpr int NC = 64 * CWM;  // consumer threads
-    static constexpr int NP = NP_;       // producer threads
+    static constexpr int BM = BM_, BN = BN_, CWM = CWM_, CWN = CWN_, MINB = MINB_;
+    static constexpr int NC = 64 * CWM * CWN;  // consumer threads
+    static constexpr int NP = NP_;             // producer threads
     static constexpr int NT = NC + NP;
-    static constexpr int WM = BM / CWM, WN = BN;
+    static constexpr int WM = BM / CWM, WN = BN / CWN;
     static constexpr int TI = WM / 32, TJ = WN / 32;
     static constexpr int BU = BN * 4 / NP;  // W units (two blocks) per producer thread per K-step
     static constexpr int ROWB = 128;        // LDS bytes per row (64 bf16)
@@ -651,11 +653,12 @@ __device__ inline void run_tile(const gemm_params & p, uint8_t * smem, const gem
         return;
     }
 
-    // Consumer: rows wm*WM.. of the tile, every column.
-    const int wm = wave, wn = 0, khalf = lane >> 5, wr = lane & 31;
+    // Consumer: rows wm*WM.. and columns wn*WN.. of the tile. swz depends
+    // only on the row mod 16, so a column block's W rows keep rows wr's.
+    const int wm = wave % C::CWM, wn = wave / C::CWM, khalf = lane >> 5, wr = lane & 31;
     int fw[4];
 #pragma unroll
-    for (int s = 0; s < 4; s++) fw[s] = wr * C::ROWB + ((2 * s + khalf) ^ swz(wr)) * 16;
+    for (int s = 0; s < 4; s++) fw[s] = (wn * C::WN + wr) * C::ROWB + ((2 * s + khalf) ^ swz(wr)) * 16;
     f32x16 acc[C::TI][C::TJ];
 #pragma unroll
     for (int i = 0; i < C::TI; i++)
@@ -793,11 +796,11 @@ __global__ __launch_bounds__(CB::NT, 1) void gemm_kernel_mixed(const gemm_params
 #endif
 // 256x128 tiles with 8 consumer waves of 32x128 and 4 producer waves, two
 // consumers on each SIMD: for the fused GLU (its long launches gain ~3% from
-// the second consumer) and for launches of at most one round of whole tiles
-// that 128x160 tiles cannot take (each CU has one tile to hide its latencies
-// in: the O projection at 2048 tokens as 160 of these, 57.9 -> 55.7 us);
-// other launches of several rounds lose what the second consumer gains to
-// its doubled W fragment reads.
+// the second consumer), the whole tiles of mixed launches, and launches of
+// at most one round of whole tiles that 128x160 tiles cannot take (each CU
+// has one tile to hide its latencies in: the O projection at 2048 tokens as
+// 160 of these, 57.9 -> 55.7 us); other launches of several rounds lose what
+// the second consumer gains to its doubled W fragment reads.
 #ifndef ZEST_GEMM_GLU
 #define ZEST_GEMM_GLU 256, 128, 8, 256
 #endif
@@ -816,6 +819,11 @@ using cfg_o = gemm_cfg<ZEST_GEMM_O>;
 using cfg_small = gemm_cfg<ZEST_GEMM_SMALL>;
 using cfg_glu = gemm_cfg<ZEST_GEMM_GLU>;
 using cfg_tiny = gemm_cfg<ZEST_GEMM_TINY>;
+// Mixed launches run their whole tiles as cfg_glu's (two consumers per SIMD)
+// and the halves as 128x128 tiles of 8 consumer waves of 32x64 (4 row blocks
+// x 2 column blocks) and 4 producers, the same threads (the q/k/v group at
+// 2048 tokens: 66.8 -> 65.6 us against one consumer per SIMD in both).
+using cfg_half8 = gemm_cfg<128, 128, 4, 256, 1, 2>;
 
 // Per device and stream: the split-K workspace (grown as needed; counters
 // zeroed when allocated, and zero again after every launch).
@@ -908,13 +916,13 @@ int set_lds(const char * name) {
     return ZEST_OK;
 }
 
-template <int EPI>
+template <class CB, class CS, int EPI>
 int set_lds_mixed(const char * name) {
     static std::atomic<bool> attr_set{false};
     if (!attr_set.load(std::memory_order_acquire)) {
-        const size_t bytes = std::max(cfg_big::LDS_BYTES, cfg_small::LDS_BYTES);
+        const size_t bytes = std::max(CB::LDS_BYTES, CS::LDS_BYTES);
         const hipError_t e =
-            hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_kernel_mixed<cfg_big, cfg_small, EPI>),
+            hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_kernel_mixed<CB, CS, EPI>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int) bytes);
         if (e != hipSuccess) return zest::fail(ZEST_E_HIP, "%s: LDS attribute: %s", name, hipGetErrorString(e));
         attr_set.store(true, std::memory_order_release);
@@ -998,9 +1006,8 @@ int launch(gemm_params p, const int64_t * N, int splits, hipStream_t s, const ch
 }
 
 // A mixed launch: the first nbig big tiles whole, the rest as halves.
-template <int EPI>
+template <class CB, class CS, int EPI>
 int launch_mixed(gemm_params p, const int64_t * N, int64_t nbig, hipStream_t s, const char * name) {
-    using CB = cfg_big;
     p.mt = (int) ((p.M + CB::BM - 1) / CB::BM);
     int nt = 0;
     for (int i = 0; i < p.nw; i++) {
@@ -1013,10 +1020,10 @@ int launch_mixed(gemm_params p, const int64_t * N, int64_t nbig, hipStream_t s, 
         return zest::fail(ZEST_E_ARG, "%s: mixed launch of %lld tiles", name, (long long) T);
     p.splits = 1;
     p.nbig = (int) nbig;
-    const int st = set_lds_mixed<EPI>(name);
+    const int st = set_lds_mixed<CB, CS, EPI>(name);
     if (st != ZEST_OK) return st;
-    hipLaunchKernelGGL((gemm_kernel_mixed<cfg_big, cfg_small, EPI>), dim3((unsigned) grid), dim3(CB::NT),
-                       std::max(cfg_big::LDS_BYTES, cfg_small::LDS_BYTES), s, p);
+    hipLaunchKernelGGL((gemm_kernel_mixed<CB, CS, EPI>), dim3((unsigned) grid), dim3(CB::NT),
+                       std::max(CB::LDS_BYTES, CS::LDS_BYTES), s, p);
     return zest::check_launch(name);
 }
 
@@ -1039,7 +1046,7 @@ int launch_any(gemm_params p, const int64_t * N, hipStream_t s, const char * nam
         if (R >= 1 && rem > 0 && R * P % 8 == 0) {
             const double mixed =
                 ((double) R + (double) ((2 * rem + P - 1) / P) * ZEST_GEMM_SMALL_STEP) * (p.nk + ZEST_GEMM_PROLOGUE);
-            if (mixed < big.cost && mixed < small.cost) return launch_mixed<EPI>(p, N, R * P, s, name);
+            if (mixed < big.cost && mixed < small.cost) return launch_mixed<cfg_glu, cfg_half8, EPI>(p, N, R * P, s, name);
         }
     }
     if constexpr (EPI < 0) {
