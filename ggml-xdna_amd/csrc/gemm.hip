@@ -20,6 +20,9 @@
 // the consumers read its first fragments before step k ends. One barrier per
 // K-step. The store is fp32 row-major, as the reference's output mode 0
 // (kernels/bfp16_gemm/aie_kernels/aie2p/mm_bfp_acc.cc:106-116, 258-278).
+// A launch of several rounds of whole tiles runs as persistent workgroups,
+// one a CU, each walking its XCD's tiles and fetching the next tile's first
+// steps while it finishes the current one (gemm_kernel_tiles).
 #include <algorithm>
 #include <atomic>
 #include <map>
@@ -548,25 +551,27 @@ __device__ inline void produce_step(const producer<C> & pr, uint8_t * smem, int 
     pr.load_w(r, w_off_next);
 }
 
-// The producer's part of one tile over K-steps [k0, k0 + ns): step j's W
-// units are loaded during step j-4 and stored into stage j%3 during step j-2
-// (the consumers read step j+1's first fragments before the barrier that
-// ends step j, so a stage must be complete a step before it is consumed, and
-// it is free only after the step that last read it). Every load goes into
-// registers and every LDS store is the compiler's own, so the compiler counts
-// the loads in flight and waits for exactly those whose registers a store
-// reads; before a barrier only the LDS stores are waited for. Steps 0-3 are
-// requested whether or not this tile has them (a step past this split's
-// steps reads the next split's slab; one past the operand's last step, `last`
-// steps after w0, reads that last step again; neither is stored), so the
-// steady state starts with an exact count; it runs without conditions, and
-// the last steps do their remaining stores one by one. The barriers match the
-// consumers', step for step.
+// The producer's part of one tile over K-steps [k0, k0 + ns), with steps 0
+// and 1 already requested into r0 and r1: step j's W units are loaded during
+// step j-4 and stored into stage j%3 during step j-2 (the consumers read step
+// j+1's first fragments before the barrier that ends step j, so a stage must
+// be complete a step before it is consumed, and it is free only after the
+// step that last read it). Every load goes into registers and every LDS store
+// is the compiler's own, so the compiler counts the loads in flight and waits
+// for exactly those whose registers a store reads; before a barrier only the
+// LDS stores are waited for. Steps 2-3 are requested whether or not this tile
+// has them (a step past this split's steps reads the next split's slab; one
+// past the operand's last step, `last` steps after w0, reads that last step
+// again; neither is stored), so the steady state starts with an exact count;
+// it runs without conditions, and the last steps do their remaining stores
+// one by one. With `next` (ns even), the two requests that follow the tile's
+// last step fetch steps 0 and 1 of the workgroup's next tile (producer pn, at
+// wn0) into r0 and r1 instead. The barriers match the consumers', step for
+// step.
 template <class C>
-__device__ inline void produce(const producer<C> & pr, uint8_t * smem, int w0, int w_kstride, int ns, int last) {
-    stage_regs<C> r0, r1;
-    pr.load_w(r0, w0);
-    pr.load_w(r1, w0 + min(1, last) * w_kstride);
+__device__ inline void produce_tile(const producer<C> & pr, uint8_t * smem, int w0, int w_kstride, int ns, int last,
+                                    stage_regs<C> & r0, stage_regs<C> & r1, const producer<C> & pn, int wn0,
+                                    int wn_kstride, bool next) {
     pr.store_w(r0, smem, 0);
     pr.load_w(r0, w0 + min(2, last) * w_kstride);
     if (ns > 1) pr.store_w(r1, smem, C::STAGE);
@@ -588,7 +593,10 @@ __device__ inline void produce(const producer<C> & pr, uint8_t * smem, int w0, i
     for (; k < ns; k += 2) {
         if (k + 2 < ns) {
             pr.store_w(r0, smem, stage);
-            if (k + 4 < ns) pr.load_w(r0, w0 + (k + 4) * w_kstride);
+            if (k + 4 < ns)
+                pr.load_w(r0, w0 + (k + 4) * w_kstride);
+            else if (next && k + 4 == ns)
+                pn.load_w(r0, wn0);
         }
         stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
         wait_lgkm0();
@@ -596,13 +604,72 @@ __device__ inline void produce(const producer<C> & pr, uint8_t * smem, int w0, i
         if (k + 1 < ns) {
             if (k + 3 < ns) {
                 pr.store_w(r1, smem, stage);
-                if (k + 5 < ns) pr.load_w(r1, w0 + (k + 5) * w_kstride);
+                if (k + 5 < ns)
+                    pr.load_w(r1, w0 + (k + 5) * w_kstride);
+                else if (next && k + 5 == ns + 1)
+                    pn.load_w(r1, wn0 + wn_kstride);
             }
             stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
             wait_lgkm0();
             bare_barrier();
         }
     }
+}
+
+// The producer's part of a workgroup's only tile.
+template <class C>
+__device__ inline void produce(const producer<C> & pr, uint8_t * smem, int w0, int w_kstride, int ns, int last) {
+    stage_regs<C> r0, r1;
+    pr.load_w(r0, w0);
+    pr.load_w(r1, w0 + min(1, last) * w_kstride);
+    produce_tile<C>(pr, smem, w0, w_kstride, ns, last, r0, r1, pr, 0, 0, false);
+}
+
+// The consumer's K loop over a tile's steps [0, ns), its A fragments of
+// steps 0 and 1 requested into a0s and a1s: starts with the barrier that
+// completes the first two W stages. Past the tile's last step, a load of
+// step j reads step min(j, last) (the next split's slab or the operand's
+// last step again, never used); with NEXT, step ns + j of the tile reads step
+// j of the workgroup's next tile at an (which then start the next call in a0s
+// and a1s: ns is even). Pairs of steps run without conditions.
+template <class C, bool NEXT>
+__device__ inline void consume_tile(f32x16 (&acc)[C::TI][C::TJ], bf16x8 (&a0s)[4][C::TI], bf16x8 (&a1s)[4][C::TI],
+                                    const uint8_t * smem, const int (&fw)[4], const a_loader<C> & al, int a0, int ks,
+                                    int ns, int last, int an) {
+    bf16x8 bw[2][C::TJ];
+    bare_barrier();
+#pragma unroll
+    for (int j = 0; j < C::TJ; j++) bw[0][j] = lds_get(smem, fw[0] + j * 32 * C::ROWB);
+    int cur = 0, k = 0;
+    for (; k + 1 < ns; k += 2) {
+        int nxt = cur == 2 * C::STAGE ? 0 : cur + C::STAGE;
+        consume<C, true>(acc, a0s, bw, smem, fw, cur, nxt, al,
+                         NEXT ? (k + 2 < ns ? a0 + (k + 2) * ks : an + (k + 2 - ns) * ks) : a0 + min(k + 2, last) * ks);
+        cur = nxt;
+        bare_barrier();
+        nxt = cur == 2 * C::STAGE ? 0 : cur + C::STAGE;
+        consume<C, true>(acc, a1s, bw, smem, fw, cur, nxt, al,
+                         NEXT ? (k + 3 < ns ? a0 + (k + 3) * ks : an + (k + 3 - ns) * ks) : a0 + min(k + 3, last) * ks);
+        cur = nxt;
+        bare_barrier();
+    }
+    if (k < ns) {
+        const int nxt = cur == 2 * C::STAGE ? 0 : cur + C::STAGE;
+        consume<C, false>(acc, a0s, bw, smem, fw, cur, nxt, al, 0);
+        bare_barrier();
+    }
+}
+
+// The consumer's epilogue of one tile.
+template <class C, int EPI>
+__device__ inline void epilogue(const f32x16 (&acc)[C::TI][C::TJ], const gemm_params & p, uint8_t * smem,
+                                const gemm_weight & W, int64_t m0, int64_t n0, int wave, int wm, int wn, int lane) {
+    if constexpr (EPI == EPI_RESIDUAL)
+        store_tile<C, true>(acc, W.c, p.M, W.n, W.ldc, m0, n0, wm, wn, lane, p.nonfinite, p.res, p.ldr, smem, wave);
+    else if constexpr (EPI < 0)
+        store_tile<C>(acc, W.c, p.M, W.n, W.ldc, m0, n0, wm, wn, lane, p.nonfinite);
+    else
+        store_glu<C, EPI>(acc, smem, p.xout, p.h, p.ldh, p.M, W.n / 2, m0, n0, wave, wm, wn, lane, p.nonfinite);
 }
 
 // Tile t of a launch in the tile order: tiles go in groups of GROUP_M tile
@@ -674,41 +741,15 @@ __device__ inline void run_tile(const gemm_params & p, uint8_t * smem, const gem
         // the operand's last K-step, counted from a0: the steps loaded past
         // it load it again (the scalar offset is not range-checked)
         const int last = nk - 1 - k0;
-        bf16x8 a0s[4][C::TI], a1s[4][C::TI], bw[2][C::TJ];
+        bf16x8 a0s[4][C::TI], a1s[4][C::TI];
         al.load_step(a0s, a0);
         al.load_step(a1s, a0 + min(1, last) * ks);
-        bare_barrier();
-#pragma unroll
-        for (int j = 0; j < C::TJ; j++) bw[0][j] = lds_get(smem, fw[0] + j * 32 * C::ROWB);
-        int cur = 0, k = 0;
-        // pairs of steps without conditions (the loads of steps past the
-        // tile's end read the next split's slab or the operand's last step
-        // again, and are never used)
-        for (; k + 1 < ns; k += 2) {
-            int nxt = cur == 2 * C::STAGE ? 0 : cur + C::STAGE;
-            consume<C, true>(acc, a0s, bw, smem, fw, cur, nxt, al, a0 + min(k + 2, last) * ks);
-            cur = nxt;
-            bare_barrier();
-            nxt = cur == 2 * C::STAGE ? 0 : cur + C::STAGE;
-            consume<C, true>(acc, a1s, bw, smem, fw, cur, nxt, al, a0 + min(k + 3, last) * ks);
-            cur = nxt;
-            bare_barrier();
-        }
-        if (k < ns) {
-            const int nxt = cur == 2 * C::STAGE ? 0 : cur + C::STAGE;
-            consume<C, false>(acc, a0s, bw, smem, fw, cur, nxt, al, 0);
-            bare_barrier();
-        }
+        consume_tile<C, false>(acc, a0s, a1s, smem, fw, al, a0, ks, ns, last, 0);
         // the loads of steps past the end are still in flight
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     }
     if (SPLIT && !fixup<C>(acc, p, smem, t, split, wave, lane)) return;
-    if constexpr (EPI == EPI_RESIDUAL)
-        store_tile<C, true>(acc, W.c, p.M, W.n, W.ldc, m0, n0, wm, wn, lane, p.nonfinite, p.res, p.ldr, smem, wave);
-    else if constexpr (EPI < 0)
-        store_tile<C>(acc, W.c, p.M, W.n, W.ldc, m0, n0, wm, wn, lane, p.nonfinite);
-    else
-        store_glu<C, EPI>(acc, smem, p.xout, p.h, p.ldh, p.M, W.n / 2, m0, n0, wave, wm, wn, lane, p.nonfinite);
+    epilogue<C, EPI>(acc, p, smem, W, m0, n0, wave, wm, wn, lane);
 }
 
 // EPI: EPI_PLAIN the fp32 store, EPI_RESIDUAL the fp32 store of acc + res,
@@ -752,6 +793,79 @@ __global__ __launch_bounds__(CB::NT, 1) void gemm_kernel_mixed(const gemm_params
     }
 }
 
+// Persistent workgroups for a launch of more than one round of whole tiles
+// (ns = nk, even, at least 4). Workgroup b works on XCD b % 8 and takes the
+// tiles of that XCD's run (the contiguous run xcd_order gives it) in turn:
+// start + b/8, start + b/8 + G/8, ... for G workgroups, a multiple of 8. The
+// producers' last two requests of a tile fetch the next tile's first two W
+// steps, so its first stages are stored without waiting for memory; the
+// consumers request the next tile's first two A steps after the epilogue
+// (held through it they would not fit the registers), and a barrier keeps the
+// producers' stores out of the LDS the epilogue uses.
+template <class C, int EPI>
+__global__ __launch_bounds__(C::NT, 1) void gemm_kernel_tiles(const gemm_params p) {
+    extern __shared__ uint4 smem_u4[];
+    uint8_t * smem = reinterpret_cast<uint8_t *>(smem_u4);
+    const int b = (int) blockIdx.x, g = (int) gridDim.x / 8, T = p.mt * p.nt, nk = p.nk;
+    const int x = b % 8, end = (x + 1) * (T / 8) + min(x + 1, T % 8);
+    int t = x * (T / 8) + min(x, T % 8) + b / 8;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int64_t m0, n0;
+    gemm_weight W = tile_of<C>(p, t, m0, n0);
+    if (wave >= C::NC / 64) {
+        const int job = tid - C::NC;
+        producer<C> pr(W.w, (int64_t) W.w_kstride * nk, job);
+        int w0 = __builtin_amdgcn_readfirstlane((int) ((n0 / ZEST_TILE_ROWS) * ZEST_TILE_BYTES));
+        stage_regs<C> r0, r1;
+        pr.load_w(r0, w0);
+        pr.load_w(r1, w0 + W.w_kstride);
+        for (;;) {
+            const int tn = t + g;
+            const bool next = tn < end;
+            int64_t mn = m0, nn = n0;
+            const gemm_weight Wn = next ? tile_of<C>(p, tn, mn, nn) : W;
+            const producer<C> pn(Wn.w, (int64_t) Wn.w_kstride * nk, job);
+            const int wn0 = __builtin_amdgcn_readfirstlane((int) ((nn / ZEST_TILE_ROWS) * ZEST_TILE_BYTES));
+            produce_tile<C>(pr, smem, w0, W.w_kstride, nk, nk - 1, r0, r1, pn, wn0, Wn.w_kstride, next);
+            if (!next) return;
+            bare_barrier();  // the consumers' epilogue is done with the LDS
+            t = tn;
+            W = Wn;
+            pr = pn;
+            w0 = wn0;
+        }
+    }
+    const int wm = wave % C::CWM, wn = wave / C::CWM, khalf = lane >> 5, wr = lane & 31;
+    int fw[4];
+#pragma unroll
+    for (int s = 0; s < 4; s++) fw[s] = (wn * C::WN + wr) * C::ROWB + ((2 * s + khalf) ^ swz(wr)) * 16;
+    const a_loader<C> al(p.a, (int64_t) p.a_kstride * nk, wm, lane);
+    const int ks = p.a_kstride;
+    int a0 = __builtin_amdgcn_readfirstlane((int) ((m0 / ZEST_XGROUP_ROWS) * ZEST_XGROUP_BYTES));
+    bf16x8 a0s[4][C::TI], a1s[4][C::TI];
+    al.load_step(a0s, a0);
+    al.load_step(a1s, a0 + ks);
+    for (;;) {
+        f32x16 acc[C::TI][C::TJ];
+#pragma unroll
+        for (int i = 0; i < C::TI; i++)
+#pragma unroll
+            for (int j = 0; j < C::TJ; j++) acc[i][j] = f32x16{};
+        consume_tile<C, false>(acc, a0s, a1s, smem, fw, al, a0, ks, nk, nk - 1, 0);
+        // the loads of steps past the end are still in flight
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+        epilogue<C, EPI>(acc, p, smem, W, m0, n0, wave, wm, wn, lane);
+        t += g;
+        if (t >= end) return;
+        W = tile_of<C>(p, t, m0, n0);
+        a0 = __builtin_amdgcn_readfirstlane((int) ((m0 / ZEST_XGROUP_ROWS) * ZEST_XGROUP_BYTES));
+        al.load_step(a0s, a0);
+        al.load_step(a1s, a0 + ks);
+        bare_barrier();  // the epilogue is done with the LDS the producers fill next
+    }
+}
+
 // 256x128 tiles (4 consumer waves of 64x128); 128x128 (4 of 32x128) where
 // the cost model prefers them (few rows, or too few big tiles).
 #ifndef ZEST_GEMM_BIG
@@ -770,6 +884,9 @@ __global__ __launch_bounds__(CB::NT, 1) void gemm_kernel_mixed(const gemm_params
 // launch, however little data they move. A 128x128 step costs SMALL_STEP of
 // a 256x128 one (half the MFMA work, not half the waiting). The cheapest plan
 // wins.
+#ifndef ZEST_GEMM_PERSIST
+#define ZEST_GEMM_PERSIST 1
+#endif
 #ifndef ZEST_GEMM_MAX_SPLIT
 #define ZEST_GEMM_MAX_SPLIT 16
 #endif
@@ -916,6 +1033,18 @@ int set_lds(const char * name) {
     return ZEST_OK;
 }
 
+template <class C, int EPI>
+int set_lds_tiles(const char * name) {
+    static std::atomic<bool> attr_set{false};
+    if (!attr_set.load(std::memory_order_acquire)) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_kernel_tiles<C, EPI>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int) C::LDS_BYTES);
+        if (e != hipSuccess) return zest::fail(ZEST_E_HIP, "%s: LDS attribute: %s", name, hipGetErrorString(e));
+        attr_set.store(true, std::memory_order_release);
+    }
+    return ZEST_OK;
+}
+
 template <class CB, class CS, int EPI>
 int set_lds_mixed(const char * name) {
     static std::atomic<bool> attr_set{false};
@@ -996,6 +1125,21 @@ int launch(gemm_params p, const int64_t * N, int splits, hipStream_t s, const ch
         p.partial = sp.partial;
         p.counters = sp.counters;
     }
+#if ZEST_GEMM_PERSIST
+    if (EPI != EPI_RESIDUAL && p.splits == 1 && C::MINB == 1 && p.nk % 2 == 0 && p.nk >= 4) {
+        // more than one round: persistent workgroups, one a CU (not for the
+        // residual epilogue, whose persistent form does not fit the registers)
+        int dev = 0;
+        (void) hipGetDevice(&dev);
+        const int64_t G = cu_count(dev) / 8 * 8;
+        if (G >= 8 && T > G) {
+            const int st = set_lds_tiles<C, EPI>(name);
+            if (st != ZEST_OK) return st;
+            hipLaunchKernelGGL((gemm_kernel_tiles<C, EPI>), dim3((unsigned) G), dim3(C::NT), C::LDS_BYTES, s, p);
+            return zest::check_launch(name);
+        }
+    }
+#endif
     const int st = p.splits > 1 ? set_lds<C, EPI, true>(name) : set_lds<C, EPI, false>(name);
     if (st != ZEST_OK) return st;
     if (p.splits > 1)

@@ -7,7 +7,8 @@ kernel must never form one. This restates, in integers, the offsets of
 gemm.hip's a_loader (the consumers' A fragments), producer::load_w (the W
 slab) and fixup's partial sums, with the step sequences of run_tile and
 produce, and checks the largest byte each launch touches against the
-operand's size. (store_tile's stores and residual reads keep their whole
+operand's size; and that the persistent kernel's workgroups take every tile
+once and request the next tile's first steps only after their own. (store_tile's stores and residual reads keep their whole
 offset in the vector offset; test_gemm_gpu's ragged residual test covers
 them.) CPU only."""
 from __future__ import annotations
@@ -59,6 +60,42 @@ def producer_steps(ns, last):
             steps.append(k + 5)
         k += 2
     return steps
+
+
+def producer_tail_requests(ns):
+    """produce_tile's requests after its prologue, for a tile followed by
+    another (`next`): ('own', step) for the tile's steps, ('next', step) for
+    the next tile's first steps, in the order they are made."""
+    req = [("own", 2), ("own", 3)]
+    k = 0
+    while k + 5 < ns:
+        req += [("own", k + 4), ("own", k + 5)]
+        k += 2
+    while k < ns:
+        if k + 2 < ns:
+            if k + 4 < ns:
+                req.append(("own", k + 4))
+            elif k + 4 == ns:
+                req.append(("next", 0))
+        if k + 1 < ns and k + 3 < ns:
+            if k + 5 < ns:
+                req.append(("own", k + 5))
+            elif k + 5 == ns + 1:
+                req.append(("next", 1))
+        k += 2
+    return req
+
+
+def persistent_tiles(T, G):
+    """gemm_kernel_tiles' walk: workgroup b on XCD b % 8 takes the tiles of
+    that XCD's run (xcd_order's contiguous run) from start + b // 8 in steps of
+    G // 8."""
+    g, out = G // 8, []
+    for b in range(G):
+        x = b % 8
+        end = (x + 1) * (T // 8) + min(x + 1, T % 8)
+        out.append(list(range(x * (T // 8) + min(x, T % 8) + b // 8, end, g)))
+    return out
 
 
 def check_launch(M, N, K, BM, BN, CWM, S):
@@ -123,6 +160,29 @@ def test_o_tiles_need_whole_160_row_weights():
     # would read rows its packed operand (256 rows) does not hold
     with pytest.raises(AssertionError):
         check_launch(1024, 200, 1024, 128, 160, 4, 1)
+
+
+@pytest.mark.parametrize("ns", [4, 6, 8, 16, 40, 64, 152, 272])
+def test_persistent_tile_requests_each_step_once(ns):
+    # a tile followed by another requests each of its own steps 2..ns-1 once,
+    # then the next tile's steps 0 and 1 into the registers that start it
+    # (step 0 into the even set, step 1 into the odd one)
+    req = producer_tail_requests(ns)
+    own = [s for kind, s in req if kind == "own"]
+    assert sorted(own) == list(range(2, ns))
+    assert [s for kind, s in req if kind == "next"] == [0, 1]
+    assert req.index(("next", 0)) > req.index(("own", ns - 2))
+    assert req.index(("next", 1)) > req.index(("own", ns - 1))
+
+
+@pytest.mark.parametrize("T,G", [(257, 256), (384, 256), (512, 256), (1216, 256), (768, 256), (300, 248), (1000, 8)])
+def test_persistent_workgroups_cover_every_tile_once(T, G):
+    walks = persistent_tiles(T, G)
+    tiles = sorted(t for w in walks for t in w)
+    assert tiles == list(range(T))
+    assert all(len(w) >= 1 for w in walks)
+    # the rounds stay balanced: no workgroup takes more than one tile more than another
+    assert max(map(len, walks)) - min(map(len, walks)) <= 1
 
 
 def test_unclamped_prefetch_would_leave_the_operand():

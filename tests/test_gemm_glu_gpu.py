@@ -66,6 +66,7 @@ def separate(z, kind, a, m, gate, up, wtype, f, k):
     (12, 2048, 9728, 2560),  # BASELINE config 2's gate/up: 2048 x 9728 x 2560, Q4_K
     (8, 2048, 1280, 9728),   # few tiles, long K: the launch splits K
     (0, 2048, 3072, 512),    # 384 tiles: a round and a half, the half as 128-row tiles
+    (0, 1500, 4096, 512),    # 6 x 64 = 384 tiles, ragged rows: persistent workgroups
 ])
 def test_gemm_glu_matches_unfused_swiglu(zest_gpu, oracle, wtype, M, F, K):
     import torch

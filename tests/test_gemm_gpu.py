@@ -253,6 +253,37 @@ def test_gemm_160_row_tiles(zest_gpu, oracle, M, ns, K):
         assert torch.equal(got.view(torch.int32), want.view(torch.int32))
 
 
+@pytest.mark.parametrize("M,ns,K", [
+    (4000, [2048, 1024, 1024], 512),  # 16 x 32 = 512 tiles of 256 x 128: two rounds, persistent workgroups
+    (2048, [4096, 4096, 4096], 1024),  # 8 x 96 = 768 tiles: three rounds
+    (4000, [2048, 1024, 1024], 576),  # an odd number of K-steps: one workgroup a tile
+])
+def test_gemm_rounds_equal_one_round_launches(zest_gpu, oracle, M, ns, K):
+    # A launch of more than one round of whole tiles, unsplit, runs as
+    # persistent workgroups that take their XCD's tiles in turn and fetch the
+    # next tile's first steps during the current one. Every output is summed
+    # over K in the same order as in a launch of one round, so the group
+    # launch equals, bit for bit, each weight launched alone (at most one
+    # round), and it meets the oracle's bar.
+    import torch
+    x = Rng(M + K).normal(M * K).reshape(M, K)
+    a = zest_gpu.pack_act_x(_dev(x))
+    ws = [zest_gpu.convert_weight(0, _dev(Rng(n + i + K).normal(n * K, 0, 0.02).reshape(n, K).view(np.uint8)), n, K)
+          for i, n in enumerate(ns)]
+    nf = torch.zeros(1, dtype=torch.int32, device="cuda")
+    outs = zest_gpu.gemm_group(a, M, ws, ns, K, nonfinite=nf)
+    alone = [zest_gpu.gemm(a, M, w, n, K) for w, n in zip(ws, ns)]
+    torch.cuda.synchronize()
+    assert int(nf.item()) == 0
+    for i in range(len(ns)):
+        assert torch.equal(outs[i].view(torch.int32), alone[i].view(torch.int32)), i
+    rows = np.unique(np.concatenate([np.linspace(0, M - 1, 32).astype(int), [255, 256, M - 1]]))
+    ad = decoded_act(zest_gpu, oracle, a, M, K)[rows]
+    r64, ab = oracle.mul_mat_f64(decoded(zest_gpu, oracle, ws[-1], ns[-1], K), ad)
+    worst, maxrel = gemm_check(outs[-1].cpu().numpy()[rows], r64, ab, K)
+    assert worst <= 1.0 and maxrel <= 1e-3
+
+
 def test_gemm_part_round_as_half_tiles(zest_gpu, oracle):
     # M = 2048, N = 6144: 384 tiles of 256 x 128, one round of the GPU's 256
     # CUs and half of another; the launch runs the last 128 tiles as 256 of
