@@ -300,11 +300,14 @@ def traffic_summary(fetch_dir: str, write_dir: str) -> int:
 
 # The stack's GEMM launch kinds, told apart by the kernel's template arguments
 # (demangled names): the q/k/v group runs as a mixed launch, O as a residual
-# launch, gate/up as the fused GLU launch (epilogue kind 2, SwiGLU), down as a
-# split-K residual launch.
+# launch, gate/up as the fused GLU launch (epilogue kind 2, SwiGLU; persistent
+# workgroups when it takes more than one round), down as a split-K residual
+# launch.
 def gemm_kind(name: str):
     if "gemm_kernel_mixed" in name:
         return "qkv"
+    if "gemm_kernel_tiles<" in name:
+        return "gate_up" if ", 2>(" in name else "other"
     if "gemm_kernel<" not in name:
         return None
     if ", -2, true>" in name:
