@@ -22,7 +22,8 @@
 // (kernels/bfp16_gemm/aie_kernels/aie2p/mm_bfp_acc.cc:106-116, 258-278).
 // A launch of several rounds of whole tiles runs as persistent workgroups,
 // one a CU, each walking its XCD's tiles and fetching the next tile's first
-// steps while it finishes the current one (gemm_kernel_tiles).
+// steps while it finishes the current one (gemm_kernel_tiles; mixed launches:
+// gemm_kernel_mixed_tiles).
 #include <algorithm>
 #include <atomic>
 #include <map>
@@ -866,6 +867,110 @@ __global__ __launch_bounds__(C::NT, 1) void gemm_kernel_tiles(const gemm_params 
     }
 }
 
+// One item of a persistent mixed launch, a consumer wave's part: the K loop
+// of a tile (its A fragments of steps 0 and 1 requested into a0s and a1s),
+// then its epilogue.
+template <class C, int EPI>
+__device__ inline void consume_item(const gemm_params & p, uint8_t * smem, const gemm_weight & W, int64_t m0,
+                                    int64_t n0, int wave, int lane, bf16x8 (&a0s)[4][C::TI],
+                                    bf16x8 (&a1s)[4][C::TI]) {
+    const int wm = wave % C::CWM, wn = wave / C::CWM, khalf = lane >> 5, wr = lane & 31;
+    int fw[4];
+#pragma unroll
+    for (int s = 0; s < 4; s++) fw[s] = (wn * C::WN + wr) * C::ROWB + ((2 * s + khalf) ^ swz(wr)) * 16;
+    const a_loader<C> al(p.a, (int64_t) p.a_kstride * p.nk, wm, lane);
+    const int a0 = __builtin_amdgcn_readfirstlane((int) ((m0 / ZEST_XGROUP_ROWS) * ZEST_XGROUP_BYTES));
+    f32x16 acc[C::TI][C::TJ];
+#pragma unroll
+    for (int i = 0; i < C::TI; i++)
+#pragma unroll
+        for (int j = 0; j < C::TJ; j++) acc[i][j] = f32x16{};
+    consume_tile<C, false>(acc, a0s, a1s, smem, fw, al, a0, p.a_kstride, p.nk, p.nk - 1, 0);
+    // the loads of steps past the end are still in flight
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    epilogue<C, EPI>(acc, p, smem, W, m0, n0, wave, wm, wn, lane);
+}
+
+// A consumer wave's requests of a tile's first two A steps.
+template <class C>
+__device__ inline void load_item_a(const gemm_params & p, int64_t m0, int wave, int lane, bf16x8 (&a0s)[4][C::TI],
+                                   bf16x8 (&a1s)[4][C::TI]) {
+    const a_loader<C> al(p.a, (int64_t) p.a_kstride * p.nk, wave % C::CWM, lane);
+    const int a0 = __builtin_amdgcn_readfirstlane((int) ((m0 / ZEST_XGROUP_ROWS) * ZEST_XGROUP_BYTES));
+    al.load_step(a0s, a0);
+    al.load_step(a1s, a0 + p.a_kstride);
+}
+
+// The mixed launch as persistent workgroups (nk even, at least 4), one a CU:
+// workgroup b takes the whole tiles of XCD b % 8's run (the first nbig/8 of
+// its tiles, as gemm_kernel_mixed's first nbig workgroups have them), then
+// the half tiles of that XCD's run of halves, from b/8 in steps of G/8 (G
+// workgroups, a multiple of 8, at most nbig). The producers request the next
+// item's first two W steps during the current item's last ones (a half tile
+// has its whole tile's W rows and the same producer layout); the consumers
+// request its first two A steps after their epilogue.
+template <class CB, class CS, int EPI>
+__global__ __launch_bounds__(CB::NT, 1) void gemm_kernel_mixed_tiles(const gemm_params p) {
+    static_assert(CB::NT == CS::NT && CS::BM * 2 == CB::BM && CS::BN == CB::BN && CS::NP == CB::NP &&
+                      CS::TI == CB::TI,
+                  "halves of the big tiles, with the same producers");
+    extern __shared__ uint4 smem_u4[];
+    uint8_t * smem = reinterpret_cast<uint8_t *>(smem_u4);
+    const int b = (int) blockIdx.x, g = (int) gridDim.x / 8, x = b % 8, j = b / 8, nk = p.nk;
+    const int T = p.mt * p.nt, per_xcd = p.nbig / 8, nhalf = 2 * (T - p.nbig);
+    const int hs = x * (nhalf / 8) + min(x, nhalf % 8), he = (x + 1) * (nhalf / 8) + min(x + 1, nhalf % 8);
+    const int n_whole = (per_xcd - j + g - 1) / g;
+    const int n_items = n_whole + (hs + j < he ? (he - hs - j + g - 1) / g : 0);
+    // item i: its tile, and the first row of its rows (a half's)
+    auto item = [&](int i, int64_t & m0, int64_t & n0) {
+        if (i < n_whole) return tile_of<CB>(p, x * per_xcd + j + i * g, m0, n0);
+        const int u = hs + j + (i - n_whole) * g;
+        const gemm_weight w = tile_of<CB>(p, p.nbig + u / 2, m0, n0);
+        m0 += (u % 2) * CS::BM;
+        return w;
+    };
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int64_t m0, n0;
+    gemm_weight W = item(0, m0, n0);
+    if (wave >= CB::NC / 64) {
+        const int job = tid - CB::NC;
+        producer<CB> pr(W.w, (int64_t) W.w_kstride * nk, job);
+        int w0 = __builtin_amdgcn_readfirstlane((int) ((n0 / ZEST_TILE_ROWS) * ZEST_TILE_BYTES));
+        stage_regs<CB> r0, r1;
+        pr.load_w(r0, w0);
+        pr.load_w(r1, w0 + W.w_kstride);
+        for (int i = 0;; i++) {
+            const bool next = i + 1 < n_items;
+            int64_t mn = m0, nn = n0;
+            const gemm_weight Wn = next ? item(i + 1, mn, nn) : W;
+            const producer<CB> pn(Wn.w, (int64_t) Wn.w_kstride * nk, job);
+            const int wn0 = __builtin_amdgcn_readfirstlane((int) ((nn / ZEST_TILE_ROWS) * ZEST_TILE_BYTES));
+            produce_tile<CB>(pr, smem, w0, W.w_kstride, nk, nk - 1, r0, r1, pn, wn0, Wn.w_kstride, next);
+            if (!next) return;
+            bare_barrier();  // the consumers' epilogue is done with the LDS
+            W = Wn;
+            pr = pn;
+            w0 = wn0;
+        }
+    }
+    bf16x8 a0s[4][CB::TI], a1s[4][CB::TI];
+    load_item_a<CB>(p, m0, wave, lane, a0s, a1s);
+    for (int i = 0;; i++) {
+        if (i < n_whole)
+            consume_item<CB, EPI>(p, smem, W, m0, n0, wave, lane, a0s, a1s);
+        else
+            consume_item<CS, EPI>(p, smem, W, m0, n0, wave, lane, a0s, a1s);
+        if (i + 1 >= n_items) return;
+        W = item(i + 1, m0, n0);
+        if (i + 1 < n_whole)
+            load_item_a<CB>(p, m0, wave, lane, a0s, a1s);
+        else
+            load_item_a<CS>(p, m0, wave, lane, a0s, a1s);
+        bare_barrier();  // the epilogue is done with the LDS the producers fill next
+    }
+}
+
 // 256x128 tiles (4 consumer waves of 64x128); 128x128 (4 of 32x128) where
 // the cost model prefers them (few rows, or too few big tiles).
 #ifndef ZEST_GEMM_BIG
@@ -1046,6 +1151,20 @@ int set_lds_tiles(const char * name) {
 }
 
 template <class CB, class CS, int EPI>
+int set_lds_mixed_tiles(const char * name) {
+    static std::atomic<bool> attr_set{false};
+    if (!attr_set.load(std::memory_order_acquire)) {
+        const size_t bytes = std::max(CB::LDS_BYTES, CS::LDS_BYTES);
+        const hipError_t e =
+            hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_kernel_mixed_tiles<CB, CS, EPI>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int) bytes);
+        if (e != hipSuccess) return zest::fail(ZEST_E_HIP, "%s: LDS attribute: %s", name, hipGetErrorString(e));
+        attr_set.store(true, std::memory_order_release);
+    }
+    return ZEST_OK;
+}
+
+template <class CB, class CS, int EPI>
 int set_lds_mixed(const char * name) {
     static std::atomic<bool> attr_set{false};
     if (!attr_set.load(std::memory_order_acquire)) {
@@ -1126,19 +1245,20 @@ int launch(gemm_params p, const int64_t * N, int splits, hipStream_t s, const ch
         p.counters = sp.counters;
     }
 #if ZEST_GEMM_PERSIST
-    if (EPI != EPI_RESIDUAL && p.splits == 1 && C::MINB == 1 && p.nk % 2 == 0 && p.nk >= 4) {
-        // more than one round: persistent workgroups, one a CU (not for the
-        // residual epilogue, whose persistent form does not fit the registers)
-        int dev = 0;
-        (void) hipGetDevice(&dev);
-        const int64_t G = cu_count(dev) / 8 * 8;
-        if (G >= 8 && T > G) {
-            const int st = set_lds_tiles<C, EPI>(name);
-            if (st != ZEST_OK) return st;
-            hipLaunchKernelGGL((gemm_kernel_tiles<C, EPI>), dim3((unsigned) G), dim3(C::NT), C::LDS_BYTES, s, p);
-            return zest::check_launch(name);
+    // more than one round: persistent workgroups, one a CU (not for the
+    // residual epilogue, whose persistent form does not fit the registers)
+    if constexpr (EPI != EPI_RESIDUAL && C::MINB == 1)
+        if (p.splits == 1 && p.nk % 2 == 0 && p.nk >= 4) {
+            int dev = 0;
+            (void) hipGetDevice(&dev);
+            const int64_t G = cu_count(dev) / 8 * 8;
+            if (G >= 8 && T > G) {
+                const int st = set_lds_tiles<C, EPI>(name);
+                if (st != ZEST_OK) return st;
+                hipLaunchKernelGGL((gemm_kernel_tiles<C, EPI>), dim3((unsigned) G), dim3(C::NT), C::LDS_BYTES, s, p);
+                return zest::check_launch(name);
+            }
         }
-    }
 #endif
     const int st = p.splits > 1 ? set_lds<C, EPI, true>(name) : set_lds<C, EPI, false>(name);
     if (st != ZEST_OK) return st;
@@ -1164,6 +1284,23 @@ int launch_mixed(gemm_params p, const int64_t * N, int64_t nbig, hipStream_t s, 
         return zest::fail(ZEST_E_ARG, "%s: mixed launch of %lld tiles", name, (long long) T);
     p.splits = 1;
     p.nbig = (int) nbig;
+#if ZEST_GEMM_PERSIST
+    // persistent workgroups, one a CU (not for the residual epilogue, whose
+    // persistent form does not fit the registers)
+    if constexpr (EPI != EPI_RESIDUAL)
+        if (p.nk % 2 == 0 && p.nk >= 4) {
+            int dev = 0;
+            (void) hipGetDevice(&dev);
+            const int64_t G = std::min<int64_t>(nbig, cu_count(dev) / 8 * 8);
+            if (G >= 8) {
+                const int st = set_lds_mixed_tiles<CB, CS, EPI>(name);
+                if (st != ZEST_OK) return st;
+                hipLaunchKernelGGL((gemm_kernel_mixed_tiles<CB, CS, EPI>), dim3((unsigned) G), dim3(CB::NT),
+                                   std::max(CB::LDS_BYTES, CS::LDS_BYTES), s, p);
+                return zest::check_launch(name);
+            }
+        }
+#endif
     const int st = set_lds_mixed<CB, CS, EPI>(name);
     if (st != ZEST_OK) return st;
     hipLaunchKernelGGL((gemm_kernel_mixed<CB, CS, EPI>), dim3((unsigned) grid), dim3(CB::NT),

@@ -257,6 +257,7 @@ def test_gemm_160_row_tiles(zest_gpu, oracle, M, ns, K):
     (4000, [2048, 1024, 1024], 512),  # 16 x 32 = 512 tiles of 256 x 128: two rounds, persistent workgroups
     (2048, [4096, 4096, 4096], 1024),  # 8 x 96 = 768 tiles: three rounds
     (4000, [2048, 1024, 1024], 576),  # an odd number of K-steps: one workgroup a tile
+    (4096, [4096, 1024], 512),  # 640 tiles: two rounds and a half, the half as 128-row tiles (each workgroup two whole, one half)
 ])
 def test_gemm_rounds_equal_one_round_launches(zest_gpu, oracle, M, ns, K):
     # A launch of more than one round of whole tiles, unsplit, runs as
