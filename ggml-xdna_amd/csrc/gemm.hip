@@ -78,6 +78,10 @@ struct gemm_cfg {
     static constexpr int STAGES = 3;
     static constexpr size_t LDS_BYTES =
         (size_t) STAGES * STAGE > (size_t) BM * BN * 4 ? (size_t) STAGES * STAGE : (size_t) BM * BN * 4;
+    // a persistent launch: the GLU epilogue's staging (WM rows of 16 TJ + 4
+    // floats a wave) above the ring
+    static constexpr size_t LDS_APART = (size_t) STAGES * STAGE + (size_t) (NC / 64) * WM * (16 * TJ + 4) * 4;
+    static constexpr size_t LDS_TILES = LDS_BYTES > LDS_APART ? LDS_BYTES : LDS_APART;
     static_assert(BN * 4 % NP == 0, "work must divide evenly");
     static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be whole 32x32 MFMA tiles");
 };
@@ -318,8 +322,10 @@ __device__ inline void store_tile(const f32x16 (&acc)[C::TI][C::TJ], float * Cou
 // activation packer does (store_expanded16: two 16-byte stores). Each wave
 // has its own LDS region, so no barrier is needed: a wave's LDS operations
 // complete in order. Rows and columns past M and F come from zero padding and
-// store zeros, as the packer's padding is.
-template <class C, int KIND>
+// store zeros, as the packer's padding is. With APART the regions lie above
+// the W ring (a persistent workgroup's producers fill the next tile's first
+// stages meanwhile); else each is the wave's region of the split-K fixup.
+template <class C, int KIND, bool APART = false>
 __device__ inline void store_glu(const f32x16 (&acc)[C::TI][C::TJ], uint8_t * smem, uint8_t * xout, float * h,
                                  int64_t ldh, int64_t M, int64_t F, int64_t m0, int64_t n0, int wave, int wm, int wn,
                                  int lane, uint32_t * nonfinite) {
@@ -329,8 +335,9 @@ __device__ inline void store_glu(const f32x16 (&acc)[C::TI][C::TJ], uint8_t * sm
     // (rows r..r+15, one 16-byte column chunk) then hit distinct banks
     constexpr int P = HW + 4;
     static_assert(P <= C::WN && (size_t) C::BM * C::BN * 4 <= C::LDS_BYTES, "staging must fit the wave's region");
-    // the wave's LDS region, the one the split-K fixup uses: WM x WN floats
-    float * st = reinterpret_cast<float *>(smem + wave * (C::WM * C::WN * 4));
+    static_assert(P == 16 * C::TJ + 4 && C::LDS_APART <= C::LDS_TILES, "staging above the ring must fit");
+    float * st = reinterpret_cast<float *>(APART ? smem + C::STAGES * C::STAGE + wave * (C::WM * P * 4)
+                                                 : smem + wave * (C::WM * C::WN * 4));
     const int64_t c0 = n0 / 2 + wn * HW;
     bool bad = false;
 #pragma unroll
@@ -661,8 +668,9 @@ __device__ inline void consume_tile(f32x16 (&acc)[C::TI][C::TJ], bf16x8 (&a0s)[4
     }
 }
 
-// The consumer's epilogue of one tile.
-template <class C, int EPI>
+// The consumer's epilogue of one tile; APART as for store_glu (the plain
+// store uses no LDS).
+template <class C, int EPI, bool APART = false>
 __device__ inline void epilogue(const f32x16 (&acc)[C::TI][C::TJ], const gemm_params & p, uint8_t * smem,
                                 const gemm_weight & W, int64_t m0, int64_t n0, int wave, int wm, int wn, int lane) {
     if constexpr (EPI == EPI_RESIDUAL)
@@ -670,7 +678,8 @@ __device__ inline void epilogue(const f32x16 (&acc)[C::TI][C::TJ], const gemm_pa
     else if constexpr (EPI < 0)
         store_tile<C>(acc, W.c, p.M, W.n, W.ldc, m0, n0, wm, wn, lane, p.nonfinite);
     else
-        store_glu<C, EPI>(acc, smem, p.xout, p.h, p.ldh, p.M, W.n / 2, m0, n0, wave, wm, wn, lane, p.nonfinite);
+        store_glu<C, EPI, APART>(acc, smem, p.xout, p.h, p.ldh, p.M, W.n / 2, m0, n0, wave, wm, wn, lane,
+                                 p.nonfinite);
 }
 
 // Tile t of a launch in the tile order: tiles go in groups of GROUP_M tile
@@ -795,14 +804,17 @@ __global__ __launch_bounds__(CB::NT, 1) void gemm_kernel_mixed(const gemm_params
 }
 
 // Persistent workgroups for a launch of more than one round of whole tiles
-// (ns = nk, even, at least 4). Workgroup b works on XCD b % 8 and takes the
-// tiles of that XCD's run (the contiguous run xcd_order gives it) in turn:
-// start + b/8, start + b/8 + G/8, ... for G workgroups, a multiple of 8. The
-// producers' last two requests of a tile fetch the next tile's first two W
-// steps, so its first stages are stored without waiting for memory; the
-// consumers request the next tile's first two A steps after the epilogue
-// (held through it they would not fit the registers), and a barrier keeps the
-// producers' stores out of the LDS the epilogue uses.
+// (ns = nk, even, at least 4; not the residual epilogue). Workgroup b works on
+// XCD b % 8 and takes the tiles of that XCD's run (the contiguous run
+// xcd_order gives it) in turn: start + b/8, start + b/8 + G/8, ... for G
+// workgroups, a multiple of 8. The producers' last two requests of a tile
+// fetch the next tile's first two W steps, and once past the tile's last
+// barrier they expand and store them into the first two stages while the
+// consumers run the epilogue (which uses no LDS, or the GLU's staging above
+// the ring; the only LDS read a consumer still has in flight there is its
+// unused read ahead of a next stage). The consumers request the next tile's
+// first two A steps after the epilogue (held through it they would not fit
+// the registers).
 template <class C, int EPI>
 __global__ __launch_bounds__(C::NT, 1) void gemm_kernel_tiles(const gemm_params p) {
     extern __shared__ uint4 smem_u4[];
@@ -830,7 +842,6 @@ __global__ __launch_bounds__(C::NT, 1) void gemm_kernel_tiles(const gemm_params 
             const int wn0 = __builtin_amdgcn_readfirstlane((int) ((nn / ZEST_TILE_ROWS) * ZEST_TILE_BYTES));
             produce_tile<C>(pr, smem, w0, W.w_kstride, nk, nk - 1, r0, r1, pn, wn0, Wn.w_kstride, next);
             if (!next) return;
-            bare_barrier();  // the consumers' epilogue is done with the LDS
             t = tn;
             W = Wn;
             pr = pn;
@@ -856,20 +867,19 @@ __global__ __launch_bounds__(C::NT, 1) void gemm_kernel_tiles(const gemm_params 
         consume_tile<C, false>(acc, a0s, a1s, smem, fw, al, a0, ks, nk, nk - 1, 0);
         // the loads of steps past the end are still in flight
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-        epilogue<C, EPI>(acc, p, smem, W, m0, n0, wave, wm, wn, lane);
+        epilogue<C, EPI, true>(acc, p, smem, W, m0, n0, wave, wm, wn, lane);
         t += g;
         if (t >= end) return;
         W = tile_of<C>(p, t, m0, n0);
         a0 = __builtin_amdgcn_readfirstlane((int) ((m0 / ZEST_XGROUP_ROWS) * ZEST_XGROUP_BYTES));
         al.load_step(a0s, a0);
         al.load_step(a1s, a0 + ks);
-        bare_barrier();  // the epilogue is done with the LDS the producers fill next
     }
 }
 
 // One item of a persistent mixed launch, a consumer wave's part: the K loop
 // of a tile (its A fragments of steps 0 and 1 requested into a0s and a1s),
-// then its epilogue.
+// then its epilogue (with no LDS of its own).
 template <class C, int EPI>
 __device__ inline void consume_item(const gemm_params & p, uint8_t * smem, const gemm_weight & W, int64_t m0,
                                     int64_t n0, int wave, int lane, bf16x8 (&a0s)[4][C::TI],
@@ -888,6 +898,7 @@ __device__ inline void consume_item(const gemm_params & p, uint8_t * smem, const
     consume_tile<C, false>(acc, a0s, a1s, smem, fw, al, a0, p.a_kstride, p.nk, p.nk - 1, 0);
     // the loads of steps past the end are still in flight
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    static_assert(EPI < 0 && EPI != EPI_RESIDUAL, "the plain store");
     epilogue<C, EPI>(acc, p, smem, W, m0, n0, wave, wm, wn, lane);
 }
 
@@ -907,8 +918,9 @@ __device__ inline void load_item_a(const gemm_params & p, int64_t m0, int wave, 
 // the half tiles of that XCD's run of halves, from b/8 in steps of G/8 (G
 // workgroups, a multiple of 8, at most nbig). The producers request the next
 // item's first two W steps during the current item's last ones (a half tile
-// has its whole tile's W rows and the same producer layout); the consumers
-// request its first two A steps after their epilogue.
+// has its whole tile's W rows and the same producer layout) and store them
+// into the first two stages while the consumers run the epilogue (the plain
+// store, no LDS); the consumers request its first two A steps after it.
 template <class CB, class CS, int EPI>
 __global__ __launch_bounds__(CB::NT, 1) void gemm_kernel_mixed_tiles(const gemm_params p) {
     static_assert(CB::NT == CS::NT && CS::BM * 2 == CB::BM && CS::BN == CB::BN && CS::NP == CB::NP &&
@@ -948,7 +960,6 @@ __global__ __launch_bounds__(CB::NT, 1) void gemm_kernel_mixed_tiles(const gemm_
             const int wn0 = __builtin_amdgcn_readfirstlane((int) ((nn / ZEST_TILE_ROWS) * ZEST_TILE_BYTES));
             produce_tile<CB>(pr, smem, w0, W.w_kstride, nk, nk - 1, r0, r1, pn, wn0, Wn.w_kstride, next);
             if (!next) return;
-            bare_barrier();  // the consumers' epilogue is done with the LDS
             W = Wn;
             pr = pn;
             w0 = wn0;
@@ -967,7 +978,6 @@ __global__ __launch_bounds__(CB::NT, 1) void gemm_kernel_mixed_tiles(const gemm_
             load_item_a<CB>(p, m0, wave, lane, a0s, a1s);
         else
             load_item_a<CS>(p, m0, wave, lane, a0s, a1s);
-        bare_barrier();  // the epilogue is done with the LDS the producers fill next
     }
 }
 
@@ -1143,7 +1153,7 @@ int set_lds_tiles(const char * name) {
     static std::atomic<bool> attr_set{false};
     if (!attr_set.load(std::memory_order_acquire)) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_kernel_tiles<C, EPI>),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int) C::LDS_BYTES);
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int) C::LDS_TILES);
         if (e != hipSuccess) return zest::fail(ZEST_E_HIP, "%s: LDS attribute: %s", name, hipGetErrorString(e));
         attr_set.store(true, std::memory_order_release);
     }
@@ -1255,7 +1265,7 @@ int launch(gemm_params p, const int64_t * N, int splits, hipStream_t s, const ch
             if (G >= 8 && T > G) {
                 const int st = set_lds_tiles<C, EPI>(name);
                 if (st != ZEST_OK) return st;
-                hipLaunchKernelGGL((gemm_kernel_tiles<C, EPI>), dim3((unsigned) G), dim3(C::NT), C::LDS_BYTES, s, p);
+                hipLaunchKernelGGL((gemm_kernel_tiles<C, EPI>), dim3((unsigned) G), dim3(C::NT), C::LDS_TILES, s, p);
                 return zest::check_launch(name);
             }
         }
