@@ -637,13 +637,11 @@ __device__ inline void produce(const producer<C> & pr, uint8_t * smem, int w0, i
 // steps 0 and 1 requested into a0s and a1s: starts with the barrier that
 // completes the first two W stages. Past the tile's last step, a load of
 // step j reads step min(j, last) (the next split's slab or the operand's
-// last step again, never used); with NEXT, step ns + j of the tile reads step
-// j of the workgroup's next tile at an (which then start the next call in a0s
-// and a1s: ns is even). Pairs of steps run without conditions.
-template <class C, bool NEXT>
+// last step again, never used). Pairs of steps run without conditions.
+template <class C>
 __device__ inline void consume_tile(f32x16 (&acc)[C::TI][C::TJ], bf16x8 (&a0s)[4][C::TI], bf16x8 (&a1s)[4][C::TI],
                                     const uint8_t * smem, const int (&fw)[4], const a_loader<C> & al, int a0, int ks,
-                                    int ns, int last, int an) {
+                                    int ns, int last) {
     bf16x8 bw[2][C::TJ];
     bare_barrier();
 #pragma unroll
@@ -651,13 +649,11 @@ __device__ inline void consume_tile(f32x16 (&acc)[C::TI][C::TJ], bf16x8 (&a0s)[4
     int cur = 0, k = 0;
     for (; k + 1 < ns; k += 2) {
         int nxt = cur == 2 * C::STAGE ? 0 : cur + C::STAGE;
-        consume<C, true>(acc, a0s, bw, smem, fw, cur, nxt, al,
-                         NEXT ? (k + 2 < ns ? a0 + (k + 2) * ks : an + (k + 2 - ns) * ks) : a0 + min(k + 2, last) * ks);
+        consume<C, true>(acc, a0s, bw, smem, fw, cur, nxt, al, a0 + min(k + 2, last) * ks);
         cur = nxt;
         bare_barrier();
         nxt = cur == 2 * C::STAGE ? 0 : cur + C::STAGE;
-        consume<C, true>(acc, a1s, bw, smem, fw, cur, nxt, al,
-                         NEXT ? (k + 3 < ns ? a0 + (k + 3) * ks : an + (k + 3 - ns) * ks) : a0 + min(k + 3, last) * ks);
+        consume<C, true>(acc, a1s, bw, smem, fw, cur, nxt, al, a0 + min(k + 3, last) * ks);
         cur = nxt;
         bare_barrier();
     }
@@ -754,7 +750,7 @@ __device__ inline void run_tile(const gemm_params & p, uint8_t * smem, const gem
         bf16x8 a0s[4][C::TI], a1s[4][C::TI];
         al.load_step(a0s, a0);
         al.load_step(a1s, a0 + min(1, last) * ks);
-        consume_tile<C, false>(acc, a0s, a1s, smem, fw, al, a0, ks, ns, last, 0);
+        consume_tile<C>(acc, a0s, a1s, smem, fw, al, a0, ks, ns, last);
         // the loads of steps past the end are still in flight
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     }
@@ -864,7 +860,7 @@ __global__ __launch_bounds__(C::NT, 1) void gemm_kernel_tiles(const gemm_params 
         for (int i = 0; i < C::TI; i++)
 #pragma unroll
             for (int j = 0; j < C::TJ; j++) acc[i][j] = f32x16{};
-        consume_tile<C, false>(acc, a0s, a1s, smem, fw, al, a0, ks, nk, nk - 1, 0);
+        consume_tile<C>(acc, a0s, a1s, smem, fw, al, a0, ks, nk, nk - 1);
         // the loads of steps past the end are still in flight
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
         epilogue<C, EPI, true>(acc, p, smem, W, m0, n0, wave, wm, wn, lane);
@@ -895,7 +891,7 @@ __device__ inline void consume_item(const gemm_params & p, uint8_t * smem, const
     for (int i = 0; i < C::TI; i++)
 #pragma unroll
         for (int j = 0; j < C::TJ; j++) acc[i][j] = f32x16{};
-    consume_tile<C, false>(acc, a0s, a1s, smem, fw, al, a0, p.a_kstride, p.nk, p.nk - 1, 0);
+    consume_tile<C>(acc, a0s, a1s, smem, fw, al, a0, p.a_kstride, p.nk, p.nk - 1);
     // the loads of steps past the end are still in flight
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     static_assert(EPI < 0 && EPI != EPI_RESIDUAL, "the plain store");
