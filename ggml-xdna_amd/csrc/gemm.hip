@@ -64,15 +64,16 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // default). LDS holds the expanded W ring; after the K loop each consumer
 // wave uses WM x WN floats of it for its epilogue. MINB workgroups a CU at
 // least (the launch bound).
-template <int BM_, int BN_, int CWM_, int NP_ = 64 * CWM_, int MINB_ = 1, int CWN_ = 1>
+template <int BM_, int BN_, int CWM_, int NP_ = 64 * CWM_, int MINB_ = 1, int CWN_ = 1, int NP1_ = 0>
 struct gemm_cfg {
     static constexpr int BM = BM_, BN = BN_, CWM = CWM_, CWN = CWN_, MINB = MINB_;
     static constexpr int NC = 64 * CWM * CWN;  // consumer threads
     static constexpr int NP = NP_;             // producer threads
+    static constexpr int NP1 = NP1_;           // of them, the last NP1 take one W unit each, not two
     static constexpr int NT = NC + NP;
     static constexpr int WM = BM / CWM, WN = BN / CWN;
     static constexpr int TI = WM / 32, TJ = WN / 32;
-    static constexpr int BU = BN * 4 / NP;  // W units (two blocks) per producer thread per K-step
+    static constexpr int NP2 = NP - NP1;    // producer threads of two W units (two blocks each) a K-step
     static constexpr int ROWB = 128;        // LDS bytes per row (64 bf16)
     static constexpr int STAGE = BN * ROWB;
     static constexpr int STAGES = 3;
@@ -82,7 +83,8 @@ struct gemm_cfg {
     // floats a wave) above the ring
     static constexpr size_t LDS_APART = (size_t) STAGES * STAGE + (size_t) (NC / 64) * WM * (16 * TJ + 4) * 4;
     static constexpr size_t LDS_TILES = LDS_BYTES > LDS_APART ? LDS_BYTES : LDS_APART;
-    static_assert(BN * 4 % NP == 0, "work must divide evenly");
+    static_assert(NP2 % 64 == 0 && NP1 % 64 == 0 && NP2 / 32 + NP1 / 64 == BN / 16,
+                  "32 two-unit or 64 one-unit producer threads a 16-row W tile, whole waves of each");
     static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be whole 32x32 MFMA tiles");
 };
 
@@ -104,11 +106,11 @@ __device__ inline uint4 load16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
-// A producer thread's registers for one K-step's W units.
-template <class C>
+// A producer thread's registers for one K-step's U W units.
+template <class C, int U = 2>
 struct stage_regs {
-    uint4 wm[C::BU];
-    uint32_t we;  // both units' exponent bytes: unit 0 in bits 0-15, unit 1 in bits 16-31
+    uint4 wm[U];
+    uint32_t we;  // the units' exponent bytes: unit 0 in bits 0-15, unit 1 in bits 16-31
 };
 
 typedef __attribute__((address_space(3))) void * lds_ptr_t;
@@ -117,40 +119,48 @@ typedef __attribute__((address_space(3))) void * lds_ptr_t;
 // offset is wave-uniform (a scalar offset), the lane's place in it a fixed
 // vector offset. The hardware range check covers the vector offset only, so
 // every slab offset a load is given names a K-step of the operand (callers
-// clamp the steps past the end to the last one). Thread p takes
+// clamp the steps past the end to the last one). With U = 2, thread p takes
 // two adjacent units of tile p/32 of the W slab: row p%16, column quarters 2h
 // and 2h+1 with h = p/16%2, i.e. 32 contiguous mantissa bytes (two 16-byte
-// loads) and 4 contiguous exponent bytes (one 4-byte load). 16 consecutive
-// lanes are 16 consecutive rows, for the swizzled stores.
-template <class C>
+// loads) and 4 contiguous exponent bytes (one 4-byte load). With U = 1 (the
+// slab's last tiles, after the NP2/32 of the two-unit threads), thread p
+// takes one unit of tile NP2/32 + p/64: row p%16, quarter q = p/16%4 (16
+// mantissa bytes, 2 exponent bytes). 16 consecutive lanes are 16 consecutive
+// rows, for the swizzled stores.
+template <class C, int U = 2>
 struct producer {
-    static_assert(C::BU == 2 && C::NP / 32 == C::BN / 16, "two W units per producer thread, 32 threads a tile");
+    static_assert(U == 1 || U == 2, "one or two W units a thread");
     __amdgpu_buffer_rsrc_t rw;
     int vwm, vwe;          // lane offsets: W mantissas, W exponents
-    int stw[2][2];         // LDS offsets of the two W units' two chunks each
+    int stw[U][2];         // LDS offsets of the W units' two chunks each
 
     __device__ producer(const uint8_t * W, int64_t w_bytes, int p) {
         rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(W), (short) 0, (int) w_bytes, 0x00020000);
-        const int t = p >> 5, row = p & 15, h = (p >> 4) & 1;
-        vwm = t * ZEST_TILE_BYTES + row * ZEST_TILE_K + h * 32;
-        vwe = t * ZEST_TILE_BYTES + ZEST_TILE_MANT + row * 8 + h * 4;
+        const int t = U == 2 ? p >> 5 : C::NP2 / 32 + (p >> 6), row = p & 15;
+        const int q0 = U == 2 ? 2 * ((p >> 4) & 1) : (p >> 4) & 3;  // the first unit's quarter
+        vwm = t * ZEST_TILE_BYTES + row * ZEST_TILE_K + q0 * 16;
+        vwe = t * ZEST_TILE_BYTES + ZEST_TILE_MANT + row * 8 + q0 * 2;
         const int wrow = t * 16 + row, sw = swz(wrow);
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            stw[i][0] = wrow * C::ROWB + ((4 * h + 2 * i) ^ sw) * 16;
-            stw[i][1] = wrow * C::ROWB + ((4 * h + 2 * i + 1) ^ sw) * 16;
+        for (int i = 0; i < U; i++) {
+            stw[i][0] = wrow * C::ROWB + ((2 * (q0 + i)) ^ sw) * 16;
+            stw[i][1] = wrow * C::ROWB + ((2 * (q0 + i) + 1) ^ sw) * 16;
         }
     }
 
-    __device__ void load_w(stage_regs<C> & st, int w_off) const {
+    __device__ void load_w(stage_regs<C, U> & st, int w_off) const {
         st.wm[0] = load16(rw, vwm, w_off);
-        st.wm[1] = load16(rw, vwm + 16, w_off);
-        st.we = __builtin_amdgcn_raw_buffer_load_b32(rw, vwe, w_off, 0);
+        if constexpr (U == 2) {
+            st.wm[1] = load16(rw, vwm + 16, w_off);
+            st.we = __builtin_amdgcn_raw_buffer_load_b32(rw, vwe, w_off, 0);
+        } else {
+            st.we = __builtin_amdgcn_raw_buffer_load_b16(rw, vwe, w_off, 0);
+        }
     }
 
     // W unit i of a step, by the branch-free fast expansion, stored; true if
     // the unit needs the general expansion (store_w_general) instead.
-    __device__ bool store_w_unit(const stage_regs<C> & st, int i, uint8_t * smem, int stage) const {
+    __device__ bool store_w_unit(const stage_regs<C, U> & st, int i, uint8_t * smem, int stage) const {
         uint32_t b[8];
         const bool slow = zest::expand16_fast(st.wm[i], i ? st.we >> 16 : st.we & 0xffffu, b);
         lds_put(smem, stw[i][0] + stage, make_uint4(b[0], b[1], b[2], b[3]));
@@ -159,9 +169,9 @@ struct producer {
     }
 
     // Every unit of the step by the general expansion, stored.
-    __device__ void store_w_general(const stage_regs<C> & st, uint8_t * smem, int stage) const {
+    __device__ void store_w_general(const stage_regs<C, U> & st, uint8_t * smem, int stage) const {
 #pragma unroll
-        for (int i = 0; i < C::BU; i++) {
+        for (int i = 0; i < U; i++) {
             uint32_t b[8];
             zest::expand16(st.wm[i], i ? st.we >> 16 : st.we & 0xffffu, b);
             lds_put(smem, stw[i][0] + stage, make_uint4(b[0], b[1], b[2], b[3]));
@@ -172,10 +182,10 @@ struct producer {
     // The units take the branch-free fast expansion; a unit whose exponent
     // bytes need the general one is redone behind a single wave-uniform
     // branch, which real weights almost never take.
-    __device__ void store_w(const stage_regs<C> & st, uint8_t * smem, int stage) const {
+    __device__ void store_w(const stage_regs<C, U> & st, uint8_t * smem, int stage) const {
         bool slow = false;
 #pragma unroll
-        for (int i = 0; i < C::BU; i++) slow |= store_w_unit(st, i, smem, stage);
+        for (int i = 0; i < U; i++) slow |= store_w_unit(st, i, smem, stage);
         if (__builtin_expect(__any(slow), 0)) store_w_general(st, smem, stage);
     }
 };
@@ -546,12 +556,12 @@ __device__ inline void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 // expanded and stored into `stage`, step j+2's requested into the same
 // registers. A unit whose exponent bytes need the general expansion is
 // redone behind one wave-uniform branch, which real weights almost never take.
-template <class C>
-__device__ inline void produce_step(const producer<C> & pr, uint8_t * smem, int stage, stage_regs<C> & r,
+template <class C, int U>
+__device__ inline void produce_step(const producer<C, U> & pr, uint8_t * smem, int stage, stage_regs<C, U> & r,
                                    int w_off_next) {
     bool slow = false;
 #pragma unroll
-    for (int u = 0; u < C::BU; u++) {
+    for (int u = 0; u < U; u++) {
         slow |= pr.store_w_unit(r, u, smem, stage);
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -576,10 +586,10 @@ __device__ inline void produce_step(const producer<C> & pr, uint8_t * smem, int 
 // last step fetch steps 0 and 1 of the workgroup's next tile (producer pn, at
 // wn0) into r0 and r1 instead. The barriers match the consumers', step for
 // step.
-template <class C>
-__device__ inline void produce_tile(const producer<C> & pr, uint8_t * smem, int w0, int w_kstride, int ns, int last,
-                                    stage_regs<C> & r0, stage_regs<C> & r1, const producer<C> & pn, int wn0,
-                                    int wn_kstride, bool next) {
+template <class C, int U = 2>
+__device__ inline void produce_tile(const producer<C, U> & pr, uint8_t * smem, int w0, int w_kstride, int ns,
+                                    int last, stage_regs<C, U> & r0, stage_regs<C, U> & r1, const producer<C, U> & pn,
+                                    int wn0, int wn_kstride, bool next) {
     pr.store_w(r0, smem, 0);
     pr.load_w(r0, w0 + min(2, last) * w_kstride);
     if (ns > 1) pr.store_w(r1, smem, C::STAGE);
@@ -589,11 +599,11 @@ __device__ inline void produce_tile(const producer<C> & pr, uint8_t * smem, int 
     // during step k: step k+2 stored into stage (k+2)%3, step k+4 requested
     int stage = 2 * C::STAGE, k = 0;
     for (; k + 5 < ns; k += 2) {
-        produce_step<C>(pr, smem, stage, r0, w0 + (k + 4) * w_kstride);
+        produce_step<C, U>(pr, smem, stage, r0, w0 + (k + 4) * w_kstride);
         stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
         wait_lgkm0();
         bare_barrier();
-        produce_step<C>(pr, smem, stage, r1, w0 + (k + 5) * w_kstride);
+        produce_step<C, U>(pr, smem, stage, r1, w0 + (k + 5) * w_kstride);
         stage = stage == 2 * C::STAGE ? 0 : stage + C::STAGE;
         wait_lgkm0();
         bare_barrier();
@@ -625,12 +635,12 @@ __device__ inline void produce_tile(const producer<C> & pr, uint8_t * smem, int 
 }
 
 // The producer's part of a workgroup's only tile.
-template <class C>
-__device__ inline void produce(const producer<C> & pr, uint8_t * smem, int w0, int w_kstride, int ns, int last) {
-    stage_regs<C> r0, r1;
+template <class C, int U>
+__device__ inline void produce(const producer<C, U> & pr, uint8_t * smem, int w0, int w_kstride, int ns, int last) {
+    stage_regs<C, U> r0, r1;
     pr.load_w(r0, w0);
     pr.load_w(r1, w0 + min(1, last) * w_kstride);
-    produce_tile<C>(pr, smem, w0, w_kstride, ns, last, r0, r1, pr, 0, 0, false);
+    produce_tile<C, U>(pr, smem, w0, w_kstride, ns, last, r0, r1, pr, 0, 0, false);
 }
 
 // The consumer's K loop over a tile's steps [0, ns), its A fragments of
@@ -717,12 +727,19 @@ __device__ inline void run_tile(const gemm_params & p, uint8_t * smem, const gem
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nk = p.nk;
     if (wave >= C::NC / 64) {
-        const producer<C> pr(W.w, (int64_t) W.w_kstride * nk, tid - C::NC);
+        const int job = tid - C::NC;
         // uniform, but the tile arithmetic can leave it in a vector register,
         // and a load's scalar offset taken from one costs a loop per load
         const int w0 =
             __builtin_amdgcn_readfirstlane((int) ((n0 / ZEST_TILE_ROWS) * ZEST_TILE_BYTES) + k0 * W.w_kstride);
-        produce<C>(pr, smem, w0, W.w_kstride, ns, nk - 1 - k0);
+        if constexpr (C::NP1 > 0)
+            if (job >= C::NP2) {  // whole waves: NP2 % 64 == 0
+                const producer<C, 1> pr(W.w, (int64_t) W.w_kstride * nk, job - C::NP2);
+                produce<C, 1>(pr, smem, w0, W.w_kstride, ns, nk - 1 - k0);
+                return;
+            }
+        const producer<C, 2> pr(W.w, (int64_t) W.w_kstride * nk, job);
+        produce<C, 2>(pr, smem, w0, W.w_kstride, ns, nk - 1 - k0);
         return;
     }
 
@@ -920,7 +937,7 @@ __device__ inline void load_item_a(const gemm_params & p, int64_t m0, int wave, 
 template <class CB, class CS, int EPI>
 __global__ __launch_bounds__(CB::NT, 1) void gemm_kernel_mixed_tiles(const gemm_params p) {
     static_assert(CB::NT == CS::NT && CS::BM * 2 == CB::BM && CS::BN == CB::BN && CS::NP == CB::NP &&
-                      CS::TI == CB::TI,
+                      CS::TI == CB::TI && CB::NP1 == 0 && CS::NP1 == 0,
                   "halves of the big tiles, with the same producers");
     extern __shared__ uint4 smem_u4[];
     uint8_t * smem = reinterpret_cast<uint8_t *>(smem_u4);
@@ -1032,15 +1049,18 @@ __global__ __launch_bounds__(CB::NT, 1) void gemm_kernel_mixed_tiles(const gemm_
 #ifndef ZEST_GEMM_GLU
 #define ZEST_GEMM_GLU 256, 128, 8, 256
 #endif
-// 128x160 tiles (4 consumer waves of 32x160, 5 producer waves) for a launch
-// that 256x128 tiles would run in one round, unsplit, when its weights are
-// whole 160-row tiles and these fit one round too: the O projection at 2048
-// tokens (2048 x 2560) is 256 of them, one per CU, where 160 256x128 tiles
-// leave 96 CUs idle (55.5 -> ~49 us). A split launch keeps its plan: the
-// down projection (K 9728) as 256 of these unsplit takes ~115 us against
-// 107 us in three splits.
+// 128x160 tiles (4 consumer waves of 32x160) for a launch that 256x128 tiles
+// would run in one round, unsplit, when its weights are whole 160-row tiles
+// and these fit one round too: the O projection at 2048 tokens (2048 x 2560)
+// is 256 of them, one per CU, where 160 256x128 tiles leave 96 CUs idle
+// (55.5 -> ~49 us). The producers are this launch's critical path: four
+// waves take two W units a thread (tiles 0-7) and two waves one (tiles 8-9),
+// so the two SIMDs that hold a second producer wave carry one and a half
+// waves' expansion, not two (five waves of two units: 52.5 -> 48.6 us). A
+// split launch keeps its plan: the down projection (K 9728) as 256 of these
+// unsplit takes ~115 us against 107 us in three splits.
 #ifndef ZEST_GEMM_O
-#define ZEST_GEMM_O 128, 160, 4, 320
+#define ZEST_GEMM_O 128, 160, 4, 384, 1, 1, 128
 #endif
 using cfg_big = gemm_cfg<ZEST_GEMM_BIG>;
 using cfg_o = gemm_cfg<ZEST_GEMM_O>;
@@ -1253,7 +1273,7 @@ int launch(gemm_params p, const int64_t * N, int splits, hipStream_t s, const ch
 #if ZEST_GEMM_PERSIST
     // more than one round: persistent workgroups, one a CU (not for the
     // residual epilogue, whose persistent form does not fit the registers)
-    if constexpr (EPI != EPI_RESIDUAL && C::MINB == 1)
+    if constexpr (EPI != EPI_RESIDUAL && C::MINB == 1 && C::NP1 == 0)
         if (p.splits == 1 && p.nk % 2 == 0 && p.nk >= 4) {
             int dev = 0;
             (void) hipGetDevice(&dev);
