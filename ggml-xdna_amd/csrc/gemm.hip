@@ -1056,9 +1056,10 @@ __global__ __launch_bounds__(CB::NT, 1) void gemm_kernel_mixed_tiles(const gemm_
 // (55.5 -> ~49 us). The producers are this launch's critical path: four
 // waves take two W units a thread (tiles 0-7) and two waves one (tiles 8-9),
 // so the two SIMDs that hold a second producer wave carry one and a half
-// waves' expansion, not two (five waves of two units: 52.5 -> 48.6 us). A
-// split launch keeps its plan: the down projection (K 9728) as 256 of these
-// unsplit takes ~115 us against 107 us in three splits.
+// waves' expansion, not two (five waves of two units: 52.5 -> 48.6 us).
+// Launches with long K take them unsplit too when they fill more than half
+// the GPU (launch_any): the down projection (K 9728) at 2048 tokens, 96 us
+// against 104.5 us in three splits of 256x128 tiles.
 #ifndef ZEST_GEMM_O
 #define ZEST_GEMM_O 128, 160, 4, 384, 1, 1, 128
 #endif
@@ -1347,6 +1348,17 @@ int launch_any(gemm_params p, const int64_t * N, hipStream_t s, const char * nam
         plan_splits(tiles_of(p, N, CB::BM, CB::BN), p.nk, P, (double) CB::BM * CB::BN * 4, 1.0);
     const gemm_plan small = plan_splits(tiles_of(p, N, cfg_small::BM, cfg_small::BN), p.nk, P,
                                         (double) cfg_small::BM * cfg_small::BN * 4, ZEST_GEMM_SMALL_STEP);
+    if constexpr (EPI < 0) {
+        // one round of 128x160 tiles, unsplit, when every weight is whole
+        // 160-row tiles, they fill more than half the GPU and K is long enough
+        // for the prologue not to matter: no split-K fixup traffic, and the
+        // tile's producers keep up with its consumers (the down projection at
+        // 2048 tokens, K 9728: 104.5 us in three splits, 96 us so)
+        bool whole = true;
+        for (int i = 0; i < p.nw; i++) whole &= N[i] % cfg_o::BN == 0;
+        const int64_t To = tiles_of(p, N, cfg_o::BM, cfg_o::BN);
+        if (whole && To <= P && 2 * To > P && p.nk >= 16) return launch<cfg_o, EPI>(p, N, 1, s, name, fixed);
+    }
     if constexpr (EPI < 0) {
         // mixed: whole rounds of big tiles, the part-round left as half tiles
         const int64_t Tb = tiles_of(p, N, cfg_big::BM, cfg_big::BN), R = Tb / P, rem = Tb - R * P;

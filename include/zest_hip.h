@@ -186,7 +186,10 @@ ZEST_API int zest_convert_weight_gu(int type, const void *gate, const void *up, 
  * matmul's operand (xout, as zest_pack_act_x writes it, zest_act_bytes(M, F)
  * bytes) and/or as fp32 rows (h, row stride ldh floats); either may be NULL,
  * not both. h is bit-exact with zest_glu over the gate and up columns of
- * zest_gemm(a, w_gu) (2F columns, the same summation order), and xout with
+ * zest_gemm(a, w_gu) (2F columns, the same summation order) whenever that
+ * launch splits K as this one does: always, except where zest_gemm takes
+ * one unsplit round of 160-row tiles (2F a multiple of 160), which this
+ * launch cannot (a tile would split a gate/up pair); and xout with
  * zest_pack_act_x of that. `nonfinite` as for zest_gemm, over g, u and h.
  * F % 32 == 0.
  * Replaces the reference's fused SwiGLU matmul: find_fusions

@@ -163,7 +163,7 @@ def test_split_k_deterministic_and_reusable(zest_gpu, oracle):
     # must leave the per-tile counters at zero for the next: three rounds
     # over three such shapes give the same bits every time.
     import torch
-    shapes = [(2048, 2560, 9728), (1024, 2560, 16384), (600, 1000, 8192)]
+    shapes = [(2048, 2048, 9728), (1024, 2560, 16384), (600, 1000, 8192)]
     runs = {}
     for (M, N, K) in shapes:
         x = Rng(M + 7).normal(M * K).reshape(M, K)
@@ -219,6 +219,7 @@ def test_gemm_group(zest_gpu, oracle, M, K, ns, wtype):
     (2000, [2560], 4096),         # config 3's O projection with ragged rows: 256 tiles of 128 x 160
     (1024, [5120], 1024),
     (1500, [1600, 1760], 1024),   # a group of two weights, 252 tiles
+    (2048, [2560], 9728),         # config 3's down projection: one unsplit round, not three K splits
 ])
 def test_gemm_160_row_tiles(zest_gpu, oracle, M, ns, K):
     # a launch that 256 x 128 tiles run in one round, unsplit, while 128 x 128
@@ -321,7 +322,7 @@ def test_gemm_group_rejects_bad_counts(zest_gpu):
 
 @pytest.mark.parametrize("M,N,K", [
     (2048, 2560, 4096),   # config 3's O projection: h += O
-    (2048, 2560, 9728),   # its down projection (split K)
+    (2048, 2560, 9728),   # its down projection (one round of 128 x 160 tiles)
     (300, 200, 256),      # ragged rows, 128x128 tiles
     (1024, 1000, 512),    # a width that is not a tile multiple
     (2048, 6144, 512),    # 384 tiles: a round and a half, the half as 128-row tiles

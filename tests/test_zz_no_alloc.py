@@ -32,9 +32,10 @@ def _case(z, M, ns, K, seed):
 def test_noalloc_matches_gemm_group(zest_gpu, oracle):
     import torch
     z = zest_gpu
-    # config 3's down projection (160 tiles: its plan splits K three ways,
-    # 60 MiB of partial sums), then a smaller split-K group of two weights
-    cases = [(2048, [2560], 9728, 5), (600, [1000, 520], 8192, 9)]
+    # a down projection's shape whose weight is not whole 160-row tiles (152
+    # tiles of 256 x 128: its plan splits K three ways, 57 MiB of partial
+    # sums), then a smaller split-K group of two weights
+    cases = [(2048, [2432], 9728, 5), (600, [1000, 520], 8192, 9)]
     prepared = [(M, ns, K, *_case(z, M, ns, K, seed)) for M, ns, K, seed in cases]
     wants = []
     for M, ns, K, a, ws in prepared:
