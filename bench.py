@@ -299,10 +299,13 @@ def traffic_summary(fetch_dir: str, write_dir: str) -> int:
 
 
 # The stack's GEMM launch kinds, told apart by the kernel's template arguments
-# (demangled names): the q/k/v group runs as a mixed launch, O as a residual
-# launch, gate/up as the fused GLU launch (epilogue kind 2, SwiGLU; persistent
-# workgroups when it takes more than one round), down as a split-K residual
-# launch.
+# (demangled names) and their order: the q/k/v group runs as a mixed launch,
+# gate/up as the fused GLU launch (epilogue kind 2, SwiGLU; persistent
+# workgroups when it takes more than one round), O and down as residual
+# launches. Down runs as one unsplit round of 128x160 tiles at 2048 tokens,
+# the same kernel as O, so there the unsplit residual launches alternate O,
+# down, O, ... in the order they were made; where down splits K it is the
+# split residual launch and every unsplit one is O.
 def gemm_kind(name: str):
     if "gemm_kernel_mixed" in name:
         return "qkv"
@@ -313,10 +316,23 @@ def gemm_kind(name: str):
     if ", -2, true>" in name:
         return "down"
     if ", -2, false>" in name:
-        return "o"
+        return "residual"
     if ", 2, false>" in name or ", 2, true>" in name:
         return "gate_up"
     return "other"
+
+
+def gemm_kinds(names) -> list:
+    """gemm_kind of each kernel name, in dispatch order, with the unsplit
+    residual launches resolved into O and down."""
+    kinds = [gemm_kind(n) for n in names]
+    split_down = "down" in kinds
+    r = 0
+    for i, k in enumerate(kinds):
+        if k == "residual":
+            kinds[i] = "o" if split_down or r % 2 == 0 else "down"
+            r += 1
+    return kinds
 
 
 def kind_flops(cfg, m: int) -> dict:
@@ -344,17 +360,19 @@ def counter_summary(args) -> int:
     for d in (mfma_dir, fetch_dir, write_dir):
         per = defaultdict(float)
         for r in _counter_rows(d):
-            per[(r["Dispatch_Id"], r["Kernel_Name"], r["Counter_Name"])] += float(r["Counter_Value"])
-        for (_, name, counter), v in per.items():
-            k = gemm_kind(name)
+            per[(int(r["Dispatch_Id"]), r["Kernel_Name"], r["Counter_Name"])] += float(r["Counter_Value"])
+        dispatches = sorted({(di, name) for di, name, _ in per})
+        kind_of = dict(zip(dispatches, gemm_kinds([name for _, name in dispatches])))
+        for (di, name, counter), v in per.items():
+            k = kind_of[(di, name)]
             if k:
                 sums[k][counter].append(v)
             elif "scale_kernel" in name:
                 calib[counter].append(v)
     durs = defaultdict(list)
     for f in glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True):
-        for r in csv.DictReader(open(f)):
-            k = gemm_kind(r["Kernel_Name"])
+        rows = sorted(csv.DictReader(open(f)), key=lambda r: int(r["Start_Timestamp"]))
+        for r, k in zip(rows, gemm_kinds([r["Kernel_Name"] for r in rows])):
             if k:
                 durs[k].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3)
     if not durs or not sums:
