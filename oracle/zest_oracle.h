@@ -28,9 +28,13 @@
  *   ref_mul_mat ................ pinned: integer KAT (exact under any order),
  *                                fp64 recomputation bound
  *   host ops ................... RMS_NORM/MUL/ADD/SCALE/GLU pinned by closed forms
- *                                and fp64 recomputation; ROPE's YaRN correction
- *                                dims restate ggml_rope_yarn_corr_dims (absent):
- *                                parity unpinned for ext_factor != 0
+ *                                and fp64 recomputation; ROPE's YaRN part
+ *                                (ggml_rope_yarn_corr_dims is absent) pinned by
+ *                                YaRN's definitions: the correction dims are the
+ *                                pairs turning beta_fast / beta_slow times over
+ *                                n_ctx_orig, pairs below and above them take the
+ *                                extrapolated and interpolated angles, the
+ *                                magnitude is 1 + 0.1 ln(1/s)
  */
 #ifndef ZEST_ORACLE_H
 #define ZEST_ORACLE_H

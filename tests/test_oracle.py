@@ -519,9 +519,58 @@ def test_rope_is_a_rotation_by_pos_times_theta(oracle, mode):
 
 
 def test_rope_yarn_corr_dims_closed_form(oracle):
-    # parity unpinned against ggml (absent): checked against the YaRN formula
-    # dim(r) = n_dims*ln(n_ctx/(2*pi*r)) / (2 ln base), floor/ceil and clamped
-    n, ctx, base = 64, 4096, 10000.0
-    dim = lambda r: n * np.log(ctx / (2 * np.pi * r)) / (2 * np.log(base))
-    lo, hi = oracle.corr_dims(n, ctx, base, 32.0, 1.0)
-    assert lo == max(0.0, np.floor(dim(32.0))) and hi == min(n - 1.0, np.ceil(dim(1.0)))
+    # YaRN's correction dims are where a rotation pair completes beta turns
+    # over the original context: pair d turns n_ctx * base^(-2d/n) / (2 pi)
+    # times. The first dim is the last pair (rounded down) turning at least
+    # beta_fast times, the second the first pair (rounded up) turning at most
+    # beta_slow times, both clamped to [0, n - 1]
+    def turns(n, ctx, base, d):
+        return ctx * base ** (-2.0 * d / n) / (2 * np.pi)
+
+    checked = 0
+    for n, ctx, base, bf, bs in [(64, 4096, 10000.0, 32.0, 1.0), (128, 2048, 500000.0, 32.0, 1.0),
+                                 (96, 8192, 10000.0, 16.0, 2.0), (32, 512, 1e6, 64.0, 0.5)]:
+        lo, hi = oracle.corr_dims(n, ctx, base, bf, bs)
+        assert lo == int(lo) and hi == int(hi) and 0 <= lo <= hi <= n - 1
+        if lo > 0:
+            assert turns(n, ctx, base, lo) >= bf > turns(n, ctx, base, lo + 1)
+            checked += 1
+        else:
+            assert turns(n, ctx, base, 0) <= bf * (1 + 1e-6) or turns(n, ctx, base, 1) < bf
+        if hi < n - 1:
+            assert turns(n, ctx, base, hi) <= bs < turns(n, ctx, base, hi - 1)
+            checked += 1
+    assert checked >= 4
+
+
+def test_rope_yarn_ramp_ends_and_attention_scale(oracle):
+    # With ext_factor 1 and frequency scale s, pairs up to the first
+    # correction dim keep the extrapolated angle pos * base^(-2p/n), pairs from
+    # the second on take the interpolated one s * pos * base^(-2p/n), the mix
+    # between them moves linearly in the pair index, and every pair's
+    # magnitude is attn_factor * (1 + 0.1 ln(1/s)) (YaRN's attention scaling)
+    n, ctx, base, s, attn = 64, 4096, 10000.0, 0.25, 0.9
+    lo, hi = (int(v) for v in oracle.corr_dims(n, ctx, base, 32.0, 1.0))
+    pos = np.array([3], dtype=np.int32)
+    x = np.zeros((1, 1, n), dtype=np.float32)
+    x[0, 0, 0::2] = 1.0  # each pair (1, 0): the output is (m cos a, m sin a)
+    y = oracle.rope(x, pos, None, n, 0, ctx, base, s, 1.0, attn, 32.0, 1.0)[0, 0]
+    mag = np.hypot(y[0::2], y[1::2]).astype(np.float64)
+    ang = np.arctan2(y[1::2], y[0::2]).astype(np.float64)
+    assert np.allclose(mag, attn * (1 + 0.1 * np.log(1 / s)), rtol=1e-5)
+    p = np.arange(n // 2)
+    ext = 3.0 * base ** (-2.0 * p / n)
+    wrap = lambda a: (a + np.pi) % (2 * np.pi) - np.pi
+    assert np.allclose(wrap(ang[:lo + 1] - ext[:lo + 1]), 0, atol=2e-5)
+    assert np.allclose(wrap(ang[hi:] - s * ext[hi:]), 0, atol=2e-5)
+    # between the dims: the share of the extrapolated angle falls linearly
+    mid = np.arange(lo + 1, hi)
+    share = (ang[mid] - s * ext[mid]) / ((1 - s) * ext[mid])
+    keep = ext[mid] > 1e-3  # where the angle resolves the share
+    assert keep.sum() >= 5
+    step = np.diff(share[keep]) / np.diff(mid[keep])
+    assert np.allclose(step, -1.0 / (hi - lo), atol=2e-3) and np.all((share > -1e-3) & (share < 1 + 1e-3))
+    # ext_factor 0: plain interpolation, magnitude attn_factor
+    y0 = oracle.rope(x, pos, None, n, 0, ctx, base, s, 0.0, attn, 32.0, 1.0)[0, 0]
+    assert np.allclose(np.hypot(y0[0::2], y0[1::2]), attn, rtol=1e-5)
+    assert np.allclose(wrap(np.arctan2(y0[1::2], y0[0::2]) - s * ext), 0, atol=2e-5)
