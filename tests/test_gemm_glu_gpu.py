@@ -95,11 +95,14 @@ def test_gemm_glu_matches_unfused_swiglu(zest_gpu, oracle, wtype, M, F, K):
     assert nrmse(hs, oracle.glu(2, gs, us)) <= 1e-5  # tests/test-host-ops.cpp's bar
 
 
+@pytest.mark.parametrize("M,F,K", [
+    (300, 160, 256),    # 6 tiles: one workgroup a tile
+    (1500, 4096, 512),  # 384 tiles: persistent workgroups, each kind's own kernel
+])
 @pytest.mark.parametrize("kind", list(KINDS))
-def test_gemm_glu_every_kind(zest_gpu, kind):
+def test_gemm_glu_every_kind(zest_gpu, kind, M, F, K):
     import torch
-    M, F, K = 300, 160, 256
-    x = Rng(5).normal(M * K).reshape(M, K)
+    x = Rng(5 + M).normal(M * K).reshape(M, K)
     gate, up = _weights(0, F, K, 9)
     a = zest_gpu.pack_act_x(_dev(x))
     wgu = zest_gpu.convert_weight_gu(0, gate, up, F, K)
