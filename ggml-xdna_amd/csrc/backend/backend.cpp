@@ -468,6 +468,9 @@ std::vector<fusion> find_fusions(const std::vector<ggml_tensor *> & nodes,
             f.swapped = param_i32(n, 1) != 0;
         }
         if (f.F % 32 || n->ne[0] != f.F || nrows(n) != gm->src[1]->ne[1]) continue;
+        // one launch addresses the 2F-row weight and the packed h whole
+        const int64_t M = gm->src[1]->ne[1];
+        if (!gemm_shape_fits(M, f.K, 2 * f.F) || zest_act_bytes(M, f.F) >= (1ull << 31)) continue;
         // another reader of the gate's or up's result
         if (!read_by_other(rd, gm, n) && !(um && read_by_other(rd, um, n))) out.push_back(f);
     }
@@ -488,7 +491,8 @@ std::unordered_map<const ggml_tensor *, const ggml_tensor *> find_residuals(
             const ggml_tensor * n = a->src[side], * r = a->src[1 - side];
             if (!n || !r || !gemm_matmul(n) || fused.count(n) || !in_piece.count(n) || read_outside(n, in_piece) ||
                 !same_shape(a, n) || !same_shape(a, r) || r->type != GGML_TYPE_F32 || r->nb[0] != 4 ||
-                r->nb[1] % 16 != 0 || nrows(a) != a->ne[1])
+                r->nb[1] % 16 != 0 || (r->view_src && r->view_offs % 16 != 0) || nrows(a) != a->ne[1] ||
+                (uint64_t) std::max(r->nb[1], a->nb[1]) * 256 >= (1ull << 31))
                 continue;
             if (read_by_other(rd, n, a)) continue;  // another reader of the matmul's result
             out[a] = n;

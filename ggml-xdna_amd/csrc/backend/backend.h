@@ -37,6 +37,11 @@ bool claim_mul_mat(const ggml_tensor * op);
 bool is_weight(const ggml_tensor * w);
 bool exec_supports(const ggml_tensor * op);
 const ggml_tensor * exec_param(const ggml_tensor * op);
+// Whether one GEMM launch addresses an M x K activation operand, a K x N
+// weight's cache entry, and output bands of 256 rows of N floats, each under
+// 2 GiB (the kernels' buffer ranges); the library cuts a taller output into
+// bands itself.
+bool gemm_shape_fits(int64_t M, int64_t K, int64_t N);
 
 // Reader tracking (src/ggml-zest.cpp:1082-1109): every op the scheduler asks
 // about records its inputs' readers; a result is needed outside a graph piece

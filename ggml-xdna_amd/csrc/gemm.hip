@@ -1217,14 +1217,20 @@ int64_t tiles_of(const gemm_params & p, const int64_t * N, int BM, int BN) {
     return ((p.M + BM - 1) / BM) * nt;
 }
 
-// The cheapest number of K splits for T tiles of nk steps on P CUs, with
-// tiles of tile_bytes fp32 and steps of `step` 256x128-steps.
+// The modelled cost of T tiles of nk steps on P CUs split S ways, with tiles
+// of tile_bytes fp32 and steps of `step` 256x128-steps.
+double split_cost(int64_t T, int nk, int64_t P, double tile_bytes, double step, int S) {
+    if (S == 1) return (double) ((T + P - 1) / P) * (nk + ZEST_GEMM_PROLOGUE) * step;
+    return (double) ((T * S + P - 1) / P) * ((double) nk / S + ZEST_GEMM_PROLOGUE) * step +
+           2.0 * T * S * tile_bytes / ZEST_GEMM_FIX_BW + ZEST_GEMM_FIX_LAT;
+}
+
+// The cheapest number of K splits for T tiles (as split_cost).
 gemm_plan plan_splits(int64_t T, int nk, int64_t P, double tile_bytes, double step) {
     gemm_plan best;
-    best.cost = (double) ((T + P - 1) / P) * (nk + ZEST_GEMM_PROLOGUE) * step;
+    best.cost = split_cost(T, nk, P, tile_bytes, step, 1);
     for (int S = 2; S <= ZEST_GEMM_MAX_SPLIT && nk / S >= 4; S++) {
-        const double cost = (double) ((T * S + P - 1) / P) * ((double) nk / S + ZEST_GEMM_PROLOGUE) * step +
-                            2.0 * T * S * tile_bytes / ZEST_GEMM_FIX_BW + ZEST_GEMM_FIX_LAT;
+        const double cost = split_cost(T, nk, P, tile_bytes, step, S);
         if (cost < best.cost) {
             best.splits = S;
             best.cost = cost;
@@ -1335,59 +1341,86 @@ int launch_mixed(gemm_params p, const int64_t * N, int64_t nbig, hipStream_t s, 
     return zest::check_launch(name);
 }
 
-// The tile shape and K splits of a launch (the cost model above); `fixed` as
-// for launch().
+// The plan of a plain (or residual) launch: its tile shape and K splits.
+enum class shape_kind { o_round, mixed, tiny, small, o_one, glu_one, big };
+struct plain_plan {
+    shape_kind kind;
+    int splits;
+    int64_t nbig;  // mixed: the whole tiles
+};
+
+// The cost model above, applied: the cheapest of one round of 128x160 tiles
+// (long K), a mixed launch, 64x64 tiles, 128x128 or 256x128 tiles (each with
+// its best K split), and, for one unsplit round, 128x160 or two-consumer
+// 256x128 tiles.
+plain_plan plan_plain(const gemm_params & p, const int64_t * N, int64_t P) {
+    const gemm_plan big =
+        plan_splits(tiles_of(p, N, cfg_big::BM, cfg_big::BN), p.nk, P, (double) cfg_big::BM * cfg_big::BN * 4, 1.0);
+    const gemm_plan small = plan_splits(tiles_of(p, N, cfg_small::BM, cfg_small::BN), p.nk, P,
+                                        (double) cfg_small::BM * cfg_small::BN * 4, ZEST_GEMM_SMALL_STEP);
+    bool whole = true;  // every weight whole 160-row tiles
+    for (int i = 0; i < p.nw; i++) whole &= N[i] % cfg_o::BN == 0;
+    const int64_t To = tiles_of(p, N, cfg_o::BM, cfg_o::BN);
+    // one round of 128x160 tiles, unsplit, when every weight is whole
+    // 160-row tiles, they fill more than half the GPU and K is long enough
+    // for the prologue not to matter: no split-K fixup traffic, and the
+    // tile's producers keep up with its consumers (the down projection at
+    // 2048 tokens, K 9728: 104.5 us in three splits, 96 us so)
+    if (whole && To <= P && 2 * To > P && p.nk >= 16) return {shape_kind::o_round, 1, 0};
+    // mixed: whole rounds of big tiles, the part-round left as half tiles
+    const int64_t Tb = tiles_of(p, N, cfg_big::BM, cfg_big::BN), R = Tb / P, rem = Tb - R * P;
+    if (R >= 1 && rem > 0 && R * P % 8 == 0) {
+        const double mixed =
+            ((double) R + (double) ((2 * rem + P - 1) / P) * ZEST_GEMM_SMALL_STEP) * (p.nk + ZEST_GEMM_PROLOGUE);
+        if (mixed < big.cost && mixed < small.cost) return {shape_kind::mixed, 1, R * P};
+    }
+    // tiny tiles, cfg_tiny::MINB of them a CU
+    const gemm_plan tiny = plan_splits(tiles_of(p, N, cfg_tiny::BM, cfg_tiny::BN), p.nk, P * cfg_tiny::MINB,
+                                       (double) cfg_tiny::BM * cfg_tiny::BN * 4, ZEST_GEMM_TINY_STEP);
+    if (tiny.cost < big.cost && tiny.cost < small.cost) return {shape_kind::tiny, tiny.splits, 0};
+    if (small.cost < big.cost) return {shape_kind::small, small.splits, 0};
+    if (big.splits == 1 && Tb <= P) {
+        // one round of whole tiles: as 128x160 tiles where the weights are
+        // whole 160-row tiles (the tiles then read only rows each packed
+        // weight holds) and they fit one round too, else with two consumers
+        // per SIMD
+        if (whole && To <= P) return {shape_kind::o_one, 1, 0};
+        return {shape_kind::glu_one, 1, 0};
+    }
+    return {shape_kind::big, big.splits, 0};
+}
+
+// Plans and launches a GEMM; `fixed` as for launch(). A fused GLU launch
+// splits K as the plain launch of its 2F columns would (so its gate and up
+// sums are that launch's, bit for bit) and takes the cheaper of 256x128 and
+// 128x128 tiles at that split.
 template <int EPI>
 int launch_any(gemm_params p, const int64_t * N, hipStream_t s, const char * name,
                const sk_space * fixed = nullptr) {
     int dev = 0;
     (void) hipGetDevice(&dev);
     const int64_t P = cu_count(dev);
-    using CB = std::conditional_t<(EPI >= 0), cfg_glu, cfg_big>;
-    const gemm_plan big =
-        plan_splits(tiles_of(p, N, CB::BM, CB::BN), p.nk, P, (double) CB::BM * CB::BN * 4, 1.0);
-    const gemm_plan small = plan_splits(tiles_of(p, N, cfg_small::BM, cfg_small::BN), p.nk, P,
-                                        (double) cfg_small::BM * cfg_small::BN * 4, ZEST_GEMM_SMALL_STEP);
-    if constexpr (EPI < 0) {
-        // one round of 128x160 tiles, unsplit, when every weight is whole
-        // 160-row tiles, they fill more than half the GPU and K is long enough
-        // for the prologue not to matter: no split-K fixup traffic, and the
-        // tile's producers keep up with its consumers (the down projection at
-        // 2048 tokens, K 9728: 104.5 us in three splits, 96 us so)
-        bool whole = true;
-        for (int i = 0; i < p.nw; i++) whole &= N[i] % cfg_o::BN == 0;
-        const int64_t To = tiles_of(p, N, cfg_o::BM, cfg_o::BN);
-        if (whole && To <= P && 2 * To > P && p.nk >= 16) return launch<cfg_o, EPI>(p, N, 1, s, name, fixed);
-    }
-    if constexpr (EPI < 0) {
-        // mixed: whole rounds of big tiles, the part-round left as half tiles
-        const int64_t Tb = tiles_of(p, N, cfg_big::BM, cfg_big::BN), R = Tb / P, rem = Tb - R * P;
-        if (R >= 1 && rem > 0 && R * P % 8 == 0) {
-            const double mixed =
-                ((double) R + (double) ((2 * rem + P - 1) / P) * ZEST_GEMM_SMALL_STEP) * (p.nk + ZEST_GEMM_PROLOGUE);
-            if (mixed < big.cost && mixed < small.cost) return launch_mixed<cfg_glu, cfg_half8, EPI>(p, N, R * P, s, name);
+    const plain_plan pp = plan_plain(p, N, P);
+    if constexpr (EPI >= 0) {
+        const int S = pp.splits;
+        const double big = split_cost(tiles_of(p, N, cfg_glu::BM, cfg_glu::BN), p.nk, P,
+                                      (double) cfg_glu::BM * cfg_glu::BN * 4, 1.0, S);
+        const double small = split_cost(tiles_of(p, N, cfg_small::BM, cfg_small::BN), p.nk, P,
+                                        (double) cfg_small::BM * cfg_small::BN * 4, ZEST_GEMM_SMALL_STEP, S);
+        if (small < big) return launch<cfg_small, EPI>(p, N, S, s, name, fixed);
+        return launch<cfg_glu, EPI>(p, N, S, s, name, fixed);
+    } else {
+        switch (pp.kind) {
+            case shape_kind::o_round:
+            case shape_kind::o_one: return launch<cfg_o, EPI>(p, N, 1, s, name, fixed);
+            case shape_kind::mixed: return launch_mixed<cfg_glu, cfg_half8, EPI>(p, N, pp.nbig, s, name);
+            case shape_kind::tiny: return launch<cfg_tiny, EPI>(p, N, pp.splits, s, name, fixed);
+            case shape_kind::small: return launch<cfg_small, EPI>(p, N, pp.splits, s, name, fixed);
+            case shape_kind::glu_one: return launch<cfg_glu, EPI>(p, N, 1, s, name, fixed);
+            case shape_kind::big: break;
         }
+        return launch<cfg_big, EPI>(p, N, pp.splits, s, name, fixed);
     }
-    if constexpr (EPI < 0) {
-        // tiny tiles, cfg_tiny::MINB of them a CU
-        const gemm_plan tiny = plan_splits(tiles_of(p, N, cfg_tiny::BM, cfg_tiny::BN), p.nk, P * cfg_tiny::MINB,
-                                           (double) cfg_tiny::BM * cfg_tiny::BN * 4, ZEST_GEMM_TINY_STEP);
-        if (tiny.cost < big.cost && tiny.cost < small.cost)
-            return launch<cfg_tiny, EPI>(p, N, tiny.splits, s, name, fixed);
-    }
-    if (small.cost < big.cost) return launch<cfg_small, EPI>(p, N, small.splits, s, name, fixed);
-    if constexpr (EPI < 0)
-        if (big.splits == 1 && tiles_of(p, N, CB::BM, CB::BN) <= P) {
-            // one round of whole tiles: as 128x160 tiles where the weights
-            // are whole 160-row tiles (the tiles then read only rows each
-            // packed weight holds) and they fit one round too, else with two
-            // consumers per SIMD
-            bool whole = true;
-            for (int i = 0; i < p.nw; i++) whole &= N[i] % cfg_o::BN == 0;
-            if (whole && tiles_of(p, N, cfg_o::BM, cfg_o::BN) <= P) return launch<cfg_o, EPI>(p, N, 1, s, name, fixed);
-            return launch<cfg_glu, EPI>(p, N, 1, s, name, fixed);
-        }
-    return launch<CB, EPI>(p, N, big.splits, s, name, fixed);
 }
 
 // The parts of a launch's parameters common to every kind.
@@ -1411,7 +1444,31 @@ gemm_weight weight_of(const void * w, int64_t N, float * c, int64_t ldc) {
     return g;
 }
 
-// zest_gemm_group's checks and launch; `fixed` as for launch().
+// The rows of one launch's band. A launch reaches its output (and a
+// residual) through buffer resources whose byte ranges are 32-bit, so an
+// output of rows `ld` floats apart runs as bands of whole 256-row tiles, each
+// under 2 GiB, one launch a band (the reference likewise cuts a claimed
+// matmul into NPU calls of at most 1024 rows, src/xdna-npu.cpp:392-420).
+// 0 when not even 256 rows fit.
+int64_t band_rows(int64_t ld) {
+    const int64_t rows = ((1ll << 31) - 1) / (ld * 4);
+    return rows / ZEST_ROW_ALIGN * ZEST_ROW_ALIGN;
+}
+
+// The launch parameters of the band of rows [r0, r0 + rows): the activation
+// operand from row r0 on (whole 32-row groups; the K-step stride stays the
+// whole operand's) and each weight's output from its row r0.
+gemm_params band_of(const gemm_params & p, int64_t r0, int64_t rows) {
+    gemm_params q = p;
+    q.M = rows;
+    q.a = p.a + r0 / ZEST_XGROUP_ROWS * ZEST_XGROUP_BYTES;
+    for (int i = 0; i < p.nw; i++)
+        if (q.wt[i].c) q.wt[i].c += r0 * q.wt[i].ldc;
+    if (q.res) q.res += r0 * q.ldr;
+    return q;
+}
+
+// zest_gemm_group's checks and launches; `fixed` as for launch().
 int gemm_group(const void * a, int64_t M, int64_t K, int n, const void * const * w, const int64_t * N,
                float * const * c, const int64_t * ldc, uint32_t * nonfinite, void * stream, const char * name,
                const sk_space * fixed) {
@@ -1421,17 +1478,24 @@ int gemm_group(const void * a, int64_t M, int64_t K, int n, const void * const *
     ZEST_REQUIRE(zest_act_bytes(M, K) < (1ull << 31), "%s: activations must be under 2 GiB", name);
     gemm_params p = base_params(a, M, K, nonfinite);
     p.nw = n;
+    int64_t ld_max = 0;
     for (int i = 0; i < n; i++) {
         ZEST_REQUIRE(w[i] && c[i], "%s: null weight or output %d", name, i);
         ZEST_REQUIRE(N[i] > 0 && ldc[i] >= N[i], "%s: weight %d: N=%lld ldc=%lld", name, i, (long long) N[i],
                      (long long) ldc[i]);
-        ZEST_REQUIRE(zest_bfp16_bytes(N[i], K) < (1ull << 31) &&
-                         (uint64_t) zest_rows_padded(M) * (uint64_t) ldc[i] * 4 < (1ull << 31),
-                     "%s: weight %d and its output must be under 2 GiB (N=%lld ldc=%lld)", name, i,
-                     (long long) N[i], (long long) ldc[i]);
+        ZEST_REQUIRE(zest_bfp16_bytes(N[i], K) < (1ull << 31), "%s: weight %d must be under 2 GiB (N=%lld K=%lld)",
+                     name, i, (long long) N[i], (long long) K);
         p.wt[i] = weight_of(w[i], N[i], c[i], ldc[i]);
+        ld_max = std::max(ld_max, ldc[i]);
     }
-    return launch_any<EPI_PLAIN>(p, N, zest::as_stream(stream), name, fixed);
+    const int64_t band = band_rows(ld_max);
+    ZEST_REQUIRE(band > 0, "%s: 256 output rows of %lld floats must be under 2 GiB", name, (long long) ld_max);
+    const hipStream_t s = zest::as_stream(stream);
+    for (int64_t r0 = 0; r0 < M; r0 += band) {
+        const int st = launch_any<EPI_PLAIN>(band_of(p, r0, std::min(band, M - r0)), N, s, name, fixed);
+        if (st != ZEST_OK) return st;
+    }
+    return ZEST_OK;
 }
 
 } // namespace
@@ -1480,15 +1544,21 @@ extern "C" int zest_gemm_residual(const void * a, int64_t M, const void * w, int
                  (long long) ldr, (long long) N);
     ZEST_REQUIRE((reinterpret_cast<uintptr_t>(res) & 15) == 0 && ldr % 4 == 0,
                  "zest_gemm_residual: the residual's rows must be 16-byte aligned");
-    ZEST_REQUIRE(zest_act_bytes(M, K) < (1ull << 31) && zest_bfp16_bytes(N, K) < (1ull << 31) &&
-                     (uint64_t) zest_rows_padded(M) * (uint64_t) std::max(ldc, ldr) * 4 < (1ull << 31),
-                 "zest_gemm_residual: operands and output must be under 2 GiB");
+    ZEST_REQUIRE(zest_act_bytes(M, K) < (1ull << 31) && zest_bfp16_bytes(N, K) < (1ull << 31),
+                 "zest_gemm_residual: operands must be under 2 GiB");
+    const int64_t band = band_rows(std::max(ldc, ldr));
+    ZEST_REQUIRE(band > 0, "zest_gemm_residual: 256 rows of the output and residual must be under 2 GiB");
     gemm_params p = base_params(a, M, K, nonfinite);
     p.nw = 1;
     p.wt[0] = weight_of(w, N, c, ldc);
     p.res = res;
     p.ldr = ldr;
-    return launch_any<EPI_RESIDUAL>(p, &N, zest::as_stream(stream), "zest_gemm_residual");
+    const hipStream_t s = zest::as_stream(stream);
+    for (int64_t r0 = 0; r0 < M; r0 += band) {
+        const int st = launch_any<EPI_RESIDUAL>(band_of(p, r0, std::min(band, M - r0)), &N, s, "zest_gemm_residual");
+        if (st != ZEST_OK) return st;
+    }
+    return ZEST_OK;
 }
 
 extern "C" int zest_gemm_glu(int kind, const void * a, int64_t M, const void * w_gu, int64_t F, int64_t K,

@@ -123,6 +123,11 @@ ZEST_API int zest_convert_weight(int type, const void *raw, int64_t N, int64_t K
  * mm_bfp_acc.cc:44-116, 258-278). */
 ZEST_API int zest_gemm(const void *a, int64_t M, const void *w, int64_t N, int64_t K, float *c, int64_t ldc,
                        uint32_t *nonfinite, void *stream);
+/* Limits of zest_gemm, zest_gemm_residual and zest_gemm_group: the expanded
+ * activations and each packed weight under 2 GiB, and 256 rows of the output
+ * (and of the residual) under 2 GiB. A taller output runs as launches over
+ * bands of rows, each band's output span under 2 GiB (whole 256-row tiles;
+ * the plan, and so the K split, is made per band). */
 
 /* c[M][N] = A . W^T + res[M][N] (row stride ldr floats, 16-byte aligned
  * rows; res may be c itself, for an in-place residual add): zest_gemm with
@@ -185,12 +190,12 @@ ZEST_API int zest_convert_weight_gu(int type, const void *gate, const void *up, 
  * h[M][F] = glu(g, u) of `kind` (zest_glu's arithmetic), written as the next
  * matmul's operand (xout, as zest_pack_act_x writes it, zest_act_bytes(M, F)
  * bytes) and/or as fp32 rows (h, row stride ldh floats); either may be NULL,
- * not both. h is bit-exact with zest_glu over the gate and up columns of
- * zest_gemm(a, w_gu) (2F columns, the same summation order) whenever that
- * launch splits K as this one does: always, except where zest_gemm takes
- * one unsplit round of 160-row tiles (2F a multiple of 160), which this
- * launch cannot (a tile would split a gate/up pair); and xout with
- * zest_pack_act_x of that. `nonfinite` as for zest_gemm, over g, u and h.
+ * not both. This launch splits K among workgroups exactly as zest_gemm(a,
+ * w_gu) of 2F columns does, so its gate and up sums are that call's, bit for
+ * bit, and h is bit-exact with zest_glu over the gate and up columns of
+ * zest_gemm(a, w_gu) whenever that call runs as one launch (its fp32 output,
+ * M x 2F floats, under 2 GiB); xout is then zest_pack_act_x of that h.
+ * `nonfinite` as for zest_gemm, over g, u and h.
  * F % 32 == 0.
  * Replaces the reference's fused SwiGLU matmul: find_fusions
  * (src/xdna-exec.cpp:399-431) and the NPU kernel's output mode 2

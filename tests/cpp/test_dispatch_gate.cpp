@@ -17,6 +17,11 @@
 //            taken when one input comes from a taken op, it covers the batch,
 //            its row inputs are kept leaves, and no same-shape input may sit
 //            in host memory (graph inputs, GET_ROWS results);
+//   size     one launch addresses the weight's cache entry and the expanded
+//            activations whole and the output in bands of 256 rows or more,
+//            each under 2 GiB: an operand no band fits is left, a tall
+//            output is taken (the library cuts it into bands); the right
+//            side's rows are 16-byte aligned;
 //   never    MUL_MAT_ID and every other op; offload_op claims nothing.
 // Each rule is checked on both sides of its boundary, with the expected
 // answer computed here from the rule where it is arithmetic. BASELINE's
@@ -96,6 +101,42 @@ void weight_rule() {
     expect(made, false, "never", "an ADD of two leaves");
     expect(ggml_mul_mat(g_ctx, weight(GGML_TYPE_Q8_0, 2048, 2048), ggml_new_tensor_3d(g_ctx, GGML_TYPE_F32, 2048, 1024, 2)),
            false, "weight", "a 3-D right side");
+}
+
+// What one launch addresses: the packed weight and the expanded activations
+// whole, the output in bands of 256 rows or more, each under 2 GiB (32-bit
+// buffer ranges). A taller output is cut into bands by the library, so it is
+// taken; an operand that no band can fit is left to the scheduler.
+void size_rule() {
+    constexpr double lim = 2147483648.0;
+    auto rnd = [](int64_t v, int64_t a) { return (double) ((v + a - 1) / a * a); };
+    // an all-logits output projection: vocab 151,936 at a 4096-token ubatch,
+    // 2.49 GB of fp32 output, runs as bands of 3328 rows
+    const double out_bytes = 151936.0 * 4096 * 4;
+    test_check(out_bytes > lim, "[size] the logits output spans %.2f GB", out_bytes / 1e9);
+    expect(matmul(GGML_TYPE_Q6_K, 2560, 151936, 4096), true, "size",
+           "output projection 2560x151936 at batch 4096 (%.2f GB of output, cut into bands)", out_bytes / 1e9);
+    expect(matmul(GGML_TYPE_Q8_0, 5120, 262144, 8192), true, "size", "a 262,144-word vocabulary at batch 8192");
+    // a weight whose cache entry reaches 2 GiB: 131072 x 16384 at 9/8 bytes a value
+    const double w_bytes = rnd(131072, 256) * rnd(16384, 64) * 9 / 8;
+    expect(matmul(GGML_TYPE_Q4_K, 16384, 131072, 2048), w_bytes < lim, "size", "a weight of %.2f GB as bfp16",
+           w_bytes / 1e9);
+    expect(matmul(GGML_TYPE_Q4_K, 16384, 65536, 2048), true, "size", "half that weight (%.2f GB)", w_bytes / 2e9);
+    // activations whose expanded operand (2 bytes a value) reaches 2 GiB
+    const double a_bytes = rnd(65536, 256) * rnd(16384, 64) * 2;
+    expect(matmul(GGML_TYPE_Q8_0, 16384, 1024, 65536), a_bytes < lim, "size",
+           "65536 rows of 16384 (%.2f GB expanded)", a_bytes / 1e9);
+    expect(matmul(GGML_TYPE_Q8_0, 16384, 1024, 32768), true, "size", "32768 rows of 16384");
+    // 256 output rows of N floats must fit one band
+    expect(matmul(GGML_TYPE_Q8_0, 256, 2097152, 1024), 256.0 * 2097152 * 4 < lim, "size",
+           "N = 2,097,152: 256 output rows take 2 GiB");
+    expect(matmul(GGML_TYPE_Q8_0, 256, 2097136, 1024), true, "size", "N = 2,097,136: 256 rows just fit");
+    // the right side's rows must be 16-byte aligned (the pack's 16-byte loads)
+    ggml_tensor * big = rows(2048, 2048 + 4);
+    expect(ggml_mul_mat(g_ctx, weight(GGML_TYPE_Q8_0, 2048, 2048), ggml_view_2d(g_ctx, big, 2048, 2048, big->nb[1], 4)),
+           false, "size", "right side a view 4 bytes into its tensor");
+    expect(ggml_mul_mat(g_ctx, weight(GGML_TYPE_Q8_0, 2048, 2048), ggml_view_2d(g_ctx, big, 2048, 2048, big->nb[1], 64)),
+           true, "size", "right side a view 64 bytes into its tensor");
 }
 
 void block_rule() {
@@ -193,6 +234,7 @@ int main() {
     batch_rule();
     floor_rule();
     weight_rule();
+    size_rule();
     block_rule();
     never_rule();
     small_model_config();

@@ -20,22 +20,63 @@
 #include "zest_oracle.h"
 
 using fvec = std::vector<float>;
-using in_t = std::vector<ggml_tensor *>;
+using ivec = std::vector<int32_t>;
+
+// The inputs of one case, each made together with how its values are drawn:
+// activations and scale rows normal(0, 1.5), rope frequency factors uniform
+// in [1, 4), positions 5000 + 300 i (past a short context). Values are drawn
+// in the order the inputs are made, so a case makes them in separate
+// statements (the order in which a call's arguments are evaluated is not
+// specified).
+class case_inputs {
+public:
+    enum class draw { normal, factor, position };
+    explicit case_inputs(ggml_context * ctx) : ctx_(ctx) {}
+
+    ggml_tensor * rows(int64_t width, int64_t n, int64_t planes = 1) {
+        return add(ggml_new_tensor_3d(ctx_, GGML_TYPE_F32, width, n, planes), draw::normal);
+    }
+    ggml_tensor * row(int64_t width) { return add(ggml_new_tensor_1d(ctx_, GGML_TYPE_F32, width), draw::normal); }
+    ggml_tensor * factors(int64_t n) { return add(ggml_new_tensor_1d(ctx_, GGML_TYPE_F32, n), draw::factor); }
+    ggml_tensor * positions(int64_t n) { return add(ggml_new_tensor_1d(ctx_, GGML_TYPE_I32, n), draw::position); }
+    ggml_context * ctx() const { return ctx_; }
+
+    // Draws every input's values (in creation order, from one seeded
+    // stream), uploads them, and returns them for the oracle: the float
+    // inputs in order, and the position inputs in order.
+    void upload(uint64_t seed, std::vector<fvec> & floats, std::vector<ivec> & pos) const {
+        test_rng rng(seed);
+        for (const auto & [t, how] : made_) {
+            const size_t n = (size_t) ggml_nelements(t);
+            if (how == draw::position) {
+                ivec v(n);
+                for (size_t i = 0; i < n; i++) v[i] = 5000 + 300 * (int32_t) i;
+                ggml_backend_tensor_set(t, v.data(), 0, ggml_nbytes(t));
+                pos.push_back(std::move(v));
+                continue;
+            }
+            fvec v(n);
+            for (float & x : v) x = how == draw::factor ? (float) (1.0 + 3.0 * rng.uniform()) : rng.normal(0.0f, 1.5f);
+            ggml_backend_tensor_set(t, v.data(), 0, ggml_nbytes(t));
+            floats.push_back(std::move(v));
+        }
+    }
+
+private:
+    ggml_tensor * add(ggml_tensor * t, draw how) {
+        made_.emplace_back(t, how);
+        return t;
+    }
+    ggml_context * ctx_;
+    std::vector<std::pair<ggml_tensor *, draw>> made_;
+};
 
 struct op_case {
     const char * name;
-    std::function<ggml_tensor *(ggml_context *, in_t &)> build;
-    // the oracle's answer from the inputs' values, in creation order
-    std::function<fvec(const std::vector<fvec> &, const std::vector<std::vector<int32_t>> &)> cpu;
+    std::function<ggml_tensor *(case_inputs &)> build;
+    // the oracle's answer from the inputs' values (floats, positions)
+    std::function<fvec(const std::vector<fvec> &, const std::vector<ivec> &)> cpu;
 };
-
-static ggml_tensor * input(ggml_context * ctx, in_t & in, ggml_type type, int64_t a, int64_t b = 1, int64_t c = 1,
-                           const char * name = "x") {
-    ggml_tensor * t = ggml_new_tensor_3d(ctx, type, a, b, c);
-    ggml_set_name(t, name);
-    in.push_back(t);
-    return t;
-}
 
 static double nrmse(const fvec & got, const fvec & want) {
     double se = 0, ss = 0;
@@ -46,44 +87,30 @@ static double nrmse(const fvec & got, const fvec & want) {
     return std::sqrt(se / std::max(ss, 1e-300));
 }
 
+// One case: its graph on the backend, its inputs drawn with seed 42, its
+// result against the oracle's.
 static bool run_case(ggml_backend_t be, const op_case & c) {
     ggml_init_params ip = {ggml_tensor_overhead() * 16 + ggml_graph_overhead(), nullptr, true};
     ggml_context * ctx = ggml_init(ip);
-    in_t in;
-    ggml_tensor * out = c.build(ctx, in);
+    case_inputs in(ctx);
+    ggml_tensor * out = c.build(in);
     ggml_backend_buffer_t buf = ggml_backend_alloc_ctx_tensors(ctx, be);
     if (!buf) {
         ggml_free(ctx);
         return test_check(false, "%-32s could not allocate", c.name);
     }
-    test_rng rng(42);
-    std::vector<fvec> fin;
-    std::vector<std::vector<int32_t>> iin;
-    for (ggml_tensor * t : in) {
-        const int64_t n = ggml_nelements(t);
-        if (t->type == GGML_TYPE_I32) {
-            std::vector<int32_t> pos((size_t) n);
-            for (int64_t i = 0; i < n; i++) pos[(size_t) i] = 5000 + 300 * (int32_t) i;
-            ggml_backend_tensor_set(t, pos.data(), 0, ggml_nbytes(t));
-            iin.push_back(pos);
-        } else {
-            fvec v((size_t) n);
-            for (float & x : v) x = strcmp(t->name, "factors") == 0 ? (float) (1.0 + 3.0 * rng.uniform()) : rng.normal(0.0f, 1.5f);
-            ggml_backend_tensor_set(t, v.data(), 0, ggml_nbytes(t));
-            fin.push_back(v);
-        }
-    }
+    std::vector<fvec> floats;
+    std::vector<ivec> pos;
+    in.upload(42, floats, pos);
     ggml_cgraph * gf = ggml_new_graph(ctx);
     ggml_build_forward_expand(gf, out);
-    fvec got;
-    if (ggml_backend_graph_compute(be, gf) == GGML_STATUS_SUCCESS) {
-        got.resize((size_t) ggml_nelements(out));
-        ggml_backend_tensor_get(out, got.data(), 0, ggml_nbytes(out));
-    }
+    const bool ran = ggml_backend_graph_compute(be, gf) == GGML_STATUS_SUCCESS;
+    fvec got(ran ? (size_t) ggml_nelements(out) : 0);
+    if (ran) ggml_backend_tensor_get(out, got.data(), 0, ggml_nbytes(out));
     ggml_backend_buffer_free(buf);
     ggml_free(ctx);
-    const fvec want = c.cpu(fin, iin);
-    if (got.empty() || got.size() != want.size()) return test_check(false, "%-32s could not compute", c.name);
+    const fvec want = c.cpu(floats, pos);
+    if (!ran || got.size() != want.size()) return test_check(false, "%-32s could not compute", c.name);
     const double e = nrmse(got, want);
     return test_check(std::isfinite(e) && e <= 1e-5, "%-32s nrmse %.2e (allowed 1e-05)", c.name, e);
 }
@@ -273,92 +300,83 @@ int main() {
 
     const int64_t D = 256, T = 8, HD = 64, H = 4;
     using vin = std::vector<fvec>;
-    using iin = std::vector<std::vector<int32_t>>;
+    using pin = std::vector<ivec>;
+    // the oracle's answer of `rows` x `width` floats, filled by `f`
+    auto answer = [](int64_t n, auto f) {
+        fvec y((size_t) n);
+        f(y.data());
+        return y;
+    };
     auto glu_split = [&](const char * name, ggml_glu_op op, int kind) {
         return op_case{name,
-                       [=](ggml_context * ctx, in_t & in) {
-                           ggml_tensor * g = input(ctx, in, GGML_TYPE_F32, D, T);
-                           return ggml_glu_split(ctx, g, input(ctx, in, GGML_TYPE_F32, D, T), op);
+                       [=](case_inputs & in) {
+                           ggml_tensor * g = in.rows(D, T);  // made first: its values are drawn first
+                           ggml_tensor * u = in.rows(D, T);
+                           return ggml_glu_split(in.ctx(), g, u, op);
                        },
-                       [=](const vin & v, const iin &) {
-                           fvec y((size_t) (D * T));
-                           orc_glu(kind, v[0].data(), D, v[1].data(), D, T, D, y.data());
-                           return y;
+                       [=](const vin & v, const pin &) {
+                           return answer(D * T, [&](float * y) { orc_glu(kind, v[0].data(), D, v[1].data(), D, T, D, y); });
                        }};
     };
     auto glu_one = [&](const char * name, ggml_glu_op op, int kind, bool swapped) {
-        return op_case{name,
-                       [=](ggml_context * ctx, in_t & in) {
-                           return ggml_glu(ctx, input(ctx, in, GGML_TYPE_F32, 2 * D, T), op, swapped);
-                       },
-                       [=](const vin & v, const iin &) {
-                           fvec y((size_t) (D * T));
-                           const float * a = v[0].data();
-                           orc_glu(kind, swapped ? a + D : a, 2 * D, swapped ? a : a + D, 2 * D, T, D, y.data());
-                           return y;
+        return op_case{name, [=](case_inputs & in) { return ggml_glu(in.ctx(), in.rows(2 * D, T), op, swapped); },
+                       [=](const vin & v, const pin &) {
+                           const float * gate = v[0].data() + (swapped ? D : 0), * up = v[0].data() + (swapped ? 0 : D);
+                           return answer(D * T, [&](float * y) { orc_glu(kind, gate, 2 * D, up, 2 * D, T, D, y); });
                        }};
     };
+    // ROPE over T tokens of H heads of HD, rotating the first n_dims of each
+    // head, base 10000, beta_fast 32, beta_slow 1
     auto rope = [&](const char * name, int n_dims, int mode, int n_ctx_orig, float freq_scale, float ext_factor,
                     bool factors) {
         return op_case{name,
-                       [=](ggml_context * ctx, in_t & in) {
-                           ggml_tensor * x = input(ctx, in, GGML_TYPE_F32, HD, H, T);
-                           ggml_tensor * pos = input(ctx, in, GGML_TYPE_I32, T, 1, 1, "pos");
-                           ggml_tensor * ff = factors ? input(ctx, in, GGML_TYPE_F32, n_dims / 2, 1, 1, "factors") : nullptr;
-                           return ggml_rope_ext(ctx, x, pos, ff, n_dims, mode, n_ctx_orig, 10000.0f, freq_scale,
+                       [=](case_inputs & in) {
+                           ggml_tensor * x = in.rows(HD, H, T);
+                           ggml_tensor * p = in.positions(T);
+                           ggml_tensor * ff = factors ? in.factors(n_dims / 2) : nullptr;
+                           return ggml_rope_ext(in.ctx(), x, p, ff, n_dims, mode, n_ctx_orig, 10000.0f, freq_scale,
                                                 ext_factor, 1.0f, 32.0f, 1.0f);
                        },
-                       [=](const vin & v, const iin & p) {
-                           fvec y((size_t) (HD * H * T));
-                           orc_rope(v[0].data(), T, H, HD, p[0].data(), factors ? v[1].data() : nullptr, n_dims, mode,
-                                    n_ctx_orig, 10000.0f, freq_scale, ext_factor, 1.0f, 32.0f, 1.0f, y.data());
-                           return y;
+                       [=](const vin & v, const pin & p) {
+                           return answer(HD * H * T, [&](float * y) {
+                               orc_rope(v[0].data(), T, H, HD, p[0].data(), factors ? v[1].data() : nullptr, n_dims,
+                                        mode, n_ctx_orig, 10000.0f, freq_scale, ext_factor, 1.0f, 32.0f, 1.0f, y);
+                           });
                        }};
     };
 
     const op_case cases[] = {
-        {"rms_norm", [&](ggml_context * ctx, in_t & in) { return ggml_rms_norm(ctx, input(ctx, in, GGML_TYPE_F32, D, T), 1e-6f); },
-         [&](const vin & v, const iin &) {
-             fvec y((size_t) (D * T));
-             orc_rms_norm(v[0].data(), T, D, 1e-6f, y.data());
-             return y;
+        {"rms_norm", [&](case_inputs & in) { return ggml_rms_norm(in.ctx(), in.rows(D, T), 1e-6f); },
+         [&](const vin & v, const pin &) {
+             return answer(D * T, [&](float * y) { orc_rms_norm(v[0].data(), T, D, 1e-6f, y); });
          }},
         {"mul by a scale row",
-         [&](ggml_context * ctx, in_t & in) {
-             ggml_tensor * x = input(ctx, in, GGML_TYPE_F32, D, T);
-             return ggml_mul(ctx, x, input(ctx, in, GGML_TYPE_F32, D));
+         [&](case_inputs & in) {
+             ggml_tensor * x = in.rows(D, T);
+             return ggml_mul(in.ctx(), x, in.row(D));
          },
-         [&](const vin & v, const iin &) {
-             fvec y((size_t) (D * T));
-             orc_mul_row(v[0].data(), T, D, v[1].data(), y.data());
-             return y;
+         [&](const vin & v, const pin &) {
+             return answer(D * T, [&](float * y) { orc_mul_row(v[0].data(), T, D, v[1].data(), y); });
          }},
         {"add",
-         [&](ggml_context * ctx, in_t & in) {
-             ggml_tensor * x = input(ctx, in, GGML_TYPE_F32, D, T);
-             return ggml_add(ctx, x, input(ctx, in, GGML_TYPE_F32, D, T));
+         [&](case_inputs & in) {
+             ggml_tensor * a = in.rows(D, T);
+             return ggml_add(in.ctx(), a, in.rows(D, T));
          },
-         [&](const vin & v, const iin &) {
-             fvec y((size_t) (D * T));
-             orc_add(v[0].data(), v[1].data(), D * T, y.data());
-             return y;
+         [&](const vin & v, const pin &) {
+             return answer(D * T, [&](float * y) { orc_add(v[0].data(), v[1].data(), D * T, y); });
          }},
         {"add a bias row",
-         [&](ggml_context * ctx, in_t & in) {
-             ggml_tensor * x = input(ctx, in, GGML_TYPE_F32, D, T);
-             return ggml_add(ctx, x, input(ctx, in, GGML_TYPE_F32, D));
+         [&](case_inputs & in) {
+             ggml_tensor * x = in.rows(D, T);
+             return ggml_add(in.ctx(), x, in.row(D));
          },
-         [&](const vin & v, const iin &) {
-             fvec y((size_t) (D * T));
-             orc_add_row(v[0].data(), T, D, v[1].data(), y.data());
-             return y;
+         [&](const vin & v, const pin &) {
+             return answer(D * T, [&](float * y) { orc_add_row(v[0].data(), T, D, v[1].data(), y); });
          }},
-        {"scale and bias",
-         [&](ggml_context * ctx, in_t & in) { return ggml_scale_bias(ctx, input(ctx, in, GGML_TYPE_F32, D, T), 0.37f, 0.25f); },
-         [&](const vin & v, const iin &) {
-             fvec y((size_t) (D * T));
-             orc_scale(v[0].data(), D * T, 0.37f, 0.25f, y.data());
-             return y;
+        {"scale and bias", [&](case_inputs & in) { return ggml_scale_bias(in.ctx(), in.rows(D, T), 0.37f, 0.25f); },
+         [&](const vin & v, const pin &) {
+             return answer(D * T, [&](float * y) { orc_scale(v[0].data(), D * T, 0.37f, 0.25f, y); });
          }},
         glu_split("swiglu, split", GGML_GLU_OP_SWIGLU, ORC_GLU_SWIGLU),
         glu_split("geglu, split", GGML_GLU_OP_GEGLU, ORC_GLU_GEGLU),

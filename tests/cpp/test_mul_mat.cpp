@@ -4,8 +4,8 @@
 // Two bars. (1) The rigorous one: against an fp64 product of the SAME operands
 // the GPU multiplies (activations through the oracle's bfp16 encode/decode,
 // weights through the oracle's GGUF dequantiser and then bfp16), every output within
-// 1e-3*|r| + 2*K*2^-24*sum|a_k w_k| (bf16 products are exact in fp32, so only
-// the summation order differs). (2) The reference's own style: against the
+// 2*K*2^-24*sum|a_k w_k| (bf16 products are exact in fp32, so only the fp32
+// summation order may differ; no relative slack). (2) The reference's own style: against the
 // fp64 product of the raw operands, nrmse <= 1e-2 and cosine > 0.9999 (bfp16
 // activations carry 8-bit mantissas).
 //
@@ -101,7 +101,9 @@ static result judge(const case_spec & c, const std::vector<float> & got, const s
     double se = 0, ss = 0, dot = 0, ng = 0;
     for (size_t i = 0; i < r.size(); i++) {
         const double g = got[i];
-        const double bound = 1e-3 * std::fabs(r[i]) + 2.0 * (double) c.k * 0x1p-24 * absdot[i];
+        // fp32 summation order of exact bf16 products is the only allowed
+        // difference: no relative slack, so a systematic error shows
+        const double bound = 2.0 * (double) c.k * 0x1p-24 * absdot[i];
         const double e = std::fabs(g - r[i]);
         if (!(e <= bound)) res.ok_bound = false;
         res.worst = std::max(res.worst, bound > 0 ? e / bound : (e > 0 ? INFINITY : 0));

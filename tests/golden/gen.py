@@ -52,6 +52,18 @@ def make_data(n: int, seed: int) -> np.ndarray:
     return np.ldexp(x, e.astype(np.int32)).astype(np.float32)
 
 
+def wide_blocks(rows: int, k: int, seed: int, std: float = 1.0) -> np.ndarray:
+    """N(0, std) values [rows][k] with each 8-value block along k scaled by
+    2^U(-12, 12): products of two such operands span about 2^48, so fp32
+    partial sums of them are rarely exact and summing K in another order
+    (another split of K among workgroups) changes bits. Operands for tests
+    that claim two launches sum in the same order."""
+    rng = Rng(seed)
+    x = rng.normal(rows * k, 0.0, std).reshape(rows, k // 8, 8)
+    e = rng.ints(rows * (k // 8), -12, 12).reshape(rows, k // 8, 1).astype(np.int32)
+    return np.ldexp(x, e).reshape(rows, k).astype(np.float32)
+
+
 def edge_blocks() -> np.ndarray:
     """Blocks that take the encoder's special paths: all zeros and negative
     zeros, subnormal-only blocks (exponent byte 0), tiny normals (bytes 1..6,

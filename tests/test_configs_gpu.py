@@ -11,6 +11,8 @@ tests/test-mul-mat.cpp:101-125 and :140-157, and end to end on models).
   checks).
 * Configuration 3 (Qwen3-4B-shaped): two layers chained at a 2048-token chunk,
   the residual stream carried from launch to launch and layer to layer.
+* Configuration 2 (the SwiGLU triple, Q4_K, 1% of channels x20): fused
+  gate/up -> packed SwiGLU -> down as one chain.
 
 Matmuls meet the GEMM bar against fp64 sums over the same decoded operands on
 sampled rows: |g - r64| <= 2 K 2^-24 sum|a b| (the products are exact, so
@@ -168,6 +170,53 @@ def gate_up(z, oracle, m, f, k, wtype, seed, outlier_frac=0.0, outlier_scale=1.0
     u64, _ = oracle.mul_mat_f64(_wdec(z, oracle, z.convert_weight(wtype, up, f, k), f, k), ad)
     want = oracle.glu(SWIGLU, g64.astype(np.float32), u64.astype(np.float32))
     assert nrmse(hs, want) <= 1e-5
+
+
+# ---- configuration 2: the SwiGLU MUL_MAT triple ---------------------------------------------
+
+def test_config2_swiglu_triple(zest_gpu, oracle):
+    """BASELINE configuration 2 as one chain: 2048 tokens of N(0,1) with 1% of
+    the channels x20 -> the fused gate/up GEMM (Q4_K, 2560 -> 2 x 9728) ->
+    its SwiGLU, packed by its epilogue -> down (Q4_K, 9728 -> 2560). Every
+    stage is checked on sampled rows against the oracle on that stage's own
+    GPU input: the packs bit-exact with the oracle's encoder, the gate and up
+    sums (the fused launch's are those of the plain GEMM over the interleaved
+    weight, bit for bit) and the down projection within the GEMM bar with no
+    relative slack, and h within the host ops' bar of the oracle's SwiGLU."""
+    import torch
+    z = zest_gpu
+    m, H, F = 2048, 2560, 9728
+    x = _acts(m, H, 201, outlier_frac=0.01, outlier_scale=20.0)
+    a = z.pack_act_x(x)
+    gate, up = _raw(Q4_K, F, H, 202), _raw(Q4_K, F, H, 203)
+    wgu = z.convert_weight_gu(Q4_K, gate, up, F, H)
+    wdn = z.convert_weight(Q4_K, _raw(Q4_K, H, F, 204), H, F)
+    nf = _nf()
+    xo, h = z.gemm_glu(SWIGLU, a, m, wgu, F, H, h=True, nonfinite=nf)
+    y = z.gemm(xo, m, wdn, H, F, nonfinite=nf)
+    c = z.gemm(a, m, wgu, 2 * F, H).view(m, F // 32, 2, 32)
+    g = c[:, :, 0, :].reshape(m, F).contiguous()
+    u = c[:, :, 1, :].reshape(m, F).contiguous()
+    h_chain = z.glu(SWIGLU, g, u, F)
+    torch.cuda.synchronize()
+    assert int(nf.item()) == 0
+    assert torch.equal(h.view(torch.int32), h_chain.view(torch.int32))
+    rows = _rows(m)
+    ad = _pack_check(z, oracle, x, a, rows)
+    # gate and up against fp64 sums over the same decoded operands
+    g64, gab = oracle.mul_mat_f64(_wdec(z, oracle, z.convert_weight(Q4_K, gate, F, H), F, H), ad)
+    u64, uab = oracle.mul_mat_f64(_wdec(z, oracle, z.convert_weight(Q4_K, up, F, H), F, H), ad)
+    _check(g.cpu().numpy()[rows], g64, gab, H)
+    _check(u.cpu().numpy()[rows], u64, uab, H)
+    hs = h.cpu().numpy()[rows]
+    e = nrmse(hs, oracle.glu(SWIGLU, g64.astype(np.float32), u64.astype(np.float32)))
+    assert e <= 1e-5, e
+    # the down projection's operand is the encoding of h, and its product
+    dd = z.expanded_to_rows(xo.cpu().numpy(), m, F)[rows]
+    assert np.array_equal(dd.view(np.uint32), oracle.decode_rows(oracle.encode_rows(hs)).view(np.uint32))
+    r64, ab = oracle.mul_mat_f64(_wdec(z, oracle, wdn, H, F), dd)
+    ratio, maxrel = _check(y.cpu().numpy()[rows], r64, ab, F)
+    print(f"config 2 triple: down bound use {ratio:.2f}, max rel {maxrel:.2e}, SwiGLU nrmse {e:.2e}")
 
 
 # ---- configuration 5: 27B-class layer at a 4096-token chunk --------------------------------

@@ -6,10 +6,13 @@ Its result must be bit-exact with the unfused chain over the same GEMM:
 zest_gemm of the interleaved weight (pinned against the oracle in
 test_gemm_gpu), whose gate and up columns go through zest_glu (pinned in
 test_ops_gpu) and zest_pack_act_x (bit-exact with the oracle's encoder in
-test_pack_gpu). Both launches split the same tiles the same way, so each
-output is summed over K in the same order and every float matches (the
-shapes avoid 2F a multiple of 160, where the plain launch can take one
-unsplit round of 160-row tiles that the fused one cannot). Against
+test_pack_gpu). The fused launch splits K among workgroups exactly as the
+plain launch of its 2F columns does (whatever tile shapes the two take), so
+each output is summed over K in the same order and every float matches. The
+bit-exact tests that could miss a change of summation order use operands
+whose 8-value blocks span 2^+-12 (fp32 partial sums of their products are
+rarely exact), and a control shows that with them another K partition does
+change bits. Against
 the chain the reference runs unfused (separate gate and up GEMMs, whose
 launches can split K differently) and against the oracle, h must meet the
 host ops' bar (nrmse <= 1e-5, tests/test-host-ops.cpp).
@@ -18,7 +21,7 @@ from __future__ import annotations
 
 import numpy as np
 import pytest
-from gen import Rng
+from gen import Rng, wide_blocks
 from helpers import load_quant, nrmse
 
 pytestmark = pytest.mark.gpu
@@ -93,6 +96,63 @@ def test_gemm_glu_matches_unfused_swiglu(zest_gpu, oracle, wtype, M, F, K):
     # and h is the oracle's SwiGLU of the gate and up products
     gs, us = g.cpu().numpy()[rows], u.cpu().numpy()[rows]
     assert nrmse(hs, oracle.glu(2, gs, us)) <= 1e-5  # tests/test-host-ops.cpp's bar
+
+
+def _wide_case(z, M, F, K, seed):
+    """Order-sensitive operands: activations and F32 gate/up weights with
+    8-value blocks spread over 2^+-12."""
+    x = wide_blocks(M, K, seed)
+    gate = _dev(wide_blocks(F, K, seed + 1, 0.05).view(np.uint8))
+    up = _dev(wide_blocks(F, K, seed + 2, 0.05).view(np.uint8))
+    a = z.pack_act_x(_dev(x))
+    return a, z.convert_weight_gu(0, gate, up, F, K)
+
+
+def test_order_sensitive_operands_show_another_k_split(zest_gpu):
+    # The control for the bit-exact tests below: with these operands the same
+    # GEMM summed over another partition of K (two launches over the halves
+    # of K, added in fp32) differs from the one-launch sums in many outputs,
+    # so a fused launch that split K otherwise than the plain one would fail
+    # its bit-exact test. (With N(0,1) activations and small weights, every
+    # fp32 partial sum is exact and no order change would show.)
+    import torch
+    M, N, K = 512, 512, 4096
+    x = wide_blocks(M, K, 61)
+    w = wide_blocks(N, K, 62, 0.05)
+    a = zest_gpu.pack_act_x(_dev(x))
+    full = zest_gpu.gemm(a, M, zest_gpu.convert_weight(0, _dev(w.view(np.uint8)), N, K), N, K)
+    h = K // 2
+    halves = None
+    for lo in (0, h):
+        ah = zest_gpu.pack_act_x(_dev(np.ascontiguousarray(x[:, lo:lo + h])))
+        wh = zest_gpu.convert_weight(0, _dev(np.ascontiguousarray(w[:, lo:lo + h]).view(np.uint8)), N, h)
+        part = zest_gpu.gemm(ah, M, wh, N, h)
+        halves = part if halves is None else halves + part
+    torch.cuda.synchronize()
+    differ = float((full.view(torch.int32) != halves.view(torch.int32)).float().mean())
+    assert differ > 0.1, differ
+    assert torch.allclose(full, halves, rtol=1e-4, atol=float(full.abs().max()) * 1e-5)
+
+
+@pytest.mark.parametrize("M,F,K", [
+    (520, 896, 1536),   # plain launch as 64x64 tiles, unsplit
+    (2048, 1024, 8192),  # few tiles, long K: split
+    (256, 512, 4096),
+    (2048, 6144, 4096),  # three rounds: persistent workgroups
+    (1500, 4096, 4096),
+])
+def test_gemm_glu_bit_exact_order_sensitive(zest_gpu, M, F, K):
+    # the fused gate/up sums are the plain GEMM's over the interleaved weight
+    # bit for bit, on operands where a change of K summation order shows
+    import torch
+    a, wgu = _wide_case(zest_gpu, M, F, K, M + F + K)
+    x_ref, h_ref, _, _ = unfused(zest_gpu, 2, a, M, wgu, F, K)
+    nf = torch.zeros(1, dtype=torch.int32, device="cuda")
+    xo, h = zest_gpu.gemm_glu(2, a, M, wgu, F, K, h=True, nonfinite=nf)
+    torch.cuda.synchronize()
+    assert int(nf.item()) == 0
+    assert torch.equal(h.view(torch.int32), h_ref.view(torch.int32)), (M, F, K)
+    assert torch.equal(xo, x_ref), (M, F, K)
 
 
 @pytest.mark.parametrize("M,F,K", [

@@ -8,7 +8,7 @@ from __future__ import annotations
 
 import numpy as np
 import pytest
-from gen import Rng, make_data
+from gen import Rng, make_data, wide_blocks
 from helpers import gemm_check, load_quant
 
 pytestmark = pytest.mark.gpu
@@ -266,11 +266,12 @@ def test_gemm_rounds_equal_one_round_launches(zest_gpu, oracle, M, ns, K):
     # next tile's first steps during the current one. Every output is summed
     # over K in the same order as in a launch of one round, so the group
     # launch equals, bit for bit, each weight launched alone (at most one
-    # round), and it meets the oracle's bar.
+    # round), and it meets the oracle's bar. The operands' blocks spread over
+    # 2^+-12, so a change of summation order would show.
     import torch
-    x = Rng(M + K).normal(M * K).reshape(M, K)
+    x = wide_blocks(M, K, M + K)
     a = zest_gpu.pack_act_x(_dev(x))
-    ws = [zest_gpu.convert_weight(0, _dev(Rng(n + i + K).normal(n * K, 0, 0.02).reshape(n, K).view(np.uint8)), n, K)
+    ws = [zest_gpu.convert_weight(0, _dev(wide_blocks(n, K, n + i + K, 0.02).view(np.uint8)), n, K)
           for i, n in enumerate(ns)]
     nf = torch.zeros(1, dtype=torch.int32, device="cuda")
     outs = zest_gpu.gemm_group(a, M, ws, ns, K, nonfinite=nf)
@@ -282,8 +283,8 @@ def test_gemm_rounds_equal_one_round_launches(zest_gpu, oracle, M, ns, K):
     rows = np.unique(np.concatenate([np.linspace(0, M - 1, 32).astype(int), [255, 256, M - 1]]))
     ad = decoded_act(zest_gpu, oracle, a, M, K)[rows]
     r64, ab = oracle.mul_mat_f64(decoded(zest_gpu, oracle, ws[-1], ns[-1], K), ad)
-    worst, maxrel = gemm_check(outs[-1].cpu().numpy()[rows], r64, ab, K)
-    assert worst <= 1.0 and maxrel <= 1e-3
+    worst, _ = gemm_check(outs[-1].cpu().numpy()[rows], r64, ab, K)
+    assert worst <= 1.0
 
 
 def test_gemm_part_round_as_half_tiles(zest_gpu, oracle):
@@ -291,10 +292,11 @@ def test_gemm_part_round_as_half_tiles(zest_gpu, oracle):
     # CUs and half of another; the launch runs the last 128 tiles as 256 of
     # 128 x 128. Each output is summed over K in the same order either way, so
     # the result equals, bit for bit, two launches over the column halves (192
-    # whole tiles each), and the oracle within the GEMM bar.
+    # whole tiles each), and the oracle within the GEMM bar. Order-sensitive
+    # operands (blocks spread over 2^+-12).
     M, N, K = 2048, 6144, 512
-    x = Rng(3).normal(M * K).reshape(M, K)
-    w = Rng(4).normal(N * K, 0, 0.02).reshape(N, K)
+    x = wide_blocks(M, K, 3)
+    w = wide_blocks(N, K, 4, 0.02)
     c, nf, a, wp = run_gemm(zest_gpu, x, 0, w.view(np.uint8), N)
     assert nf == 0
     half = N // 2
@@ -305,8 +307,8 @@ def test_gemm_part_round_as_half_tiles(zest_gpu, oracle):
     assert np.array_equal(c.view(np.uint32), both.view(np.uint32))
     rows = np.unique(np.concatenate([np.linspace(0, M - 1, 40).astype(int), [1024, 1151, 1152, 1279, 2047]]))
     r64, ab = oracle.mul_mat_f64(decoded(zest_gpu, oracle, wp, N, K), decoded_act(zest_gpu, oracle, a, M, K)[rows])
-    worst, maxrel = gemm_check(c[rows], r64, ab, K)
-    assert worst <= 1.0 and maxrel <= 1e-3
+    worst, _ = gemm_check(c[rows], r64, ab, K)
+    assert worst <= 1.0
 
 
 def test_gemm_group_rejects_bad_counts(zest_gpu):
@@ -388,10 +390,12 @@ def test_gemm_random_shapes(zest_gpu, oracle):
         a = zest_gpu.pack_act_x(_dev(x))
         kind = case % 4
         if kind == 3:
+            # order-sensitive operands: blocks spread over 2^+-12
             F = max(32, N // 64 * 32)
-            up = rng.normal(0, 0.05, (F, K)).astype(np.float32)
-            wgu = zest_gpu.convert_weight_gu(0, _dev(np.ascontiguousarray(w[:F]).view(np.uint8)),
-                                             _dev(up.view(np.uint8)), F, K)
+            x = wide_blocks(M, K, 1000 + case)
+            a = zest_gpu.pack_act_x(_dev(x))
+            gate, up = wide_blocks(F, K, 2000 + case, 0.05), wide_blocks(F, K, 3000 + case, 0.05)
+            wgu = zest_gpu.convert_weight_gu(0, _dev(gate.view(np.uint8)), _dev(up.view(np.uint8)), F, K)
             c = zest_gpu.gemm(a, M, wgu, 2 * F, K).view(M, F // 32, 2, 32)
             h_ref = zest_gpu.glu(2, c[:, :, 0, :].reshape(M, F).contiguous(), c[:, :, 1, :].reshape(M, F).contiguous(), F)
             nf = torch.zeros(1, dtype=torch.int32, device="cuda")
@@ -426,3 +430,51 @@ def test_gemm_random_shapes(zest_gpu, oracle):
         bound = 2.0 * K * 2.0 ** -24 * ab + sl
         assert np.isfinite(got[rows]).all() and (err <= bound).all(), (kind, M, N, K, float((err / bound).max()))
 
+
+
+def test_gemm_output_bands(zest_gpu, oracle):
+    # an output whose span passes 2 GiB (the all-logits projection: vocab
+    # 151,936 at a 4096-token ubatch, 2.49 GB of fp32) runs as launches over
+    # bands of 3328 rows (13 tiles of 256 rows under 2 GiB each); rows on both
+    # sides of the band edge and the ragged end are checked against the
+    # oracle, the residual epilogue's bands bit for bit against the plain
+    # bands plus the add, and a group launch with a narrow weight beside the
+    # wide one against the oracle
+    import torch
+    quant = load_quant()
+    M, N, K = 4096, 151936, 512
+    assert M * N * 4 >= 2 ** 31
+    x = Rng(151).normal(M * K).reshape(M, K)
+    w = Rng(152).normal(N * K, 0, 0.02).reshape(N, K)
+    raw = quant.quantize(8, torch.from_numpy(w).cuda())
+    a = zest_gpu.pack_act_x(_dev(x))
+    wp = zest_gpu.convert_weight(8, raw, N, K)
+    del raw
+    nf = torch.zeros(1, dtype=torch.int32, device="cuda")
+    c = zest_gpu.gemm(a, M, wp, N, K, nonfinite=nf)
+    torch.cuda.synchronize()
+    assert int(nf.item()) == 0
+    rows = np.array([0, 1, 1000, 3326, 3327, 3328, 3329, 3583, 3584, 4094, 4095])
+    got = c[torch.from_numpy(rows).cuda()].cpu().numpy()
+    ad = decoded_act(zest_gpu, oracle, a, M, K)[rows]
+    wd = decoded(zest_gpu, oracle, wp, N, K)
+    r64, ab = oracle.mul_mat_f64(wd, ad)
+    del wd
+    worst, maxrel = gemm_check(got, r64, ab, K)
+    assert worst <= 1.0, worst
+    assert maxrel <= 1e-3, maxrel
+    # the residual epilogue over the same bands: acc + res, added once
+    res = torch.empty_like(c).normal_()
+    out = zest_gpu.gemm_residual(a, M, wp, N, K, res, nonfinite=nf)
+    torch.cuda.synchronize()
+    assert int(nf.item()) == 0
+    sel = torch.from_numpy(rows).cuda()
+    assert torch.equal(out[sel].view(torch.int32), (c[sel] + res[sel]).view(torch.int32))
+    del out, res
+    # a group: the wide weight beside a narrow one, banded on the widest row
+    wn = zest_gpu.convert_weight(8, quant.quantize(8, torch.from_numpy(w[:512]).cuda()), 512, K)
+    outs = zest_gpu.gemm_group(a, M, [wn, wp], [512, N], K)
+    torch.cuda.synchronize()
+    assert gemm_check(outs[1][sel].cpu().numpy(), r64, ab, K)[0] <= 1.0
+    n64, nab = oracle.mul_mat_f64(oracle.decode_rows(zest_gpu.tiles_to_blocks(wn.cpu().numpy(), 512, K)), ad)
+    assert gemm_check(outs[0][sel].cpu().numpy(), n64, nab, K)[0] <= 1.0
