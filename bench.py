@@ -502,6 +502,12 @@ def main() -> int:
     names = {v[0]: k for k, v in GGUF_BLOCKS.items()}
     convert = [convert_rate(z, names[t]) for t in dict.fromkeys((cfg.ffn_type, cfg.down_type))]
     pack = pack_rates(z) + [norm_rate(z)]
+    # each beside the ceiling it is held against: a device copy moving the
+    # same bytes, on rotating sets in the same run
+    for r in convert + pack:
+        c = copy_rate(r["bytes"])
+        r["copy_frac"] = c["frac"]
+        r["of_copy"] = round(c["us"] / r["us"], 3)
     line = {
         "metric": METRIC,
         "value": round(value, 2),

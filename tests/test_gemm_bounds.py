@@ -213,3 +213,37 @@ def test_glu_epilogue_columns_stay_inside_the_operand(F):
                 c0 = n0 // 2 + wn * HW
                 if c0 < Fp:
                     assert c0 + HW <= Fp, (F, BN, WN, n0, wn)
+
+
+def band_rows(ld):
+    """gemm.hip's band_rows: whole 256-row tiles of an output `ld` floats a
+    row whose byte span stays under 2 GiB (0 if not even 256 rows fit)."""
+    return (2 ** 31 - 1) // (ld * 4) // 256 * 256
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 151936, 512), (4096, 151936, 2560), (8192, 262144, 5120),
+                                   (3329, 160000, 64), (10000, 70000, 1024), (5000, 2097136, 256)])
+def test_output_bands_stay_inside_operands(M, N, K):
+    # A launch whose output span reaches 2 GiB runs as one launch a band of
+    # rows (band_of): the band's activations start at its first row's 32-row
+    # group (the K-step stride stays the whole operand's) and its output at
+    # its first row. The bands cover every row once, each band's output span
+    # is under 2 GiB, and every A fragment a band's tiles load lies inside
+    # the whole expanded operand, for every tile shape.
+    band = band_rows(N)
+    assert band >= 256
+    bands = [(r0, min(band, M - r0)) for r0 in range(0, M, band)]
+    assert sum(rows for _, rows in bands) == M and bands[0][0] == 0
+    assert all(r0 % 256 == 0 and rows * N * 4 < 2 ** 31 for r0, rows in bands)
+    assert len(bands) > 1 or M * N * 4 < 2 ** 31
+    nk = k_steps(K)
+    ks = rows_pad(M) // 32 * XGROUP_BYTES
+    a_size = ks * nk
+    for r0, rows in bands:
+        shift = r0 // 32 * XGROUP_BYTES
+        for BM, _, CWM in CONFIGS:
+            WM, TI = BM // CWM, BM // CWM // 32
+            top = max((tm * BM // 32 + wm * WM // 32 + TI - 1) * XGROUP_BYTES
+                      for tm in range((rows + BM - 1) // BM) for wm in range(CWM))
+            a_hi = shift + top + 31 * 32 + 16 + 3 * XSUB_BYTES + 16 + (nk - 1) * ks
+            assert a_hi <= a_size, (M, N, K, r0, rows, BM)
