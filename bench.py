@@ -242,6 +242,88 @@ def hbm_kernels(args) -> int:
     return 0
 
 
+def operand_activity(args) -> int:
+    """The same GEMM launches on operands of different bit activity: random
+    bytes, the workload's own kind (N(0,1) activations against quantised
+    N(0, 0.02) Q4_K weights), and operands whose mantissas are all zero (the
+    matrix core's inputs then do not toggle). The kernel, shapes, tiles and
+    memory traffic are the same in every case; only the data's switching
+    activity, and so the chip's power draw and clock, differ. One JSON line
+    per shape, microseconds and TFLOP/s per case."""
+    import torch
+    z = load_pkg()
+    import ggml_xdna_amd.quant as quant
+    torch.cuda.set_device(0)
+    z.init(0)
+    for (m, n, k) in ACTIVITY_SHAPES:
+        g = torch.Generator(device="cuda").manual_seed(0)
+        a_x = z.pack_act_x(torch.randn((m, k), device="cuda", generator=g))
+        a_zero = z.pack_act_x(torch.zeros((m, k), device="cuda"))
+        w_rand = torch.randint(0, 256, (z.bfp16_bytes(n, k),), dtype=torch.uint8, device="cuda", generator=g)
+        tiles = w_rand.view(-1, 1152)
+        tiles[:, 1024:] = torch.randint(118, 128, (tiles.shape[0], 128), dtype=torch.uint8, device="cuda", generator=g)
+        w_q4k = z.convert_weight(12, quant.quantize(12, torch.randn((n, k), device="cuda", generator=g) * 0.02), n, k)
+        w_zero = w_rand.clone()
+        w_zero.view(-1, 1152)[:, :1024] = 0  # mantissas zero, exponent bytes kept
+        c = torch.empty((m, n), device="cuda")
+        res = {}
+        operands = {"random bytes": (a_x, w_rand), "workload data": (a_x, w_q4k), "W mantissas zero": (a_x, w_zero),
+                    "A zero": (a_zero, w_q4k), "workload data again": (a_x, w_q4k)}
+        for name in ACTIVITY_CASES:
+            a, w = operands[name]
+            us = _timed(lambda i: z.gemm(a, m, w, n, k, out=c), activity_reps(m, n, k))
+            res[name] = {"us": round(us, 1), "TFLOP/s": round(2.0 * m * n * k / us / 1e6, 1)}
+        print(json.dumps({"shape": [m, n, k], "cases": res}), flush=True)
+    return 0
+
+
+ACTIVITY_SHAPES = ((8192, 8192, 8192), (2048, 19456, 2560), (2048, 2560, 9728))
+ACTIVITY_CASES = ("random bytes", "workload data", "W mantissas zero", "A zero", "workload data again")
+
+
+def activity_reps(m: int, n: int, k: int) -> int:
+    return 10 if m * n * k > 2e11 else 40
+
+
+def activity_summary(pmc_dir: str, trace_dir: str) -> int:
+    """Per shape and case of --operand-activity under rocprofv3: the GEMM's
+    average duration (kernel trace), its clock (GRBM_GUI_ACTIVE, summed over
+    the 8 XCDs, over the duration) and the MFMA-busy share of the SIMD cycles
+    (SQ_VALU_MFMA_BUSY_CYCLES), over each case's timed launches."""
+    import csv
+    import glob
+    from collections import defaultdict
+    per = defaultdict(float)
+    for r in _counter_rows(pmc_dir):
+        if "gemm_kernel" in r["Kernel_Name"]:
+            per[(int(r["Dispatch_Id"]), r["Counter_Name"])] += float(r["Counter_Value"])
+    ids = sorted({d for d, _ in per})
+    durs = []
+    for f in glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True):
+        rows = sorted(csv.DictReader(open(f)), key=lambda r: int(r["Start_Timestamp"]))
+        durs += [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3 for r in rows
+                 if "gemm_kernel" in r["Kernel_Name"]]
+    sizes = [1 + activity_reps(*sh) for sh in ACTIVITY_SHAPES for _ in ACTIVITY_CASES]
+    if len(ids) != sum(sizes) or len(durs) != sum(sizes):
+        print(f"expected {sum(sizes)} GEMM dispatches, found {len(ids)} counted and {len(durs)} traced",
+              file=sys.stderr)
+        return 1
+    out, at = [], 0
+    for sh in ACTIVITY_SHAPES:
+        m, n, k = sh
+        for case in ACTIVITY_CASES:
+            sel = range(at + 1, at + 1 + activity_reps(*sh))  # the warm launch left out
+            at += 1 + activity_reps(*sh)
+            us = sum(durs[i] for i in sel) / len(sel)
+            xcd = sum(per[(ids[i], "GRBM_GUI_ACTIVE")] for i in sel) / len(sel) / 8.0
+            busy = sum(per[(ids[i], "SQ_VALU_MFMA_BUSY_CYCLES")] for i in sel) / len(sel)
+            out.append({"shape": list(sh), "case": case, "us": round(us, 1),
+                        "TFLOP/s": round(2.0 * m * n * k / us / 1e6, 1), "clock_ghz": round(xcd / (us * 1e3), 3),
+                        "mfma_busy_pct": round(100.0 * busy / (xcd * 1024), 1)})
+    print(json.dumps(out, indent=1))
+    return 0
+
+
 CALIB_FLOATS = 64 << 20  # the calibration kernel's floats: 256 MiB each way
 
 
@@ -421,11 +503,19 @@ def main() -> int:
     ap.add_argument("--traffic-probe", action="store_true", help="one step and the calibration kernel, for rocprofv3")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
     ap.add_argument("--hbm", action="store_true", help="HBM rates of the converter (every type) and the pack")
+    ap.add_argument("--operand-activity", action="store_true",
+                    help="the same GEMM launches on random, workload and all-zero operands (power sensitivity)")
+    ap.add_argument("--activity-summary", nargs=2, metavar=("PMC_DIR", "TRACE_DIR"),
+                    help="clock and MFMA busy per case from rocprofv3 runs of --operand-activity")
     ap.add_argument("--counter-summary", nargs=4, metavar=("MFMA_DIR", "FETCH_DIR", "WRITE_DIR", "TRACE_DIR"),
                     help="per GEMM launch kind: time, MFMA busy, clock, HBM bytes from rocprofv3 runs of --traffic-probe")
     args = ap.parse_args()
     if args.hbm:
         return hbm_kernels(args)
+    if args.operand_activity:
+        return operand_activity(args)
+    if args.activity_summary:
+        return activity_summary(*args.activity_summary)
     if args.counter_summary:
         return counter_summary(args)
     if args.traffic_summary:

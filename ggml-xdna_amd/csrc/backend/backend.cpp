@@ -155,7 +155,8 @@ struct piece_plan;
 struct context {
     hipStream_t stream = nullptr;  // compute
     hipStream_t loader = nullptr;  // weight conversion at load
-    uint32_t * nonfinite = nullptr;
+    uint32_t * nonfinite = nullptr;       // device word the kernels OR 1 into
+    uint32_t * nonfinite_host = nullptr;  // pinned host copy, read after each piece's synchronize
 
     struct weight_entry {
         void * packed = nullptr;
@@ -188,7 +189,8 @@ struct context {
 
     bool init(std::string & err) {
         if (hipSetDevice(device_index()) != hipSuccess || hipStreamCreateWithFlags(&stream, hipStreamNonBlocking) ||
-            hipStreamCreateWithFlags(&loader, hipStreamNonBlocking) || hipMalloc(&nonfinite, 256)) {
+            hipStreamCreateWithFlags(&loader, hipStreamNonBlocking) || hipMalloc(&nonfinite, 256) ||
+            hipHostMalloc(&nonfinite_host, sizeof(uint32_t), hipHostMallocDefault)) {
             err = "cannot create streams on the device";
             return false;
         }
@@ -349,6 +351,7 @@ context::~context() {
     }
     for (block & b : blocks) (void) hipFree(b.p);
     if (nonfinite) (void) hipFree(nonfinite);
+    if (nonfinite_host) (void) hipHostFree(nonfinite_host);
     if (stream) (void) hipStreamDestroy(stream);
     if (loader) (void) hipStreamDestroy(loader);
 }
@@ -934,6 +937,10 @@ struct piece {
         for (const pending_out & o : host_outs)
             if (hipMemcpyAsync(o.t->data, o.dev, nbytes(o.t), hipMemcpyDeviceToHost, ctx.stream) != hipSuccess)
                 return fail("copying a result to host memory failed");
+        // the non-finite flag comes back with the piece's one synchronize
+        if (hipMemcpyAsync(ctx.nonfinite_host, ctx.nonfinite, sizeof(uint32_t), hipMemcpyDeviceToHost, ctx.stream) !=
+            hipSuccess)
+            return fail("reading the non-finite flag failed");
         return true;
     }
 };
@@ -974,11 +981,7 @@ ggml_status graph_compute(ggml_backend_t backend, ggml_cgraph * cgraph) {
     const hipError_t se = hipStreamSynchronize(ctx.stream);
     const auto t3 = clock::now();
     if (ok && se != hipSuccess) ok = p.fail(std::string("the GPU reported ") + hipGetErrorString(se));
-    if (ok) {
-        uint32_t nf = 0;
-        if (hipMemcpy(&nf, ctx.nonfinite, sizeof(nf), hipMemcpyDeviceToHost) != hipSuccess || nf)
-            ok = p.fail("the results held NaN or infinity");
-    }
+    if (ok && *ctx.nonfinite_host) ok = p.fail("the results held NaN or infinity");
     ctx.compute_ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     ctx.pieces++;
     static const int64_t trace_level = env_int("GGML_XDNA_TRACE", 0);
