@@ -63,22 +63,28 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // w / CWM); NP/64 producer waves (as many as the consumers' row blocks by
 // default). LDS holds the expanded W ring; after the K loop each consumer
 // wave uses WM x WN floats of it for its epilogue. MINB workgroups a CU at
-// least (the launch bound).
-template <int BM_, int BN_, int CWM_, int NP_ = 64 * CWM_, int MINB_ = 1, int CWN_ = 1, int NP1_ = 0>
+// least (the launch bound). KG K-groups: the workgroup holds KG copies of
+// these waves, each with a ring of its own, and K-group g takes the g-th of
+// KG equal runs of the tile's K-steps; the groups' sums are added in LDS,
+// in group order (run_tile).
+template <int BM_, int BN_, int CWM_, int NP_ = 64 * CWM_, int MINB_ = 1, int CWN_ = 1, int NP1_ = 0, int KG_ = 1>
 struct gemm_cfg {
-    static constexpr int BM = BM_, BN = BN_, CWM = CWM_, CWN = CWN_, MINB = MINB_;
+    static constexpr int BM = BM_, BN = BN_, CWM = CWM_, CWN = CWN_, MINB = MINB_, KG = KG_;
     static constexpr int NC = 64 * CWM * CWN;  // consumer threads
     static constexpr int NP = NP_;             // producer threads
     static constexpr int NP1 = NP1_;           // of them, the last NP1 take one W unit each, not two
-    static constexpr int NT = NC + NP;
+    static constexpr int NW = (NC + NP) / 64;  // waves of a K-group
+    static constexpr int NT = KG * (NC + NP);
     static constexpr int WM = BM / CWM, WN = BN / CWN;
     static constexpr int TI = WM / 32, TJ = WN / 32;
     static constexpr int NP2 = NP - NP1;    // producer threads of two W units (two blocks each) a K-step
     static constexpr int ROWB = 128;        // LDS bytes per row (64 bf16)
     static constexpr int STAGE = BN * ROWB;
     static constexpr int STAGES = 3;
-    static constexpr size_t LDS_BYTES =
-        (size_t) STAGES * STAGE > (size_t) BM * BN * 4 ? (size_t) STAGES * STAGE : (size_t) BM * BN * 4;
+    static constexpr size_t RING = (size_t) STAGES * STAGE;
+    // K-group g's ring at g * RING; after the K loop, the epilogue regions
+    // of group 0's waves in [0, BM*BN*4) and group g's sums at g * BM*BN*4
+    static constexpr size_t LDS_BYTES = KG * (RING > (size_t) BM * BN * 4 ? RING : (size_t) BM * BN * 4);
     // a persistent launch: the GLU epilogue's staging (WM rows of 16 TJ + 4
     // floats a wave) above the ring
     static constexpr size_t LDS_APART = (size_t) STAGES * STAGE + (size_t) (NC / 64) * WM * (16 * TJ + 4) * 4;
@@ -719,13 +725,35 @@ __device__ inline int xcd_order(int b, int n) {
 }
 
 // One output tile (rows m0.., columns n0.. of weight W), over K-steps
-// [k0, k0 + ns); with SPLIT, unit `split` of tile t.
+// [k0, k0 + ns); with SPLIT, unit `split` of tile t. With K-groups (C::KG >
+// 1; ns a multiple of KG), group g runs steps [k0 + g*ns/KG, k0 +
+// (g+1)*ns/KG) on its own ring, the groups meet the same barriers step for
+// step, and after the K loop every wave meets one more: groups 1.. have left
+// their sums in LDS, and group 0 adds them in group order (((s0 + s1) + s2)
+// + ...) before the split-K fixup and the epilogue. A group's waves take
+// their roles rotated by g * NC/64, so that with waves placed on SIMDs in
+// turn each SIMD holds consumers and producers alike.
 template <class C, int EPI, bool SPLIT>
 __device__ inline void run_tile(const gemm_params & p, uint8_t * smem, const gemm_weight & W, int64_t m0, int64_t n0,
                                 int k0, int ns, int t, int split) {
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int grp = 0, wave, tid;
+    if constexpr (C::KG > 1) {
+        grp = __builtin_amdgcn_readfirstlane((int) threadIdx.x / (C::NC + C::NP));
+        const int wig = __builtin_amdgcn_readfirstlane(((int) threadIdx.x % (C::NC + C::NP)) >> 6);
+        wave = (wig + grp * (C::NC / 64)) % C::NW;
+        tid = wave * 64 + ((int) threadIdx.x & 63);
+    } else {
+        tid = threadIdx.x;
+        wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    }
+    const int lane = tid & 63;
     const int nk = p.nk;
+    uint8_t * const base = smem;
+    if constexpr (C::KG > 1) {
+        smem += grp * C::RING;
+        ns /= C::KG;
+        k0 += grp * ns;
+    }
     if (wave >= C::NC / 64) {
         const int job = tid - C::NC;
         // uniform, but the tile arithmetic can leave it in a vector register,
@@ -736,10 +764,12 @@ __device__ inline void run_tile(const gemm_params & p, uint8_t * smem, const gem
             if (job >= C::NP2) {  // whole waves: NP2 % 64 == 0
                 const producer<C, 1> pr(W.w, (int64_t) W.w_kstride * nk, job - C::NP2);
                 produce<C, 1>(pr, smem, w0, W.w_kstride, ns, nk - 1 - k0);
+                if constexpr (C::KG > 1) bare_barrier();  // the K-groups' sums
                 return;
             }
         const producer<C, 2> pr(W.w, (int64_t) W.w_kstride * nk, job);
         produce<C, 2>(pr, smem, w0, W.w_kstride, ns, nk - 1 - k0);
+        if constexpr (C::KG > 1) bare_barrier();  // the K-groups' sums
         return;
     }
 
@@ -771,6 +801,44 @@ __device__ inline void run_tile(const gemm_params & p, uint8_t * smem, const gem
         // the loads of steps past the end are still in flight
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     }
+    smem = base;
+    if constexpr (C::KG > 1) {
+        // every group is past its K loop's last barrier, so no ring is read
+        // or written any more except by a consumer's unused read ahead
+        if (grp > 0) {
+            uint8_t * sums = smem + (size_t) grp * C::BM * C::BN * 4 + wave * (C::WM * C::WN * 4);
+#pragma unroll
+            for (int i = 0; i < C::TI; i++)
+#pragma unroll
+                for (int j = 0; j < C::TJ; j++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+                        *reinterpret_cast<float4 *>(sums + ((i * C::TJ + j) * 4 + q) * 1024 + lane * 16) =
+                            make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                        acc[i][j][4 * q + 3]);
+            wait_lgkm0();
+            bare_barrier();
+            return;
+        }
+        bare_barrier();
+#pragma unroll
+        for (int g = 1; g < C::KG; g++) {
+            const uint8_t * sums = smem + (size_t) g * C::BM * C::BN * 4 + wave * (C::WM * C::WN * 4);
+#pragma unroll
+            for (int i = 0; i < C::TI; i++)
+#pragma unroll
+                for (int j = 0; j < C::TJ; j++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const float4 x =
+                            *reinterpret_cast<const float4 *>(sums + ((i * C::TJ + j) * 4 + q) * 1024 + lane * 16);
+                        acc[i][j][4 * q] += x.x;
+                        acc[i][j][4 * q + 1] += x.y;
+                        acc[i][j][4 * q + 2] += x.z;
+                        acc[i][j][4 * q + 3] += x.w;
+                    }
+        }
+    }
     if (SPLIT && !fixup<C>(acc, p, smem, t, split, wave, lane)) return;
     epilogue<C, EPI>(acc, p, smem, W, m0, n0, wave, wm, wn, lane);
 }
@@ -798,7 +866,8 @@ __global__ __launch_bounds__(C::NT, C::MINB) void gemm_kernel(const gemm_params 
 // workgroups it is given), then the halves.
 template <class CB, class CS, int EPI>
 __global__ __launch_bounds__(CB::NT, 1) void gemm_kernel_mixed(const gemm_params p) {
-    static_assert(CB::NT == CS::NT && CS::BM * 2 == CB::BM && CS::BN == CB::BN, "halves of the big tiles");
+    static_assert(CB::NT == CS::NT && CS::BM * 2 == CB::BM && CS::BN == CB::BN && CB::KG == 1 && CS::KG == 1,
+                  "halves of the big tiles");
     extern __shared__ uint4 smem_u4[];
     uint8_t * smem = reinterpret_cast<uint8_t *>(smem_u4);
     const int b = (int) blockIdx.x, per_xcd = p.nbig / 8, i = b / 8;
@@ -830,6 +899,7 @@ __global__ __launch_bounds__(CB::NT, 1) void gemm_kernel_mixed(const gemm_params
 // the registers).
 template <class C, int EPI>
 __global__ __launch_bounds__(C::NT, 1) void gemm_kernel_tiles(const gemm_params p) {
+    static_assert(C::KG == 1, "one K-group");
     extern __shared__ uint4 smem_u4[];
     uint8_t * smem = reinterpret_cast<uint8_t *>(smem_u4);
     const int b = (int) blockIdx.x, g = (int) gridDim.x / 8, T = p.mt * p.nt, nk = p.nk;
@@ -937,7 +1007,7 @@ __device__ inline void load_item_a(const gemm_params & p, int64_t m0, int wave, 
 template <class CB, class CS, int EPI>
 __global__ __launch_bounds__(CB::NT, 1) void gemm_kernel_mixed_tiles(const gemm_params p) {
     static_assert(CB::NT == CS::NT && CS::BM * 2 == CB::BM && CS::BN == CB::BN && CS::NP == CB::NP &&
-                      CS::TI == CB::TI && CB::NP1 == 0 && CS::NP1 == 0,
+                      CS::TI == CB::TI && CB::NP1 == 0 && CS::NP1 == 0 && CB::KG == 1 && CS::KG == 1,
                   "halves of the big tiles, with the same producers");
     extern __shared__ uint4 smem_u4[];
     uint8_t * smem = reinterpret_cast<uint8_t *>(smem_u4);
@@ -1039,6 +1109,18 @@ __global__ __launch_bounds__(CB::NT, 1) void gemm_kernel_mixed_tiles(const gemm_
 #ifndef ZEST_GEMM_TINY_STEP
 #define ZEST_GEMM_TINY_STEP 0.45  // measured: ~0.38 us a step in a launch of 16 or 64 steps
 #endif
+// The same tiles as two K-groups (eight waves a workgroup), alone or with K
+// splits, for launches of at most one and a half such workgroups a CU: each
+// CU has twice the loads in flight, and the groups' sums meet in LDS instead
+// of through a split-K fixup in HBM (the down projection of a 1024-token
+// chunk at hidden 1024, 1024 x 1024 x 4096: 17.3 us against 21.3 in two
+// splits of single-group tiles; its O projection, K 1024: 8.1 against 9.2
+// unsplit). A group's step costs TINY2_STEP of a 256x128 one in the cost
+// model (fitted to the launch times of the hidden-1024 layer's four GEMMs at
+// 256 to 4096 tokens).
+#ifndef ZEST_GEMM_TINY2_STEP
+#define ZEST_GEMM_TINY2_STEP 0.4
+#endif
 // 256x128 tiles with 8 consumer waves of 32x128 and 4 producer waves, two
 // consumers on each SIMD: for the fused GLU (its long launches gain ~3% from
 // the second consumer), the whole tiles of mixed launches, and launches of
@@ -1073,6 +1155,7 @@ using cfg_tiny = gemm_cfg<ZEST_GEMM_TINY>;
 // x 2 column blocks) and 4 producers, the same threads (the q/k/v group at
 // 2048 tokens: 66.8 -> 65.6 us against one consumer per SIMD in both).
 using cfg_half8 = gemm_cfg<128, 128, 4, 256, 1, 2>;
+using cfg_tiny2 = gemm_cfg<ZEST_GEMM_TINY, 1, 0, 2>;
 
 // Per device and stream: the split-K workspace (grown as needed; counters
 // zeroed when allocated, and zero again after every launch).
@@ -1255,6 +1338,9 @@ int launch(gemm_params p, const int64_t * N, int splits, hipStream_t s, const ch
     p.nt = nt;
     const int64_t T = (int64_t) p.mt * nt;
     p.splits = splits;
+    if (C::KG > 1 && p.nk % (splits * C::KG))
+        return zest::fail(ZEST_E_ARG, "%s: %d K-steps do not make %d splits of %d K-groups", name, p.nk, splits,
+                          C::KG);
     const int64_t grid = T * p.splits;
     if (grid >= (1ll << 31) || (p.splits > 1 && grid * C::BM * C::BN * 4 >= (1ll << 31)))
         return zest::fail(ZEST_E_ARG, "%s: %lld tiles is too many", name, (long long) T);
@@ -1280,7 +1366,7 @@ int launch(gemm_params p, const int64_t * N, int splits, hipStream_t s, const ch
 #if ZEST_GEMM_PERSIST
     // more than one round: persistent workgroups, one a CU (not for the
     // residual epilogue, whose persistent form does not fit the registers)
-    if constexpr (EPI != EPI_RESIDUAL && C::MINB == 1 && C::NP1 == 0)
+    if constexpr (EPI != EPI_RESIDUAL && C::MINB == 1 && C::NP1 == 0 && C::KG == 1)
         if (p.splits == 1 && p.nk % 2 == 0 && p.nk >= 4) {
             int dev = 0;
             (void) hipGetDevice(&dev);
@@ -1347,12 +1433,13 @@ struct plain_plan {
     shape_kind kind;
     int splits;
     int64_t nbig;  // mixed: the whole tiles
+    int kg = 1;    // tiny: K-groups
 };
 
 // The cost model above, applied: the cheapest of one round of 128x160 tiles
-// (long K), a mixed launch, 64x64 tiles, 128x128 or 256x128 tiles (each with
-// its best K split), and, for one unsplit round, 128x160 or two-consumer
-// 256x128 tiles.
+// (long K), a mixed launch, 64x64 tiles (with their best K split, alone or as
+// two K-groups), 128x128 or 256x128 tiles (each with its best K split), and,
+// for one unsplit round, 128x160 or two-consumer 256x128 tiles.
 plain_plan plan_plain(const gemm_params & p, const int64_t * N, int64_t P) {
     const gemm_plan big =
         plan_splits(tiles_of(p, N, cfg_big::BM, cfg_big::BN), p.nk, P, (double) cfg_big::BM * cfg_big::BN * 4, 1.0);
@@ -1375,8 +1462,20 @@ plain_plan plan_plain(const gemm_params & p, const int64_t * N, int64_t P) {
         if (mixed < big.cost && mixed < small.cost) return {shape_kind::mixed, 1, R * P};
     }
     // tiny tiles, cfg_tiny::MINB of them a CU
-    const gemm_plan tiny = plan_splits(tiles_of(p, N, cfg_tiny::BM, cfg_tiny::BN), p.nk, P * cfg_tiny::MINB,
-                                       (double) cfg_tiny::BM * cfg_tiny::BN * 4, ZEST_GEMM_TINY_STEP);
+    const int64_t Tt = tiles_of(p, N, cfg_tiny::BM, cfg_tiny::BN);
+    const gemm_plan tiny =
+        plan_splits(Tt, p.nk, P * cfg_tiny::MINB, (double) cfg_tiny::BM * cfg_tiny::BN * 4, ZEST_GEMM_TINY_STEP);
+    // as two K-groups: the launch's nk/2 group steps in S splits
+    gemm_plan tiny2;
+    tiny2.splits = 0;
+    for (int S = 1; S <= 8; S *= 2) {
+        if (p.nk % (2 * S) || p.nk / (2 * S) < 4 || 2 * Tt * S > 3 * P) continue;
+        const double cost = split_cost(Tt, p.nk / 2, P, (double) cfg_tiny::BM * cfg_tiny::BN * 4,
+                                       ZEST_GEMM_TINY2_STEP, S);
+        if (tiny2.splits == 0 || cost < tiny2.cost) tiny2 = {S, cost};
+    }
+    if (tiny2.splits > 0 && tiny2.cost < tiny.cost && tiny2.cost < big.cost && tiny2.cost < small.cost)
+        return {shape_kind::tiny, tiny2.splits, 0, 2};
     if (tiny.cost < big.cost && tiny.cost < small.cost) return {shape_kind::tiny, tiny.splits, 0};
     if (small.cost < big.cost) return {shape_kind::small, small.splits, 0};
     if (big.splits == 1 && Tb <= P) {
@@ -1391,9 +1490,11 @@ plain_plan plan_plain(const gemm_params & p, const int64_t * N, int64_t P) {
 }
 
 // Plans and launches a GEMM; `fixed` as for launch(). A fused GLU launch
-// splits K as the plain launch of its 2F columns would (so its gate and up
-// sums are that launch's, bit for bit) and takes the cheaper of 256x128 and
-// 128x128 tiles at that split.
+// splits K as the plain launch of its 2F columns would, in as many K-groups
+// (so its gate and up sums are that launch's, bit for bit: a sum depends on
+// the K-steps' partition and order, not on the tile shape), and takes the
+// cheaper of 256x128 and 128x128 tiles at that split (64x64 tiles for
+// K-groups).
 template <int EPI>
 int launch_any(gemm_params p, const int64_t * N, hipStream_t s, const char * name,
                const sk_space * fixed = nullptr) {
@@ -1403,6 +1504,7 @@ int launch_any(gemm_params p, const int64_t * N, hipStream_t s, const char * nam
     const plain_plan pp = plan_plain(p, N, P);
     if constexpr (EPI >= 0) {
         const int S = pp.splits;
+        if (pp.kg == 2) return launch<cfg_tiny2, EPI>(p, N, S, s, name, fixed);
         const double big = split_cost(tiles_of(p, N, cfg_glu::BM, cfg_glu::BN), p.nk, P,
                                       (double) cfg_glu::BM * cfg_glu::BN * 4, 1.0, S);
         const double small = split_cost(tiles_of(p, N, cfg_small::BM, cfg_small::BN), p.nk, P,
@@ -1414,7 +1516,9 @@ int launch_any(gemm_params p, const int64_t * N, hipStream_t s, const char * nam
             case shape_kind::o_round:
             case shape_kind::o_one: return launch<cfg_o, EPI>(p, N, 1, s, name, fixed);
             case shape_kind::mixed: return launch_mixed<cfg_glu, cfg_half8, EPI>(p, N, pp.nbig, s, name);
-            case shape_kind::tiny: return launch<cfg_tiny, EPI>(p, N, pp.splits, s, name, fixed);
+            case shape_kind::tiny:
+                if (pp.kg == 2) return launch<cfg_tiny2, EPI>(p, N, pp.splits, s, name, fixed);
+                return launch<cfg_tiny, EPI>(p, N, pp.splits, s, name, fixed);
             case shape_kind::small: return launch<cfg_small, EPI>(p, N, pp.splits, s, name, fixed);
             case shape_kind::glu_one: return launch<cfg_glu, EPI>(p, N, 1, s, name, fixed);
             case shape_kind::big: break;

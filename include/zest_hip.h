@@ -147,8 +147,11 @@ ZEST_API int zest_gemm_residual(const void *a, int64_t M, const void *w, int64_t
  * tile's K among workgroups (split-K) and sums the splits in a fixed order,
  * through a workspace the library allocates per device and stream on first
  * use (and grows, synchronizing the stream): calls that share a stream run
- * in order and never share it concurrently. The same holds for zest_gemm
- * and zest_gemm_glu, which run through the same launch. */
+ * in order and never share it concurrently. A launch of at most one small
+ * tile a CU may instead split each tile's K between two groups of waves in
+ * one workgroup (K-groups), whose sums meet in LDS, also in a fixed order.
+ * The same holds for zest_gemm and zest_gemm_glu, which run through the
+ * same launch. */
 #define ZEST_GEMM_MAX_GROUP 4
 ZEST_API int zest_gemm_group(const void *a, int64_t M, int64_t K, int n, const void *const *w, const int64_t *N,
                              float *const *c, const int64_t *ldc, uint32_t *nonfinite, void *stream);
@@ -190,9 +193,9 @@ ZEST_API int zest_convert_weight_gu(int type, const void *gate, const void *up, 
  * h[M][F] = glu(g, u) of `kind` (zest_glu's arithmetic), written as the next
  * matmul's operand (xout, as zest_pack_act_x writes it, zest_act_bytes(M, F)
  * bytes) and/or as fp32 rows (h, row stride ldh floats); either may be NULL,
- * not both. This launch splits K among workgroups exactly as zest_gemm(a,
- * w_gu) of 2F columns does, so its gate and up sums are that call's, bit for
- * bit, and h is bit-exact with zest_glu over the gate and up columns of
+ * not both. This launch splits K among workgroups and K-groups exactly as
+ * zest_gemm(a, w_gu) of 2F columns does, so its gate and up sums are that
+ * call's, bit for bit, and h is bit-exact with zest_glu over the gate and up columns of
  * zest_gemm(a, w_gu) whenever that call runs as one launch (its fp32 output,
  * M x 2F floats, under 2 GiB); xout is then zest_pack_act_x of that h.
  * `nonfinite` as for zest_gemm, over g, u and h.

@@ -98,7 +98,7 @@ def persistent_tiles(T, G):
     return out
 
 
-def check_launch(M, N, K, BM, BN, CWM, S):
+def check_launch(M, N, K, BM, BN, CWM, S, KG=1):
     nk = k_steps(K)
     Mp, Np = rows_pad(M), rows_pad(N)
     ks = Mp // 32 * XGROUP_BYTES             # p.a_kstride
@@ -112,9 +112,14 @@ def check_launch(M, N, K, BM, BN, CWM, S):
     # the producer thread of the highest offset: tile BN/16-1, row 15, h 1, second 16 bytes
     w_vmax = (BN // 16 - 1) * TILE_BYTES + 15 * TILE_K + 32 + 16 + 16
     w_emax = (BN // 16 - 1) * TILE_BYTES + TILE_MANT + 15 * 8 + 4 + 4
+    runs = []  # (split, K-group's first step, its steps)
     for split in range(S):
         k0 = split * nk // S
         ns = (split + 1) * nk // S - k0
+        # run_tile: K-group g of the split takes the g-th of KG equal runs
+        assert ns % KG == 0, (nk, S, KG)
+        runs += [(split, k0 + g * (ns // KG), ns // KG) for g in range(KG)]
+    for split, k0, ns in runs:
         last = nk - 1 - k0
         a_hi = max(consumer_steps(ns, last))
         w_hi = max(producer_steps(ns, last))
@@ -150,6 +155,11 @@ def test_scalar_offsets_stay_inside_operands(M, N, K):
         if S > 1 and nk // S < 4:
             continue  # the planner never splits below four steps a split
         check_launch(M, N, K, BM, BN, CWM, S)
+    # 64x64 tiles as two K-groups (cfg_tiny2), in every split count the
+    # launch accepts (nk a multiple of splits x groups)
+    for S in range(1, 9):
+        if nk % (2 * S) == 0 and nk // (2 * S) >= 1:
+            check_launch(M, N, K, 64, 64, 2, S, KG=2)
     # the 128x160 tiles (cfg_o): unsplit, and only for weights of whole 160-row tiles
     if N % 160 == 0:
         check_launch(M, N, K, 128, 160, 4, 1)
@@ -195,8 +205,9 @@ def test_unclamped_prefetch_would_leave_the_operand():
 
 
 
-# (tile columns BN, wave columns WN, waves across) of the GLU launch (cfg_glu)
-GLU_CONFIGS = [(128, 128, 1)]
+# (tile columns BN, wave columns WN, waves across) of the GLU launches
+# (cfg_glu and cfg_small; cfg_tiny2)
+GLU_CONFIGS = [(128, 128, 1), (64, 64, 1)]
 
 
 @pytest.mark.parametrize("F", [32, 64, 96, 128, 160, 4096, 9728, 17408])
@@ -247,3 +258,66 @@ def test_output_bands_stay_inside_operands(M, N, K):
                       for tm in range((rows + BM - 1) // BM) for wm in range(CWM))
             a_hi = shift + top + 31 * 32 + 16 + 3 * XSUB_BYTES + 16 + (nk - 1) * ks
             assert a_hi <= a_size, (M, N, K, r0, rows, BM)
+
+
+def producer_barriers(ns):
+    """produce_tile's barriers for a tile of ns steps: one after the
+    prologue, two per pair of the steady loop, then one per step of the
+    tail."""
+    n, k = 1, 0
+    while k + 5 < ns:
+        n += 2
+        k += 2
+    while k < ns:
+        n += 1 + (1 if k + 1 < ns else 0)
+        k += 2
+    return n
+
+
+def consumer_barriers(ns):
+    """consume_tile's barriers: one before the first step, one per step."""
+    n, k = 1, 0
+    while k + 1 < ns:
+        n += 2
+        k += 2
+    if k < ns:
+        n += 1
+    return n
+
+
+@pytest.mark.parametrize("ns", [1, 2, 3, 4, 5, 6, 7, 8, 16, 32, 33, 64])
+def test_every_wave_meets_the_same_barriers(ns):
+    # a workgroup's waves meet each s_barrier together: a tile's producers and
+    # consumers meet ns + 1, and with K-groups every group runs the same ns
+    # (the launch requires nk to be a multiple of splits x groups) and every
+    # wave meets one more, where groups 1.. hand their sums to group 0
+    assert producer_barriers(ns) == consumer_barriers(ns) == ns + 1
+
+
+def kgroup_lds(BM, BN, KG, waves, WM, WN):
+    """run_tile's LDS map of a K-group launch: (rings, sums regions, group
+    0's epilogue regions, LDS_BYTES), each a list of [lo, hi) byte ranges."""
+    ring = 3 * BN * 128
+    tile = BM * BN * 4
+    lds = KG * max(ring, tile)
+    rings = [(g * ring, (g + 1) * ring) for g in range(KG)]
+    sums = [(g * tile + w * WM * WN * 4, g * tile + (w + 1) * WM * WN * 4) for g in range(1, KG) for w in range(waves)]
+    epilogue = [(w * WM * WN * 4, (w + 1) * WM * WN * 4) for w in range(waves)]
+    return rings, sums, epilogue, lds
+
+
+@pytest.mark.parametrize("KG", [2, 3, 4])
+def test_kgroup_lds_regions(KG):
+    # cfg_tiny2's map (64x64 tiles, two consumer waves of 32x64), and the
+    # same tiles with three or four groups: every region inside the
+    # workgroup's LDS, the rings apart, the sums apart from each other and
+    # from group 0's epilogue regions (which the residual DMA, the GLU
+    # staging and the split-K fixup use while group 0 finishes)
+    rings, sums, epi, lds = kgroup_lds(64, 64, KG, 2, 32, 64)
+    regions = rings + sums + epi
+    assert all(0 <= lo < hi <= lds for lo, hi in regions)
+    assert lds <= 160 * 1024
+    def apart(rs):
+        rs = sorted(rs)
+        return all(a[1] <= b[0] for a, b in zip(rs, rs[1:]))
+    assert apart(rings) and apart(sums + epi)

@@ -6,9 +6,10 @@ Its result must be bit-exact with the unfused chain over the same GEMM:
 zest_gemm of the interleaved weight (pinned against the oracle in
 test_gemm_gpu), whose gate and up columns go through zest_glu (pinned in
 test_ops_gpu) and zest_pack_act_x (bit-exact with the oracle's encoder in
-test_pack_gpu). The fused launch splits K among workgroups exactly as the
-plain launch of its 2F columns does (whatever tile shapes the two take), so
-each output is summed over K in the same order and every float matches. The
+test_pack_gpu). The fused launch splits K among workgroups, and among the
+K-groups of a workgroup, exactly as the plain launch of its 2F columns does
+(whatever tile shapes the two take), so each output is summed over K in the
+same order and every float matches. The
 bit-exact tests that could miss a change of summation order use operands
 whose 8-value blocks span 2^+-12 (fp32 partial sums of their products are
 rarely exact), and a control shows that with them another K partition does
@@ -135,9 +136,10 @@ def test_order_sensitive_operands_show_another_k_split(zest_gpu):
 
 
 @pytest.mark.parametrize("M,F,K", [
-    (520, 896, 1536),   # plain launch as 64x64 tiles, unsplit
+    (520, 896, 1536),   # 252 tiles of 64x64, each K-split between two K-groups
+    (1024, 512, 4096),  # 256 of them, K 4096
     (2048, 1024, 8192),  # few tiles, long K: split
-    (256, 512, 4096),
+    (256, 512, 4096),    # 64 tiles of 64x64 in two K-groups and four K splits
     (2048, 6144, 4096),  # three rounds: persistent workgroups
     (1500, 4096, 4096),
 ])

@@ -84,6 +84,8 @@ def test_exponent_shift_kat(zest_gpu, oracle):
     (0, 300, 200, 200),      # K not a multiple of 64
     (8, 1, 256, 512),
     (12, 2048, 1024, 2560),  # K/V projection of config 3
+    (8, 1024, 1024, 4096),   # 64x64 tiles, one a CU, each in two K-groups
+    (8, 256, 1024, 4096),    # 64 of them, in two K-groups and four K splits
 ])
 def test_gemm_against_oracle(zest_gpu, oracle, wtype, M, N, K):
     import torch
@@ -328,6 +330,8 @@ def test_gemm_group_rejects_bad_counts(zest_gpu):
     (300, 200, 256),      # ragged rows, 128x128 tiles
     (1024, 1000, 512),    # a width that is not a tile multiple
     (2048, 6144, 512),    # 384 tiles: a round and a half, the half as 128-row tiles
+    (1024, 1024, 4096),   # 64x64 tiles in two K-groups
+    (256, 1024, 4096),    # and in four K splits
 ])
 def test_gemm_residual_is_gemm_then_add(zest_gpu, M, N, K):
     # the residual epilogue adds in the store: the same floats as the GEMM
