@@ -324,6 +324,99 @@ def activity_summary(pmc_dir: str, trace_dir: str) -> int:
     return 0
 
 
+SUSTAIN_SHAPE = (2048, 19456, 2560)  # the fused gate/up's GEMM at 2048 tokens, as a plain launch
+SUSTAIN_CASES = ("workload data", "W mantissas zero", "random bytes")
+
+
+def sustain(args) -> int:
+    """The same GEMM launch, back to back for `args.sustain` seconds per
+    operand case (the cases of --operand-activity), each after two idle
+    seconds, for sampling the board's power and clock beside it (amd-smi
+    from another process). One JSON line per phase: its wall-clock start and
+    end (time.time()) and its TFLOP/s."""
+    import time
+    import torch
+    z = load_pkg()
+    import ggml_xdna_amd.quant as quant
+    torch.cuda.set_device(0)
+    z.init(0)
+    m, n, k = SUSTAIN_SHAPE
+    g = torch.Generator(device="cuda").manual_seed(0)
+    a = z.pack_act_x(torch.randn((m, k), device="cuda", generator=g))
+    w_rand = torch.randint(0, 256, (z.bfp16_bytes(n, k),), dtype=torch.uint8, device="cuda", generator=g)
+    w_rand.view(-1, 1152)[:, 1024:] = torch.randint(118, 128, (w_rand.numel() // 1152, 128), dtype=torch.uint8,
+                                                      device="cuda", generator=g)
+    w_q4k = z.convert_weight(12, quant.quantize(12, torch.randn((n, k), device="cuda", generator=g) * 0.02), n, k)
+    w_zero = w_q4k.clone()
+    w_zero.view(-1, 1152)[:, :1024] = 0
+    c = torch.empty((m, n), device="cuda")
+    weights = {"workload data": w_q4k, "W mantissas zero": w_zero, "random bytes": w_rand}
+    for case in SUSTAIN_CASES:
+        torch.cuda.synchronize()
+        t = time.time()
+        time.sleep(2.0)
+        print(json.dumps({"phase": "idle", "t0": t, "t1": time.time()}), flush=True)
+        w = weights[case]
+        t0, launches = time.time(), 0
+        while time.time() - t0 < args.sustain:
+            for _ in range(20):
+                z.gemm(a, m, w, n, k, out=c)
+            launches += 20
+            torch.cuda.synchronize()
+        t1 = time.time()
+        print(json.dumps({"phase": case, "t0": t0, "t1": t1, "launches": launches,
+                          "TFLOP/s": round(2.0 * m * n * k * launches / (t1 - t0) / 1e12, 1)}), flush=True)
+    return 0
+
+
+def _flat(d, prefix=""):
+    out = {}
+    for key, v in (d.items() if isinstance(d, dict) else enumerate(d)):
+        name = f"{prefix}.{key}" if prefix else str(key)
+        if isinstance(v, (dict, list)):
+            out.update(_flat(v, name))
+        else:
+            out[name] = v
+    return out
+
+
+def sustain_summary(phases_log: str, smi_log: str) -> int:
+    """Per phase of --sustain: the averages of amd-smi's samples taken inside
+    it (its first second left out), from a log of lines "T <time.time()>"
+    each followed by the JSON of `amd-smi metric -g 0 -p -c --json`: socket
+    power and the GFX clock (the mean over the XCDs' clocks)."""
+    phases = [json.loads(l) for l in open(phases_log) if l.startswith("{")]
+    samples, t, buf = [], None, []
+
+    def flush():
+        if t is not None and buf:
+            try:
+                samples.append((t, _flat(json.loads("".join(buf)))))
+            except ValueError:
+                pass
+
+    for line in open(smi_log):
+        if line.startswith("T "):
+            flush()
+            t, buf = float(line.split()[1]), []
+        else:
+            buf.append(line)
+    flush()
+    out = []
+    for ph in phases:
+        inside = [f for (ts, f) in samples if ph["t0"] + 1.0 <= ts <= ph["t1"]]
+        row = {"phase": ph["phase"], "samples": len(inside)}
+        if "TFLOP/s" in ph:
+            row["TFLOP/s"] = ph["TFLOP/s"]
+        for label, pick in (("socket_power_W", lambda key: key.endswith("power.socket_power.value")),
+                            ("gfx_clock_mhz", lambda key: ".clock.gfx_" in key and key.endswith(".clk.value"))):
+            vals = [float(v) for f in inside for key, v in f.items() if pick(key) and str(v).replace(".", "").isdigit()]
+            row[label] = round(sum(vals) / len(vals), 1) if vals else None
+        out.append(row)
+    print(json.dumps(out, indent=1))
+    return 0
+
+
 CALIB_FLOATS = 64 << 20  # the calibration kernel's floats: 256 MiB each way
 
 
@@ -507,6 +600,10 @@ def main() -> int:
                     help="the same GEMM launches on random, workload and all-zero operands (power sensitivity)")
     ap.add_argument("--activity-summary", nargs=2, metavar=("PMC_DIR", "TRACE_DIR"),
                     help="clock and MFMA busy per case from rocprofv3 runs of --operand-activity")
+    ap.add_argument("--sustain", type=float, default=None, metavar="SECONDS",
+                    help="one GEMM back to back for SECONDS per operand case, for sampling power beside it")
+    ap.add_argument("--sustain-summary", nargs=2, metavar=("PHASES_LOG", "SMI_LOG"),
+                    help="power, clock and power-cap status per --sustain phase from amd-smi samples")
     ap.add_argument("--counter-summary", nargs=4, metavar=("MFMA_DIR", "FETCH_DIR", "WRITE_DIR", "TRACE_DIR"),
                     help="per GEMM launch kind: time, MFMA busy, clock, HBM bytes from rocprofv3 runs of --traffic-probe")
     args = ap.parse_args()
@@ -516,6 +613,10 @@ def main() -> int:
         return operand_activity(args)
     if args.activity_summary:
         return activity_summary(*args.activity_summary)
+    if args.sustain is not None:
+        return sustain(args)
+    if args.sustain_summary:
+        return sustain_summary(*args.sustain_summary)
     if args.counter_summary:
         return counter_summary(args)
     if args.traffic_summary:
