@@ -45,6 +45,7 @@ ROOT = Path(__file__).resolve().parent
 METRIC = "bfp16 prefill MUL_MAT TFLOP/s (% bf16 MFMA peak); layer-stack prefill tok/s"
 BF16_PEAK = 2516.6   # TFLOP/s, MI355X dense bf16 MFMA
 HBM_PEAK = 8000.0    # GB/s
+BOARD_POWER_LIMIT_W = 1400  # MI355X total board power, as published
 
 
 def load_pkg():
@@ -689,6 +690,19 @@ def main() -> int:
                     "mfma_busy_pct": round(sum(k["mfma_busy_pct"] * k["us"] * k["launches"] for k in kinds.values()) / wt, 1),
                     "clock_ghz": round(sum(k["clock_ghz"] * k["us"] * k["launches"] for k in kinds.values()) / wt, 3),
                     "per_kind_frac": {n: k["frac_of_peak"] for n, k in kinds.items()}}
+    # board power and clock beside the gate/up GEMM sustained (`--sustain`
+    # with amd-smi sampling), from the committed run
+    power = None
+    pf = ROOT / "profiles" / "gemm_board-power.json"
+    if pf.exists() and cfg.name == "qwen3-4b":
+        phases = {p["phase"]: p for p in json.loads(pf.read_text()) if p["phase"] != "idle"}
+        wl, quiet = phases.get("workload data"), phases.get("W mantissas zero")
+        if wl and quiet and wl.get("gfx_clock_mhz") and quiet.get("gfx_clock_mhz"):
+            power = {"source": str(pf.relative_to(ROOT)), "board_limit_w": BOARD_POWER_LIMIT_W,
+                     "socket_power_w": wl["socket_power_W"], "clock_ghz": round(wl["gfx_clock_mhz"] / 1e3, 3),
+                     "quiet_operands": {"socket_power_w": quiet["socket_power_W"],
+                                        "clock_ghz": round(quiet["gfx_clock_mhz"] / 1e3, 3),
+                                        "speedup": round(quiet["TFLOP/s"] / wl["TFLOP/s"], 3)}}
     # the HBM-bound kernels on rotating sets, as `--hbm` measures them
     names = {v[0]: k for k, v in GGUF_BLOCKS.items()}
     convert = [convert_rate(z, names[t]) for t in dict.fromkeys((cfg.ffn_type, cfg.down_type))]
@@ -726,7 +740,7 @@ def main() -> int:
                      "traffic_source": traffic_src,
                      "launches": launches, "avg_launch_us": round(gemm_ms * 1e3 / launches, 2),
                      "timed": "the step's GEMM launches back to back between two HIP events",
-                     "counters": counters},
+                     "counters": counters, "power": power},
         "convert": convert,
         "pack": pack,
     }
