@@ -1504,13 +1504,18 @@ int launch_any(gemm_params p, const int64_t * N, hipStream_t s, const char * nam
     const plain_plan pp = plan_plain(p, N, P);
     if constexpr (EPI >= 0) {
         const int S = pp.splits;
-        if (pp.kg == 2) return launch<cfg_tiny2, EPI>(p, N, S, s, name, fixed);
+        // The tiles cover the output operand's K padding too: the columns of
+        // 2F rounded up to 128 rows of the gate/up pair, whose rows past 2F
+        // are zero blocks, so the h columns past F store the packer's zeros
+        // (with 64-column tiles and F % 64 == 32 the last tile would end at F).
+        const int64_t Nt = (N[0] + 127) / 128 * 128;
+        if (pp.kg == 2) return launch<cfg_tiny2, EPI>(p, &Nt, S, s, name, fixed);
         const double big = split_cost(tiles_of(p, N, cfg_glu::BM, cfg_glu::BN), p.nk, P,
                                       (double) cfg_glu::BM * cfg_glu::BN * 4, 1.0, S);
         const double small = split_cost(tiles_of(p, N, cfg_small::BM, cfg_small::BN), p.nk, P,
                                         (double) cfg_small::BM * cfg_small::BN * 4, ZEST_GEMM_SMALL_STEP, S);
-        if (small < big) return launch<cfg_small, EPI>(p, N, S, s, name, fixed);
-        return launch<cfg_glu, EPI>(p, N, S, s, name, fixed);
+        if (small < big) return launch<cfg_small, EPI>(p, &Nt, S, s, name, fixed);
+        return launch<cfg_glu, EPI>(p, &Nt, S, s, name, fixed);
     } else {
         switch (pp.kind) {
             case shape_kind::o_round:

@@ -212,18 +212,31 @@ GLU_CONFIGS = [(128, 128, 1), (64, 64, 1)]
 
 @pytest.mark.parametrize("F", [32, 64, 96, 128, 160, 4096, 9728, 17408])
 def test_glu_epilogue_columns_stay_inside_the_operand(F):
-    # store_glu: the wave of tile column n0 (over the interleaved 2F rows)
-    # holds h columns c0 = n0/2 + wn*HW .. c0+HW-1, HW = WN/2; it writes the
-    # operand only when c0 < k_pad(F), and then every column it writes is
-    # inside the operand's padded width
+    # store_glu: the wave of tile column n0 holds h columns c0 = n0/2 + wn*HW
+    # .. c0+HW-1, HW = WN/2. The launch's tiles cover the pair's 2F rows
+    # rounded up to 128 (launch_any), so together they write every column of
+    # the operand's padded width k_pad(F), its K padding included, each once,
+    # and read only rows the packed pair holds (2F rounded up to 256)
     Fp = (F + 63) // 64 * 64
+    rows_pad = (2 * F + 255) // 256 * 256
     for BN, WN, waves_n in GLU_CONFIGS:
         HW = WN // 2
-        for n0 in range(0, (2 * F + BN - 1) // BN * BN, BN):
+        cols = []
+        for n0 in range(0, (2 * F + 127) // 128 * 128, BN):
+            assert n0 + BN <= rows_pad, (F, BN, n0)
             for wn in range(waves_n):
                 c0 = n0 // 2 + wn * HW
-                if c0 < Fp:
-                    assert c0 + HW <= Fp, (F, BN, WN, n0, wn)
+                assert c0 + HW <= Fp, (F, BN, WN, n0, wn)
+                cols += range(c0, c0 + HW)
+        assert sorted(cols) == list(range(Fp)), (F, BN)
+
+
+def test_glu_tiles_of_2f_alone_would_leave_padding_unwritten():
+    # the rule has teeth: 64-column tiles over 2F = 192 rows alone write h
+    # columns 0..95 of an operand 128 wide
+    F, BN, HW = 96, 64, 32
+    cols = [c for n0 in range(0, (2 * F + BN - 1) // BN * BN, BN) for c in range(n0 // 2, n0 // 2 + HW)]
+    assert max(cols) + 1 < (F + 63) // 64 * 64
 
 
 def band_rows(ld):

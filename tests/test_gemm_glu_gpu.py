@@ -158,6 +158,26 @@ def test_gemm_glu_bit_exact_order_sensitive(zest_gpu, M, F, K):
 
 
 @pytest.mark.parametrize("M,F,K", [
+    (65, 96, 2560),     # 64x64 tiles in K-groups and K splits; F % 64 == 32
+    (300, 96, 200),     # 128-column tiles; F % 64 == 32
+    (1024, 160, 4096),  # 64x64 tiles in K-groups; F % 64 == 32
+])
+def test_gemm_glu_writes_the_operand_padding(zest_gpu, M, F, K):
+    # the fused launch writes every byte of the down projection's operand,
+    # the K padding past F (half a 64-column K-tile here) and the rows past
+    # M included, into a buffer that held garbage: the bytes of
+    # zest_pack_act_x over the unfused chain's h
+    import torch
+    a, wgu = _wide_case(zest_gpu, M, F, K, 7 * M + F)
+    x_ref, h_ref, _, _ = unfused(zest_gpu, 2, a, M, wgu, F, K)
+    buf = torch.full_like(x_ref, 0xFF)
+    xo, _ = zest_gpu.gemm_glu(2, a, M, wgu, F, K, xout=buf)
+    torch.cuda.synchronize()
+    assert xo.data_ptr() == buf.data_ptr()
+    assert torch.equal(buf, x_ref), (M, F, K, int((buf != x_ref).sum()))
+
+
+@pytest.mark.parametrize("M,F,K", [
     (300, 160, 256),    # 6 tiles: one workgroup a tile
     (1500, 4096, 512),  # 384 tiles: persistent workgroups, each kind's own kernel
 ])
