@@ -436,6 +436,70 @@ def test_gemm_random_shapes(zest_gpu, oracle):
 
 
 
+def test_gemm_random_shapes_order_sensitive(zest_gpu, oracle):
+    # a wider seeded sweep on operands whose 8-value blocks span 2^+-12: rows
+    # up to a few rounds of tiles (and across the 64-, 256- and 1024-row
+    # boundaries), widths up to 12288, K up to 4096, so the planner takes
+    # every tile shape, K split and K-group form; the plain, grouped and
+    # residual launches against the oracle's bound, the residual added in
+    # place bit-exact with the GEMM then ADD, and the fused GLU of every kind
+    # bit-exact with the unfused chain, its operand written whole (padding
+    # included) into a buffer that held garbage
+    import torch
+    z = zest_gpu
+    rng = np.random.default_rng(31337)
+    for case in range(48):
+        M = int(rng.choice([1, 5, 64, 65, 200, 256, 257, 511, 768, 1024, 1025, 1536, 2048, 3000, 4096]))
+        N = int(rng.integers(1, 96)) * 32 * int(rng.choice([1, 2, 4]))
+        K = int(rng.integers(1, 64)) * 8 * int(rng.choice([1, 2, 4, 8]))
+        kind = case % 5
+        x = wide_blocks(M, K, 10_000 + case)
+        a = z.pack_act_x(_dev(x))
+        if kind == 4:
+            F = max(32, N // 64 * 32)
+            gate, up = wide_blocks(F, K, 20_000 + case, 0.05), wide_blocks(F, K, 30_000 + case, 0.05)
+            wgu = z.convert_weight_gu(0, _dev(gate.view(np.uint8)), _dev(up.view(np.uint8)), F, K)
+            c = z.gemm(a, M, wgu, 2 * F, K).view(M, F // 32, 2, 32)
+            gk = int(rng.integers(0, 5))
+            h_ref = z.glu(gk, c[:, :, 0, :].reshape(M, F).contiguous(), c[:, :, 1, :].reshape(M, F).contiguous(), F)
+            x_ref = z.pack_act_x(h_ref)
+            buf = torch.full_like(x_ref, 0xFF)
+            xo, h = z.gemm_glu(gk, a, M, wgu, F, K, xout=buf, h=True)
+            torch.cuda.synchronize()
+            assert torch.equal(h.view(torch.int32), h_ref.view(torch.int32)), (gk, M, F, K)
+            assert torch.equal(buf, x_ref), (gk, M, F, K)
+            continue
+        w = wide_blocks(N, K, 40_000 + case, 0.05)
+        wp = z.convert_weight(0, _dev(w.view(np.uint8)), N, K)
+        res = rng.normal(0, 1, (M, N)).astype(np.float32)
+        if kind == 3:
+            want = z.add(z.gemm(a, M, wp, N, K), _dev(res))
+            h0 = _dev(res)
+            z.gemm_residual(a, M, wp, N, K, h0, out=h0)
+            torch.cuda.synchronize()
+            assert torch.equal(h0.view(torch.int32), want.view(torch.int32)), (M, N, K)
+            continue
+        slack = 0.0
+        if kind == 0:
+            got = z.gemm(a, M, wp, N, K).cpu().numpy().astype(np.float64)
+        elif kind == 1:
+            out = z.gemm_residual(a, M, wp, N, K, _dev(res)).cpu().numpy().astype(np.float64)
+            got, slack = out - res, np.abs(out) * 2.0 ** -24  # the add rounds once more
+        else:
+            cuts = sorted({0, N, *(int(v) // 8 * 8 for v in rng.integers(8, max(9, N - 8), 2))})
+            parts = [(lo, hi) for lo, hi in zip(cuts, cuts[1:]) if hi > lo]
+            ws = [z.convert_weight(0, _dev(np.ascontiguousarray(w[lo:hi]).view(np.uint8)), hi - lo, K)
+                  for lo, hi in parts]
+            outs = z.gemm_group(a, M, ws, [hi - lo for lo, hi in parts], K)
+            got = np.concatenate([o.cpu().numpy() for o in outs], axis=1).astype(np.float64)
+        rows = np.unique(np.linspace(0, M - 1, min(M, 12)).astype(int))
+        r64, ab = oracle.mul_mat_f64(decoded(z, oracle, wp, N, K), decoded_act(z, oracle, a, M, K)[rows])
+        sl = slack[rows] if kind == 1 else 0.0
+        err = np.abs(got[rows] - r64)
+        bound = 2.0 * K * 2.0 ** -24 * ab + sl
+        assert np.isfinite(got[rows]).all() and (err <= bound).all(), (kind, M, N, K, float((err / bound).max()))
+
+
 def test_gemm_output_bands(zest_gpu, oracle):
     # an output whose span passes 2 GiB (the all-logits projection: vocab
     # 151,936 at a 4096-token ubatch, 2.49 GB of fp32) runs as launches over

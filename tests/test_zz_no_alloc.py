@@ -8,7 +8,7 @@ from __future__ import annotations
 
 import numpy as np
 import pytest
-from gen import Rng
+from gen import Rng, wide_blocks
 from helpers import gemm_check
 
 pytestmark = pytest.mark.gpu
@@ -82,3 +82,26 @@ def test_noalloc_refuses_a_plan_beyond_its_workspace(zest_gpu):
     c = z.gemm_group(a, M, [w], [N], K)[0]
     torch.cuda.synchronize()
     assert bool((c == 0).all())
+
+
+def test_noalloc_random_shapes(zest_gpu):
+    # seeded shapes across the planner's tile shapes, K splits and K-groups,
+    # on operands where a change of summation order shows: the no-alloc entry
+    # point gives zest_gemm_group's bits (or refuses a plan beyond its array)
+    import torch
+    z = zest_gpu
+    rng = np.random.default_rng(4242)
+    for case in range(16):
+        M = int(rng.choice([1, 65, 256, 600, 1024, 2048, 4096]))
+        N = int(rng.integers(1, 96)) * 32
+        K = int(rng.integers(1, 64)) * 64
+        a = z.pack_act_x(_dev(wide_blocks(M, K, 500 + case)))
+        w = z.convert_weight(0, _dev(wide_blocks(N, K, 600 + case, 0.05).view(np.uint8)), N, K)
+        want = z.gemm_group(a, M, [w], [N], K)[0]
+        try:
+            got = z.gemm_group(a, M, [w], [N], K, noalloc=True)[0]
+        except RuntimeError as e:
+            assert "static workspace" in str(e), (M, N, K, str(e))
+            continue
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int32), want.view(torch.int32)), (M, N, K)
