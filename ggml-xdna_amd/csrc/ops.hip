@@ -356,6 +356,10 @@ __global__ __launch_bounds__(256) void rope_kernel(const float * __restrict__ x,
         const float theta_extrap = ff ? theta[p] / ff[p] : theta[p];
         float th = freq_scale * theta_extrap, mscale = attn_factor;
         if (ext_factor != 0.0f) {
+            // every operation rounded on its own, as the CPU's expression is:
+            // a fused multiply-add moves the angle by an ulp, which at
+            // positions in the tens of thousands shows in its sine and cosine
+#pragma clang fp contract(off)
             const float yv = ((float) p - corr0) / fmaxf(0.001f, corr1 - corr0);
             const float ramp_mix = (1.0f - fminf(1.0f, fmaxf(0.0f, yv))) * ext_factor;
             th = th * (1.0f - ramp_mix) + theta_extrap * ramp_mix;

@@ -124,6 +124,21 @@ def test_rope(zest_gpu, oracle, n_dims, mode, n_ctx, fs, ext, factors):
     assert nrmse(_host(got), want) <= EXACT
 
 
+def test_rope_yarn_at_long_positions(zest_gpu, oracle):
+    # positions of a 40k-token context with YaRN: the angle in the ramp
+    # between the correction dimensions is a blend the CPU rounds step by
+    # step; fusing it into a multiply-add moved the angle by an ulp, which at
+    # these positions put the rotation 1.6e-5 off in nrmse (over the bar)
+    T, H, HD = 31, 2, 128
+    x = Rng(92).normal(T * H * HD, 0, 1.5).reshape(T, H, HD)
+    pos = np.array([13575, 36435, 23620, 23342, 38472, 37492, 38234, 8472] * 4, dtype=np.int32)[:T]
+    for mode in (0, 2):
+        want = oracle.rope(x, pos, None, 128, mode, 4096, 10000.0, 0.25, 1.0, 1.0, 32.0, 1.0)
+        corr = oracle.corr_dims(128, 4096, 10000.0, 32.0, 1.0)
+        got = zest_gpu.rope(_dev(x), _dev(pos), None, 128, mode, 10000.0, 0.25, 1.0, 1.0, corr)
+        assert nrmse(_host(got), want) <= 1e-6, mode
+
+
 def _padding_is_zero(z, buf, rows, d):
     """The expanded operand's rows past `rows` and columns past d are zero."""
     full = z.expanded_to_rows(buf, z.rows_pad(rows), z.k_pad(d))
