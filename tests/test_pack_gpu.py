@@ -294,3 +294,42 @@ def test_convert_blocks_at_the_exponent_edges(zest_gpu, oracle):
     bf = (w.view(np.uint32) >> 16).astype(np.uint16)
     want = oracle.encode_rows(oracle.dequant(30, bf.view(np.uint8), n, k))
     assert np.array_equal(gpu_convert(zest_gpu, 30, bf.view(np.uint8), n, k), want)
+
+
+def test_convert_random_shapes_into_garbage_buffers(zest_gpu, oracle):
+    # a seeded sweep: every type at random row counts and widths, quantised
+    # weights and random bytes, each converted into a zero-filled and a
+    # garbage-filled buffer; the values match the oracle and the padding
+    # comes out the same in both (the converter writes every byte it owns),
+    # and so does the gate/up pair's
+    import torch
+    rng = np.random.default_rng(5)
+    names = list(GGUF)
+    for case in range(2 * len(names)):
+        name = names[case % len(names)]
+        wtype = GGUF[name]
+        blk = 256 if wtype in K_QUANTS else (8 if wtype in (1, 30) else 32)
+        N = int(rng.choice([1, 15, 17, 31, 32, 33, 255, 257, 1000]))
+        K = int(rng.integers(1, 24)) * blk * int(rng.choice([1, 2]))
+        if rng.random() < 0.5:
+            raw = random_gguf(oracle, wtype, N, K, seed=500 + case)
+        else:
+            raw = oracle.quantize(wtype, rng.normal(0, 0.02, (N, K)).astype(np.float32))
+        want = oracle.encode_rows(oracle.dequant(wtype, raw, N, K))
+        rt = torch.from_numpy(np.ascontiguousarray(raw)).cuda()
+        zero = zest_gpu.empty_packed(N, K)
+        zero.zero_()
+        junk = torch.full_like(zero, 0xA5)
+        zest_gpu.convert_weight(wtype, rt, N, K, out=zero)
+        zest_gpu.convert_weight(wtype, rt, N, K, out=junk)
+        torch.cuda.synchronize()
+        assert np.array_equal(zest_gpu.tiles_to_blocks(zero.cpu().numpy(), N, K), want), (name, N, K)
+        assert torch.equal(zero, junk), (name, N, K, int((zero != junk).sum()))
+        if N % 32 == 0:
+            up = torch.from_numpy(random_gguf(oracle, wtype, N, K, seed=900 + case)).cuda()
+            pz = torch.zeros(zest_gpu.bfp16_bytes(2 * N, K), dtype=torch.uint8, device="cuda")
+            pj = torch.full_like(pz, 0x5A)
+            zest_gpu.convert_weight_gu(wtype, rt, up, N, K, out=pz)
+            zest_gpu.convert_weight_gu(wtype, rt, up, N, K, out=pj)
+            torch.cuda.synchronize()
+            assert torch.equal(pz, pj), (name, "gu", N, K)
