@@ -442,15 +442,31 @@ bool read_by_other(const reader_map & r, const ggml_tensor * t, const ggml_tenso
     return false;
 }
 
+// A node that writes into the memory of another tensor: an in-place op, whose
+// result is a view of its input (ggml's *_inplace ops). Packed copies of that
+// tensor's rows made before it no longer hold its values.
+bool writes_in_place(const ggml_tensor * n) { return !is_noop(n) && n->view_src != nullptr; }
+
 // The fusions of a piece (src/xdna-exec.cpp:399-431): a GLU whose gate and up
 // are matmuls of the piece on the same input, with weights of one type and
 // shape, read by nothing but the GLU, inside the piece or out; or a GLU over
 // the halves of one such matmul's output. F % 32 == 0 (the fused GEMM's
 // interleave). The reference fuses SwiGLU only; every GLU kind is fused here,
-// the epilogue computing the same GLU the GLU kernel does.
+// the epilogue computing the same GLU the GLU kernel does. Gate and up must
+// see the same values: no node between them writes into their input in place.
 std::vector<fusion> find_fusions(const std::vector<ggml_tensor *> & nodes,
                                  const std::unordered_set<const ggml_tensor *> & in_piece, const reader_map & rd) {
     std::vector<fusion> out;
+    std::unordered_map<const ggml_tensor *, size_t> at;
+    for (size_t i = 0; i < nodes.size(); i++) at[nodes[i]] = i;
+    auto rewritten_between = [&](const ggml_tensor * m1, const ggml_tensor * m2) {
+        const ggml_tensor * o = owner(m1->src[1]);
+        size_t i = at.at(m1), j = at.at(m2);
+        if (i > j) std::swap(i, j);
+        for (size_t k = i + 1; k < j; k++)
+            if (writes_in_place(nodes[k]) && owner(nodes[k]) == o) return true;
+        return false;
+    };
     for (ggml_tensor * n : nodes) {
         if (n->op != GGML_OP_GLU || glu_kind_of(param_i32(n, 0)) < 0 || !is_contiguous(n)) continue;
         const ggml_tensor * gm = n->src[0], * um = n->src[1];
@@ -459,7 +475,7 @@ std::vector<fusion> find_fusions(const std::vector<ggml_tensor *> & nodes,
         fusion f{gm, nullptr, n, false, 0, gw->ne[0]};
         if (um) {
             if (param_i32(n, 1) != 0 || !gemm_matmul(um) || !in_piece.count(um) || read_outside(um, in_piece) ||
-                !is_contiguous(um) || packed_key(gm->src[1]) != packed_key(um->src[1]))
+                !is_contiguous(um) || packed_key(gm->src[1]) != packed_key(um->src[1]) || rewritten_between(gm, um))
                 continue;
             const ggml_tensor * uw = um->src[0];
             if (uw->type != gw->type || uw->ne[0] != gw->ne[0] || uw->ne[1] != gw->ne[1]) continue;
@@ -598,6 +614,8 @@ struct piece {
     const std::unordered_set<const ggml_tensor *> & in_piece;
     std::unordered_map<const ggml_tensor *, void *> staged;   // host inputs copied up
     std::unordered_map<const ggml_tensor *, void *> packed;   // owner -> packed bfp16 activations
+    // matmuls run later with their GLU or ADD -> their input packed where they stand
+    std::unordered_map<const ggml_tensor *, const void *> deferred_in;
     struct pending_out {
         ggml_tensor * t;
         void * dev;
@@ -680,6 +698,16 @@ struct piece {
         return fail(std::string(what) + ": " + zest_last_error());
     }
 
+    // Node n is about to write into another tensor's memory (in place): the
+    // packed copies of that tensor's rows, whole or a row range, are dropped,
+    // so later matmuls pack its new values.
+    void invalidate(const ggml_tensor * n) {
+        if (!writes_in_place(n)) return;
+        const ggml_tensor * o = owner(n);
+        for (auto it = packed.begin(); it != packed.end();)
+            it = owner(it->first) == o ? packed.erase(it) : std::next(it);
+    }
+
     // The expanded bfp16 operand of matmul input x: the packed copy made with
     // x (a fused norm or GLU), or packed here, once per piece.
     const void * packed_input(const ggml_tensor * x) {
@@ -696,6 +724,13 @@ struct piece {
             return nullptr;
         packed[packed_key(x)] = ap;
         return ap;
+    }
+
+    // The input of a matmul run with its GLU or ADD, as packed where the
+    // matmul stands (its input may be rewritten in place before then).
+    const void * deferred_input(const ggml_tensor * mm) {
+        const auto it = deferred_in.find(mm);
+        return it != deferred_in.end() ? it->second : packed_input(mm->src[1]);
     }
 
     // One GEMM submission: GGML_XDNA_FAIL_AFTER fails it; GGML_XDNA_NAN_AFTER
@@ -754,7 +789,7 @@ struct piece {
         const ggml_tensor * r = a->src[0] == n ? a->src[1] : a->src[0];
         const ggml_tensor * wt = n->src[0], * x = n->src[1];
         const int64_t K = wt->ne[0], N = wt->ne[1], M = x->ne[1];
-        const void * ap = packed_input(x);
+        const void * ap = deferred_input(n);
         if (!ap) return false;
         if (!ctx.ensure_weight(wt, ctx.stream, false, err)) return false;
         const void * wp = ctx.weights.at(key_of(wt)).packed;
@@ -782,7 +817,7 @@ struct piece {
     bool fused_glu_gemm(const fusion & f) {
         const ggml_tensor * x = f.gate_mm->src[1];
         const int64_t M = x->ne[1];
-        const void * ap = packed_input(x);
+        const void * ap = deferred_input(f.gate_mm);
         if (!ap) return false;
         if (!ctx.ensure_fused(f, ctx.stream, false, err)) return false;
         const void * wp = ctx.weights.at(fused_key(f)).packed;
@@ -812,6 +847,7 @@ struct piece {
         // RMS_NORM then MUL by a scale row, the norm read by nothing else: one kernel
         ggml_tensor * next = i + 1 < nodes.size() ? nodes[i + 1] : nullptr;
         if (next && next->op == GGML_OP_MUL && next->src[0] == n && exec_supports(next) && only_reader(n, next)) {
+            invalidate(next);
             const void * wd = in(next->src[1]);
             void * pk = packed_for(next, rows, d);
             float * y = pk && only_matmuls_read(next) ? nullptr : (float *) out(next);
@@ -868,12 +904,15 @@ struct piece {
         for (size_t i = 0; i < nodes.size(); i++) {
             ggml_tensor * n = nodes[i];
             if (is_noop(n)) continue;
+            invalidate(n);
             bool ok = true;
             switch (n->op) {
                 case GGML_OP_MUL_MAT: {
                     if (fused_mm.count(n) || res_mm.count(n)) {
-                        // runs with its GLU; its input is packed now, while it is sure to be intact
-                        ok = packed_input(n->src[1]) != nullptr;
+                        // runs with its GLU or ADD; its input is packed now, as it stands here
+                        const void * ap = packed_input(n->src[1]);
+                        ok = ap != nullptr;
+                        deferred_in[n] = ap;
                         break;
                     }
                     // the run of matmuls on the same input that follows

@@ -191,6 +191,27 @@ ggml_tensor * ggml_scale_bias(ggml_context * ctx, ggml_tensor * a, float s, floa
 }
 ggml_tensor * ggml_scale(ggml_context * ctx, ggml_tensor * a, float s) { return ggml_scale_bias(ctx, a, s, 0.0f); }
 
+// a whole-tensor view of `a` computed by `op` (its result lands in a's memory)
+static ggml_tensor * in_place(ggml_context * ctx, ggml_op op, ggml_tensor * a, ggml_tensor * b) {
+    ggml_tensor * t = view_of(ctx, a, op, 0);
+    memcpy(t->ne, a->ne, sizeof(t->ne));
+    memcpy(t->nb, a->nb, sizeof(t->nb));
+    t->src[1] = b;
+    return t;
+}
+ggml_tensor * ggml_add_inplace(ggml_context * ctx, ggml_tensor * a, ggml_tensor * b) {
+    return in_place(ctx, GGML_OP_ADD, a, b);
+}
+ggml_tensor * ggml_mul_inplace(ggml_context * ctx, ggml_tensor * a, ggml_tensor * b) {
+    return in_place(ctx, GGML_OP_MUL, a, b);
+}
+ggml_tensor * ggml_scale_inplace(ggml_context * ctx, ggml_tensor * a, float s) {
+    ggml_tensor * t = in_place(ctx, GGML_OP_SCALE, a, nullptr);
+    set_f32(t, 0, s);
+    set_f32(t, 1, 0.0f);
+    return t;
+}
+
 ggml_tensor * ggml_rms_norm(ggml_context * ctx, ggml_tensor * a, float eps) {
     ggml_tensor * t = op_result(ctx, GGML_OP_RMS_NORM, a->type, a->ne);
     t->src[0] = a;

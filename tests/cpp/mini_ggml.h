@@ -51,6 +51,10 @@ ggml_tensor * ggml_add(ggml_context * ctx, ggml_tensor * a, ggml_tensor * b);
 ggml_tensor * ggml_mul(ggml_context * ctx, ggml_tensor * a, ggml_tensor * b);
 ggml_tensor * ggml_scale(ggml_context * ctx, ggml_tensor * a, float s);
 ggml_tensor * ggml_scale_bias(ggml_context * ctx, ggml_tensor * a, float s, float b);
+// in place, as ggml's *_inplace ops: the result is a view of `a` and the op writes a's memory
+ggml_tensor * ggml_add_inplace(ggml_context * ctx, ggml_tensor * a, ggml_tensor * b);
+ggml_tensor * ggml_mul_inplace(ggml_context * ctx, ggml_tensor * a, ggml_tensor * b);
+ggml_tensor * ggml_scale_inplace(ggml_context * ctx, ggml_tensor * a, float s);
 ggml_tensor * ggml_rms_norm(ggml_context * ctx, ggml_tensor * a, float eps);
 ggml_tensor * ggml_get_rows(ggml_context * ctx, ggml_tensor * a, ggml_tensor * b);
 ggml_tensor * ggml_glu(ggml_context * ctx, ggml_tensor * a, ggml_glu_op op, bool swapped);

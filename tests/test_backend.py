@@ -2,7 +2,8 @@
 loads it (GGML_BACKEND_PATH -> ggml_backend_init): the C++ programs under
 tests/cpp, one per reference test (tests/test-dispatch-gate.cpp,
 test-memory-budget.cpp, test-mul-mat.cpp, test-host-ops.cpp,
-test-safe-start.cpp, and the mul-mat-npu-nan/-fail ctest cases).
+test-safe-start.cpp, and the mul-mat-npu-nan/-fail ctest cases), and a seeded
+sweep of random pieces (test_pieces_random).
 
 Without a GPU the gate and the budget run under GGML_XDNA_PLAN_ONLY=1
 (planning only); on the GPU they run for real, with the matmul, host-op and
@@ -111,6 +112,14 @@ def test_host_ops_gpu():
     # q, k and v as one grouped launch, and the down projection with the
     # residual ADD in its store
     assert "1 fused gate/up, 1 grouped, 1 with a residual add" in out
+
+
+@pytest.mark.gpu
+def test_random_pieces_gpu():
+    # seeded random chains of norms, matmul groups, fused gate/up, residual
+    # adds and in-place ops, every output against the same chain on the CPU;
+    # the batch floor lowered so that ragged token counts down to 1 are taken
+    run("test_pieces_random", "24", "1000", GGML_XDNA_MIN_BATCH="1")
 
 
 @pytest.mark.gpu
