@@ -971,7 +971,14 @@ struct piece {
                 }
                 default: return fail(std::string("unsupported op ") + op_name(n->op) + " (" + n->name + ")");
             }
-            if (!ok) return false;
+            if (!ok) {
+                // the small ops' paths stop at a missing pointer without a reason of their own
+                if (err.empty())
+                    err = std::string(op_name(n->op)) + " (" + n->name +
+                          "): an input or the result has no memory (device scratch exhausted, a host copy failed, "
+                          "or a tensor left unallocated)";
+                return false;
+            }
         }
         for (const pending_out & o : host_outs)
             if (hipMemcpyAsync(o.t->data, o.dev, nbytes(o.t), hipMemcpyDeviceToHost, ctx.stream) != hipSuccess)

@@ -443,10 +443,12 @@ ggml_backend_buffer_t ggml_backend_alloc_ctx_tensors_from_buft(ggml_context * ct
             if (buf->iface.init_tensor) buf->iface.init_tensor(buf, &t);
             off += (ggml_nbytes(&t) + align - 1) / align * align;
         }
+    // views, of this buffer's tensors or of any tensor already allocated (as
+    // ggml_backend_view_init does)
     for (ggml_tensor & t : ctx->tensors)
-        if (t.view_src && t.view_src->buffer == buf) {
+        if (t.view_src && t.view_src->buffer && !t.data) {
             t.data = (char *) t.view_src->data + t.view_offs;
-            t.buffer = buf;
+            t.buffer = t.view_src->buffer;
         }
     return buf;
 }

@@ -11,11 +11,13 @@
 //   block's input on either side or in place -> sometimes a SCALE, in place
 //   or not,
 // with random intermediate results made graph outputs (which undoes the
-// fusions that would skip writing them). Every output is checked against the
-// same chain run on the CPU in node order: the oracle's host ops in fp32,
-// every matmul input through the bfp16 encoder as the GPU packs it, fp64
-// products of the dequantised weights as the weight cache holds them (bfp16),
-// in-place results written into the memory they share.
+// fusions that would skip writing them), and the block's input in host memory
+// or the GPU's. Every output is checked against the same chain run on the CPU
+// in node order: the oracle's host ops in fp32, every matmul input through
+// the bfp16 encoder as the GPU packs it, fp64 products of the dequantised
+// weights as the weight cache holds them (bfp16), in-place results written
+// into the memory they share. The graph is then computed again (the backend
+// reuses its plan of it): the same bits.
 //
 // Bars: nrmse <= 5e-3 over each output and <= 5e-2 over each of its rows.
 // Only fp32 rounding differs between the two chains, but every matmul input
@@ -74,12 +76,15 @@ public:
     random_piece(uint64_t seed) : rng_(seed) {
         ggml_init_params ip = {ggml_tensor_overhead() * 256 + ggml_graph_overhead(), nullptr, true};
         wctx_ = ggml_init(ip);
+        ictx_ = ggml_init(ip);
         ctx_ = ggml_init(ip);
     }
     ~random_piece() {
         ggml_backend_buffer_free(abuf_);
+        ggml_backend_buffer_free(ibuf_);
         ggml_backend_buffer_free(wbuf_);
         ggml_free(ctx_);
+        ggml_free(ictx_);
         ggml_free(wctx_);
     }
 
@@ -89,10 +94,11 @@ public:
         static const int64_t tokens[] = {1, 3, 17, 64, 100, 255, 256, 257, 513, 1000, 1024, 1100, 1500};
         T_ = tokens[pick(13)];
         D_ = pick(2) ? 512 : 256;
+        host_input_ = coin(0.3);
         char buf[96];
-        snprintf(buf, sizeof(buf), "T=%lld D=%lld", (long long) T_, (long long) D_);
+        snprintf(buf, sizeof(buf), "T=%lld D=%lld%s", (long long) T_, (long long) D_, host_input_ ? " x on host" : "");
         describe = buf;
-        ggml_tensor * cur = ggml_new_tensor_2d(ctx_, GGML_TYPE_F32, D_, T_);
+        ggml_tensor * cur = ggml_new_tensor_2d(ictx_, GGML_TYPE_F32, D_, T_);
         ggml_set_name(cur, "x");
         ggml_set_input(cur);
         leaf(cur, 1.0f, 0.0f);
@@ -102,9 +108,11 @@ public:
     }
 
     bool run(ggml_backend_t be) {
+        ggml_backend_buffer_type_t host = ggml_backend_dev_buffer_type(ggml_backend_dev_by_type(GGML_BACKEND_DEVICE_TYPE_CPU));
         wbuf_ = ggml_backend_alloc_ctx_tensors(wctx_, be);
+        ibuf_ = host_input_ ? ggml_backend_alloc_ctx_tensors_from_buft(ictx_, host) : ggml_backend_alloc_ctx_tensors(ictx_, be);
         abuf_ = ggml_backend_alloc_ctx_tensors(ctx_, be);
-        if (!wbuf_ || !abuf_) return test_check(false, "%s: could not allocate", describe.c_str());
+        if (!wbuf_ || !ibuf_ || !abuf_) return test_check(false, "%s: could not allocate", describe.c_str());
         ggml_backend_buffer_set_usage(wbuf_, GGML_BACKEND_BUFFER_USAGE_WEIGHTS);
         for (weight & w : weights_) ggml_backend_tensor_set(w.t, w.bytes.data(), 0, w.bytes.size());
         for (auto & [t, v] : leaves_) ggml_backend_tensor_set(t, v.data(), 0, ggml_nbytes(t));
@@ -115,9 +123,11 @@ public:
             return test_check(false, "%s: graph_compute failed", describe.c_str());
         cpu_chain(gf);
         bool ok = true;
+        std::vector<fvec> first;
         for (ggml_tensor * t : outputs_) {
             fvec got((size_t) ggml_nelements(t));
             ggml_backend_tensor_get(t, got.data(), 0, ggml_nbytes(t));
+            first.push_back(got);
             const fvec & want = mem_.at(root(t));
             double se = 0, ss = 0, worst_row = 0;
             const int64_t w = t->ne[0];
@@ -136,14 +146,22 @@ public:
             ok &= test_check(std::isfinite(e) && e <= 5e-3 && worst_row <= 5e-2,
                              "%s: %-28s nrmse %.2e, worst row %.2e", describe.c_str(), t->name, e, worst_row);
         }
-        return ok;
+        // again: no in-place op here writes a leaf, so the results repeat
+        bool same = ggml_backend_graph_compute(be, gf) == GGML_STATUS_SUCCESS;
+        for (size_t i = 0; same && i < outputs_.size(); i++) {
+            fvec got(first[i].size());
+            ggml_backend_tensor_get(outputs_[i], got.data(), 0, ggml_nbytes(outputs_[i]));
+            same = memcmp(got.data(), first[i].data(), got.size() * sizeof(float)) == 0;
+        }
+        return test_check(same, "%s: computed again, the same bits", describe.c_str()) && ok;
     }
 
 private:
     test_rng rng_;
-    ggml_context * wctx_, * ctx_;
-    ggml_backend_buffer_t wbuf_ = nullptr, abuf_ = nullptr;
+    ggml_context * wctx_, * ictx_, * ctx_;  // weights, the block's input, the rest
+    ggml_backend_buffer_t wbuf_ = nullptr, ibuf_ = nullptr, abuf_ = nullptr;
     int64_t T_ = 0, D_ = 0;
+    bool host_input_ = false;
     int n_weights_ = 0;
     std::deque<weight> weights_;
     std::unordered_map<const ggml_tensor *, const weight *> weight_of_;
@@ -214,6 +232,7 @@ private:
     ggml_tensor * block(int b, ggml_tensor * x) {
         // attention-input side: a group of matmuls on the norm's result
         ggml_tensor * h = norm(x, b);
+        const bool h_is_leaf = root(h)->op == GGML_OP_NONE;  // the graph's input: never written
         ggml_tensor * hin = coin(0.3) ? ggml_reshape_2d(ctx_, h, D_, T_) : h;
         static const int64_t widths[] = {32, 64, 96, 160, 256};
         const int nproj = 1 + pick(3);
@@ -230,7 +249,7 @@ private:
             x = coin(0.5) ? ggml_add(ctx_, first, x) : ggml_add(ctx_, x, first);
             name(x, "attn_out%d", b);
         }
-        if (h != x && coin(0.25)) {
+        if (!h_is_leaf && coin(0.25)) {
             // the norm's result scaled in place after its matmuls, then multiplied again
             ggml_tensor * hs = ggml_scale_inplace(ctx_, h, 0.5f);
             name(hs, "norm%d*=0.5", b);
@@ -238,7 +257,7 @@ private:
             name(e, "after_inplace%d", b);
             output(e);
         }
-        if (h != x && T_ > 4 && coin(0.25)) {
+        if (T_ > 4 && coin(0.25)) {
             // a matmul over a range of the norm's rows
             const int64_t r0 = 1 + pick((int) (T_ / 2)), r1 = r0 + 1 + pick((int) (T_ - r0 - 1));
             ggml_tensor * v = ggml_view_2d(ctx_, h, D_, r1 - r0, h->nb[1], (size_t) r0 * h->nb[1]);
@@ -275,7 +294,7 @@ private:
         const int res = pick(4);
         ggml_tensor * out = res == 0   ? ggml_add(ctx_, dn, x)
                             : res == 1 ? ggml_add(ctx_, x, dn)
-                            : res == 2 && !(x->flags & GGML_TENSOR_FLAG_INPUT) ? ggml_add_inplace(ctx_, x, dn)
+                            : res == 2 && root(x)->op != GGML_OP_NONE ? ggml_add_inplace(ctx_, x, dn)
                                                                                 : dn;
         if (out != dn) name(out, "ffn_out%d", b);
         if (coin(0.3)) {
