@@ -15,6 +15,7 @@
 #include <atomic>
 #include <chrono>
 #include <cmath>
+#include <functional>
 #include <memory>
 #include <mutex>
 #include <string>
@@ -38,6 +39,7 @@ struct buffer_ctx {
 };
 
 void evict_buffer(const ggml_backend_buffer * b);
+void forget_weight(const void * data);
 
 void buf_free(ggml_backend_buffer_t b) {
     evict_buffer(b);  // its weights' cache entries go with it
@@ -47,10 +49,14 @@ void buf_free(ggml_backend_buffer_t b) {
 }
 void * buf_base(ggml_backend_buffer_t b) { return ((buffer_ctx *) b->context)->base; }
 ggml_status buf_init_tensor(ggml_backend_buffer_t, ggml_tensor *) { return GGML_STATUS_SUCCESS; }
+// A tensor written from outside a graph may be a weight whose cache entries
+// were converted from its old bytes: they are dropped first.
 void buf_memset(ggml_backend_buffer_t, ggml_tensor * t, uint8_t value, size_t offset, size_t size) {
+    forget_weight(t->data);
     (void) hipMemset((char *) t->data + offset, value, size);
 }
 void buf_set(ggml_backend_buffer_t, ggml_tensor * t, const void * data, size_t offset, size_t size) {
+    forget_weight(t->data);
     (void) hipMemcpy((char *) t->data + offset, data, size, hipMemcpyHostToDevice);
 }
 void buf_get(ggml_backend_buffer_t, const ggml_tensor * t, void * data, size_t offset, size_t size) {
@@ -59,9 +65,11 @@ void buf_get(ggml_backend_buffer_t, const ggml_tensor * t, void * data, size_t o
 ggml_backend_buffer_type * our_buft();
 bool buf_cpy(ggml_backend_buffer_t, const ggml_tensor * src, ggml_tensor * dst) {
     if (!src->buffer || src->buffer->buft != our_buft()) return false;
+    forget_weight(dst->data);
     return hipMemcpy(dst->data, src->data, nbytes(src), hipMemcpyDeviceToDevice) == hipSuccess;
 }
 void buf_clear(ggml_backend_buffer_t b, uint8_t value) {
+    evict_buffer(b);
     auto * c = (buffer_ctx *) b->context;
     (void) hipMemset(c->base, value, c->size);
 }
@@ -104,17 +112,24 @@ ggml_backend_buffer_type * our_buft() {
 
 // ---- the backend context ---------------------------------------------------
 
+// A weight-cache entry's key: the weight's buffer, address, type and shape;
+// for a fused gate/up entry also its partner, the up weight's address and
+// buffer (or, for one weight of both halves, which half is the gate).
 struct wkey {
     const void * buffer, * data;
     int type;
     int64_t ne0, ne1;
+    const void * partner = nullptr, * partner_buffer = nullptr;
     bool operator==(const wkey & o) const {
-        return buffer == o.buffer && data == o.data && type == o.type && ne0 == o.ne0 && ne1 == o.ne1;
+        return buffer == o.buffer && data == o.data && type == o.type && ne0 == o.ne0 && ne1 == o.ne1 &&
+               partner == o.partner;
     }
+    bool uses(const void * d) const { return data == d || partner == d; }
 };
 struct wkey_hash {
     size_t operator()(const wkey & k) const {
-        return std::hash<const void *>()(k.buffer) ^ (std::hash<const void *>()(k.data) * 31) ^ (size_t) k.ne1;
+        return std::hash<const void *>()(k.buffer) ^ (std::hash<const void *>()(k.data) * 31) ^ (size_t) k.ne1 ^
+               (std::hash<const void *>()(k.partner) * 131);
     }
 };
 wkey key_of(const ggml_tensor * w) { return {w->buffer, w->data, (int) w->type, w->ne[0], w->ne[1]}; }
@@ -131,10 +146,15 @@ struct fusion {
 };
 
 // The cache key of a fused pair: the gate weight's, type + 1000, 2F rows (as
-// xdna_npu::fused_key, src/xdna-npu.h:65).
+// xdna_npu::fused_key, src/xdna-npu.h:65), and the up weight it is paired
+// with, so that a gate met with another partner gets an entry of its own.
+const char k_up_rows_first = 0;
 wkey fused_key(const fusion & f) {
-    const ggml_tensor * w = f.gate_mm->src[0];
-    return {w->buffer, w->data, 1000 + (int) w->type, f.K, 2 * f.F};
+    const ggml_tensor * w = f.gate_mm->src[0], * u = f.up_mm ? f.up_mm->src[0] : nullptr;
+    wkey k{w->buffer, w->data, 1000 + (int) w->type, f.K, 2 * f.F};
+    k.partner = u ? u->data : f.swapped ? (const void *) &k_up_rows_first : nullptr;
+    k.partner_buffer = u ? (const void *) u->buffer : nullptr;
+    return k;
 }
 
 // GGML_XDNA_FAIL_AFTER=n: every GEMM submission after the n-th fails;
@@ -186,6 +206,8 @@ struct context {
     context();
     ~context();
     void evict(const ggml_backend_buffer * b);
+    void forget(const void * data);
+    void drop_where(const std::function<bool(const wkey &)> & stale);
 
     bool init(std::string & err) {
         if (hipSetDevice(device_index()) != hipSuccess || hipStreamCreateWithFlags(&stream, hipStreamNonBlocking) ||
@@ -356,10 +378,11 @@ context::~context() {
     if (loader) (void) hipStreamDestroy(loader);
 }
 
-void context::evict(const ggml_backend_buffer * b) {
+// Drops the cache entries `stale` names, after the work that may read them.
+void context::drop_where(const std::function<bool(const wkey &)> & stale) {
     bool synced = false;
     for (auto it = weights.begin(); it != weights.end();) {
-        if (it->first.buffer != b) {
+        if (!stale(it->first)) {
             ++it;
             continue;
         }
@@ -374,9 +397,25 @@ void context::evict(const ggml_backend_buffer * b) {
     }
 }
 
+// every entry of a weight in buffer b, or paired with one there
+void context::evict(const ggml_backend_buffer * b) {
+    drop_where([b](const wkey & k) { return k.buffer == b || k.partner_buffer == b; });
+}
+
+// every entry converted from the tensor at `data`
+void context::forget(const void * data) {
+    if (weights.empty()) return;
+    drop_where([data](const wkey & k) { return k.uses(data); });
+}
+
 void evict_buffer(const ggml_backend_buffer * b) {
     std::lock_guard<std::mutex> lk(g_ctx_mu);
     for (context * c : g_contexts) c->evict(b);
+}
+
+void forget_weight(const void * data) {
+    std::lock_guard<std::mutex> lk(g_ctx_mu);
+    for (context * c : g_contexts) c->forget(data);
 }
 
 // ---- graph execution ---------------------------------------------------------

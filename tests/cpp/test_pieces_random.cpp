@@ -17,7 +17,8 @@
 // the bfp16 encoder as the GPU packs it, fp64 products of the dequantised
 // weights as the weight cache holds them (bfp16), in-place results written
 // into the memory they share. The graph is then computed again (the backend
-// reuses its plan of it): the same bits.
+// reuses its plan of it): the same bits; and once more after one of its
+// weights is rewritten with new values (its cache entries must go).
 //
 // Bars: nrmse <= 5e-3 over each output and <= 5e-2 over each of its rows.
 // Only fp32 rounding differs between the two chains, but every matmul input
@@ -121,13 +122,36 @@ public:
         ggml_backend_plan_graph(be, gf);
         if (ggml_backend_graph_compute(be, gf) != GGML_STATUS_SUCCESS)
             return test_check(false, "%s: graph_compute failed", describe.c_str());
+        std::vector<fvec> first;
+        bool ok = check(gf, "", &first);
+        // again: no in-place op here writes a leaf, so the results repeat
+        bool same = ggml_backend_graph_compute(be, gf) == GGML_STATUS_SUCCESS;
+        for (size_t i = 0; same && i < outputs_.size(); i++) {
+            fvec got(first[i].size());
+            ggml_backend_tensor_get(outputs_[i], got.data(), 0, ggml_nbytes(outputs_[i]));
+            same = memcmp(got.data(), first[i].data(), got.size() * sizeof(float)) == 0;
+        }
+        ok &= test_check(same, "%s: computed again, the same bits", describe.c_str());
+        // one weight given new values in place
+        weight & w = weights_[(size_t) pick((int) weights_.size())];
+        quantize(w);
+        ggml_backend_tensor_set(w.t, w.bytes.data(), 0, w.bytes.size());
+        if (ggml_backend_graph_compute(be, gf) != GGML_STATUS_SUCCESS)
+            return test_check(false, "%s: graph_compute failed after %s was rewritten", describe.c_str(), w.t->name);
+        char after[96];
+        snprintf(after, sizeof(after), " (%s rewritten)", w.t->name);
+        return check(gf, after, nullptr) && ok;
+    }
+
+    // every output against the CPU chain; the GPU's values kept in `got_all`
+    bool check(const ggml_cgraph * gf, const char * when, std::vector<fvec> * got_all) {
+        mem_.clear();
         cpu_chain(gf);
         bool ok = true;
-        std::vector<fvec> first;
         for (ggml_tensor * t : outputs_) {
             fvec got((size_t) ggml_nelements(t));
             ggml_backend_tensor_get(t, got.data(), 0, ggml_nbytes(t));
-            first.push_back(got);
+            if (got_all) got_all->push_back(got);
             const fvec & want = mem_.at(root(t));
             double se = 0, ss = 0, worst_row = 0;
             const int64_t w = t->ne[0];
@@ -144,16 +168,9 @@ public:
             }
             const double e = std::sqrt(se / std::max(ss, 1e-30));
             ok &= test_check(std::isfinite(e) && e <= 5e-3 && worst_row <= 5e-2,
-                             "%s: %-28s nrmse %.2e, worst row %.2e", describe.c_str(), t->name, e, worst_row);
+                             "%s%s: %-28s nrmse %.2e, worst row %.2e", describe.c_str(), when, t->name, e, worst_row);
         }
-        // again: no in-place op here writes a leaf, so the results repeat
-        bool same = ggml_backend_graph_compute(be, gf) == GGML_STATUS_SUCCESS;
-        for (size_t i = 0; same && i < outputs_.size(); i++) {
-            fvec got(first[i].size());
-            ggml_backend_tensor_get(outputs_[i], got.data(), 0, ggml_nbytes(outputs_[i]));
-            same = memcmp(got.data(), first[i].data(), got.size() * sizeof(float)) == 0;
-        }
-        return test_check(same, "%s: computed again, the same bits", describe.c_str()) && ok;
+        return ok;
     }
 
 private:
@@ -195,6 +212,14 @@ private:
         char s[64];
         snprintf(s, sizeof(s), "blk.%d.w%d.weight", b, n_weights_++);
         ggml_set_name(w.t, s);
+        quantize(w);
+        weight_of_[w.t] = &w;
+        return w.t;
+    }
+    // new values for w: its GGUF bytes and what the GPU multiplies
+    void quantize(weight & w) {
+        const int64_t k = w.t->ne[0], n = w.t->ne[1];
+        const ggml_type ty = w.t->type;
         fvec f((size_t) (k * n));
         for (float & x : f) x = rng_.normal(0.0f, 0.05f);
         const size_t rb = ggml_row_size(ty, k);
@@ -203,8 +228,6 @@ private:
         w.deq.resize(f.size());
         for (int64_t i = 0; i < n; i++) ggml_dequantize_row(ty, w.bytes.data() + i * rb, w.deq.data() + i * k, k);
         w.deq = bfp16(w.deq, n, k);
-        weight_of_[w.t] = &w;
-        return w.t;
     }
     ggml_type any_type() { return k_types[pick(10)]; }
     ggml_type type_for(int64_t k) {
