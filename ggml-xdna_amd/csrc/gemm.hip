@@ -1577,19 +1577,26 @@ gemm_params band_of(const gemm_params & p, int64_t r0, int64_t rows) {
     return q;
 }
 
-// zest_gemm_group's checks and launches; `fixed` as for launch().
+bool aligned_to(const void * p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+// zest_gemm_group's checks and launches. A no-alloc call takes its split-K
+// workspace from the device's static array (looked up once the arguments
+// pass), else from the per-stream workspace.
 int gemm_group(const void * a, int64_t M, int64_t K, int n, const void * const * w, const int64_t * N,
                float * const * c, const int64_t * ldc, uint32_t * nonfinite, void * stream, const char * name,
-               const sk_space * fixed) {
+               bool noalloc) {
     ZEST_REQUIRE(a && w && N && c && ldc, "%s: null pointer", name);
     ZEST_REQUIRE(n >= 1 && n <= ZEST_GEMM_MAX_GROUP, "%s: %d weights (1..%d)", name, n, ZEST_GEMM_MAX_GROUP);
     ZEST_REQUIRE(M > 0 && K > 0 && K % 8 == 0, "%s: M=%lld K=%lld", name, (long long) M, (long long) K);
     ZEST_REQUIRE(zest_act_bytes(M, K) < (1ull << 31), "%s: activations must be under 2 GiB", name);
+    ZEST_REQUIRE(aligned_to(a, 16) && aligned_to(nonfinite, 4), "%s: a must be 16-byte aligned, nonfinite 4", name);
     gemm_params p = base_params(a, M, K, nonfinite);
     p.nw = n;
     int64_t ld_max = 0;
     for (int i = 0; i < n; i++) {
         ZEST_REQUIRE(w[i] && c[i], "%s: null weight or output %d", name, i);
+        ZEST_REQUIRE(aligned_to(w[i], 16) && aligned_to(c[i], 4),
+                     "%s: weight %d must be 16-byte aligned and its output 4", name, i);
         ZEST_REQUIRE(N[i] > 0 && ldc[i] >= N[i], "%s: weight %d: N=%lld ldc=%lld", name, i, (long long) N[i],
                      (long long) ldc[i]);
         ZEST_REQUIRE(zest_bfp16_bytes(N[i], K) < (1ull << 31), "%s: weight %d must be under 2 GiB (N=%lld K=%lld)",
@@ -1599,6 +1606,20 @@ int gemm_group(const void * a, int64_t M, int64_t K, int n, const void * const *
     }
     const int64_t band = band_rows(ld_max);
     ZEST_REQUIRE(band > 0, "%s: 256 output rows of %lld floats must be under 2 GiB", name, (long long) ld_max);
+    sk_space ws;
+    const sk_space * fixed = nullptr;
+    if (noalloc) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return zest::fail(ZEST_E_HIP, "%s: hipGetDevice failed", name);
+        uint8_t * base = nullptr;
+        const int st = scratch_address(dev, &base);
+        if (st != ZEST_OK) return st;
+        ws.partial = reinterpret_cast<float *>(base);
+        ws.partial_bytes = ZEST_NOALLOC_PARTIAL_BYTES;
+        ws.counters = reinterpret_cast<uint32_t *>(base + ZEST_NOALLOC_PARTIAL_BYTES);
+        ws.n_counters = ZEST_NOALLOC_COUNTERS;
+        fixed = &ws;
+    }
     const hipStream_t s = zest::as_stream(stream);
     for (int64_t r0 = 0; r0 < M; r0 += band) {
         const int st = launch_any<EPI_PLAIN>(band_of(p, r0, std::min(band, M - r0)), N, s, name, fixed);
@@ -1620,23 +1641,13 @@ int scratch_setup(int dev) {
 
 extern "C" int zest_gemm_group(const void * a, int64_t M, int64_t K, int n, const void * const * w, const int64_t * N,
                                float * const * c, const int64_t * ldc, uint32_t * nonfinite, void * stream) {
-    return gemm_group(a, M, K, n, w, N, c, ldc, nonfinite, stream, "zest_gemm", nullptr);
+    return gemm_group(a, M, K, n, w, N, c, ldc, nonfinite, stream, "zest_gemm", false);
 }
 
 extern "C" int zest_gemm_group_noalloc(const void * a, int64_t M, int64_t K, int n, const void * const * w,
                                        const int64_t * N, float * const * c, const int64_t * ldc,
                                        uint32_t * nonfinite, void * stream) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return zest::fail(ZEST_E_HIP, "zest_gemm_group_noalloc: hipGetDevice failed");
-    uint8_t * base = nullptr;
-    const int st = scratch_address(dev, &base);
-    if (st != ZEST_OK) return st;
-    sk_space ws;
-    ws.partial = reinterpret_cast<float *>(base);
-    ws.partial_bytes = ZEST_NOALLOC_PARTIAL_BYTES;
-    ws.counters = reinterpret_cast<uint32_t *>(base + ZEST_NOALLOC_PARTIAL_BYTES);
-    ws.n_counters = ZEST_NOALLOC_COUNTERS;
-    return gemm_group(a, M, K, n, w, N, c, ldc, nonfinite, stream, "zest_gemm_group_noalloc", &ws);
+    return gemm_group(a, M, K, n, w, N, c, ldc, nonfinite, stream, "zest_gemm_group_noalloc", true);
 }
 
 extern "C" int zest_gemm(const void * a, int64_t M, const void * w, int64_t N, int64_t K, float * c, int64_t ldc,
@@ -1653,6 +1664,8 @@ extern "C" int zest_gemm_residual(const void * a, int64_t M, const void * w, int
                  (long long) ldr, (long long) N);
     ZEST_REQUIRE((reinterpret_cast<uintptr_t>(res) & 15) == 0 && ldr % 4 == 0,
                  "zest_gemm_residual: the residual's rows must be 16-byte aligned");
+    ZEST_REQUIRE(aligned_to(a, 16) && aligned_to(w, 16) && aligned_to(c, 4) && aligned_to(nonfinite, 4),
+                 "zest_gemm_residual: a and w must be 16-byte aligned, c and nonfinite 4");
     ZEST_REQUIRE(zest_act_bytes(M, K) < (1ull << 31) && zest_bfp16_bytes(N, K) < (1ull << 31),
                  "zest_gemm_residual: operands must be under 2 GiB");
     const int64_t band = band_rows(std::max(ldc, ldr));
@@ -1676,6 +1689,9 @@ extern "C" int zest_gemm_glu(int kind, const void * a, int64_t M, const void * w
     ZEST_REQUIRE(M > 0 && F > 0 && F % 32 == 0 && K > 0 && K % 8 == 0, "zest_gemm_glu: M=%lld F=%lld K=%lld",
                  (long long) M, (long long) F, (long long) K);
     ZEST_REQUIRE(!h || ldh >= F, "zest_gemm_glu: ldh %lld < F %lld", (long long) ldh, (long long) F);
+    ZEST_REQUIRE(aligned_to(a, 16) && aligned_to(w_gu, 16) && aligned_to(xout, 16) && aligned_to(h, 4) &&
+                     aligned_to(nonfinite, 4),
+                 "zest_gemm_glu: a, w_gu and xout must be 16-byte aligned, h and nonfinite 4");
     ZEST_REQUIRE(zest_act_bytes(M, K) < (1ull << 31) && zest_bfp16_bytes(2 * F, K) < (1ull << 31) &&
                      zest_act_bytes(M, F) < (1ull << 31),
                  "zest_gemm_glu: operands must be under 2 GiB (M=%lld F=%lld K=%lld)", (long long) M, (long long) F,

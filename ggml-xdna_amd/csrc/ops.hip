@@ -415,6 +415,7 @@ int zest_rms_norm(const float * x, int64_t rows, int64_t d, float eps, const flo
     ZEST_REQUIRE(x && (y || packed), "zest_rms_norm: null pointer");
     ZEST_REQUIRE(rows > 0 && d > 0, "zest_rms_norm: rows=%lld d=%lld", (long long) rows, (long long) d);
     ZEST_REQUIRE(!packed || d % 8 == 0, "zest_rms_norm: packing needs d %% 8 == 0");
+    ZEST_REQUIRE(aligned16(packed), "zest_rms_norm: packed must be 16-byte aligned");
     // with a packed output, the grid also covers its padding rows (zeroed)
     const int64_t R_pad = zest_rows_padded(rows), grid_rows = packed ? R_pad : rows;
     const int64_t chunks = (zest_k_padded(d) + 255) / 256;  // the output pass covers the padded width
@@ -440,6 +441,7 @@ int zest_glu(int kind, const float * g, int64_t sg, const float * u, int64_t su,
     ZEST_REQUIRE(g && u && (y || packed), "zest_glu: null pointer");
     ZEST_REQUIRE(rows > 0 && f > 0 && sg >= f && su >= f, "zest_glu: bad shape");
     ZEST_REQUIRE(!packed || f % 8 == 0, "zest_glu: packing needs f %% 8 == 0");
+    ZEST_REQUIRE(aligned16(packed), "zest_glu: packed must be 16-byte aligned");
     const int64_t R_pad = zest_rows_padded(rows), gr = packed ? R_pad : rows;
     const int64_t n = gr * (zest_k_padded(f) / 16);
     const dim3 grid(blocks_for(n, 256));
@@ -496,6 +498,7 @@ int zest_rope(const float * x, int64_t T, int64_t heads, int64_t d, const int32_
 
 int zest_check_finite(const float * y, int64_t rows, int64_t cols, int64_t ld, uint32_t * flag, void * stream) {
     ZEST_REQUIRE(y && flag && rows > 0 && cols > 0 && ld >= cols, "zest_check_finite: bad arguments");
+    ZEST_REQUIRE((reinterpret_cast<uintptr_t>(flag) & 3) == 0, "zest_check_finite: flag must be 4-byte aligned");
     hipLaunchKernelGGL(check_finite_kernel, row_grid(rows, cols), dim3(256), 0, zest::as_stream(stream), y, rows, cols,
                        ld, flag);
     return zest::check_launch("zest_check_finite");

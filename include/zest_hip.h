@@ -123,7 +123,9 @@ ZEST_API int zest_convert_weight(int type, const void *raw, int64_t N, int64_t K
  * mm_bfp_acc.cc:44-116, 258-278). */
 ZEST_API int zest_gemm(const void *a, int64_t M, const void *w, int64_t N, int64_t K, float *c, int64_t ldc,
                        uint32_t *nonfinite, void *stream);
-/* Limits of zest_gemm, zest_gemm_residual and zest_gemm_group: the expanded
+/* Limits of zest_gemm, zest_gemm_residual and zest_gemm_group: a and every
+ * w 16-byte aligned (as the packers and converters write them), outputs and
+ * `nonfinite` 4-byte aligned; the expanded
  * activations and each packed weight under 2 GiB, and 256 rows of the output
  * (and of the residual) under 2 GiB. A taller output runs as launches over
  * bands of rows, each band's output span under 2 GiB (whole 256-row tiles;
@@ -199,7 +201,7 @@ ZEST_API int zest_convert_weight_gu(int type, const void *gate, const void *up, 
  * zest_gemm(a, w_gu) whenever that call runs as one launch (its fp32 output,
  * M x 2F floats, under 2 GiB); xout is then zest_pack_act_x of that h.
  * `nonfinite` as for zest_gemm, over g, u and h.
- * F % 32 == 0.
+ * F % 32 == 0; a, w_gu and xout 16-byte aligned, h 4.
  * Replaces the reference's fused SwiGLU matmul: find_fusions
  * (src/xdna-exec.cpp:399-431) and the NPU kernel's output mode 2
  * (kernels/bfp16_gemm/aie_kernels/aie2p/mm_bfp_acc.cc:258-278), which stores
@@ -212,7 +214,7 @@ ZEST_API int zest_gemm_glu(int kind, const void *a, int64_t M, const void *w_gu,
 /* y = RMS_NORM(x) (eps), optionally times a scale row w[d] (the MUL that
  * follows a norm, :258-277). y (fp32 rows, may be NULL) and/or packed (the
  * next matmul's input as zest_pack_act_x writes it, zest_act_bytes(rows, d)
- * bytes, may be NULL). */
+ * bytes, 16-byte aligned, may be NULL). */
 ZEST_API int zest_rms_norm(const float *x, int64_t rows, int64_t d, float eps, const float *w, float *y, void *packed,
                            void *stream);
 
