@@ -182,7 +182,10 @@ struct context {
         void * packed = nullptr;
         hipEvent_t ready = nullptr;  // recorded on `loader` when built at load
     };
+    // The cache, and the lock other threads take to drop entries from it (a
+    // buffer freed or a weight rewritten while this context computes).
     std::unordered_map<wkey, weight_entry, wkey_hash> weights;
+    std::mutex weights_mu;
     int64_t built_at_load = 0, built_in_graph = 0;
 
     // per-graph device workspace: grow-only blocks, handed out from the start
@@ -238,10 +241,13 @@ struct context {
         return b.p;
     }
 
-    // The weight's cache entry, converted from its raw GGUF bytes where they
-    // are (device memory in our buffers; host memory goes up first) on
-    // `on_stream`; an entry built at load is waited for on the compute stream.
-    bool ensure_weight(const ggml_tensor * w, hipStream_t on_stream, bool at_load, std::string & err) {
+    // The weight's cache entry (its packed bytes into *packed), converted
+    // from its raw GGUF bytes where they are (device memory in our buffers;
+    // host memory goes up first) on `on_stream`; an entry built at load is
+    // waited for on the compute stream.
+    bool ensure_weight(const ggml_tensor * w, hipStream_t on_stream, bool at_load, std::string & err,
+                       const void ** packed = nullptr) {
+        std::lock_guard<std::mutex> lk(weights_mu);
         const wkey key = key_of(w);
         auto it = weights.find(key);
         if (it != weights.end()) {
@@ -251,6 +257,7 @@ struct context {
                     return false;
                 }
             }
+            if (packed) *packed = it->second.packed;
             return true;
         }
         const int64_t K = w->ne[0], N = w->ne[1];
@@ -288,12 +295,15 @@ struct context {
             built_in_graph++;
         }
         weights.emplace(key, e);
+        if (packed) *packed = e.packed;
         return true;
     }
 
     // The same for a fused gate/up pair: both weights' rows, interleaved into
     // one entry (zest_convert_weight_gu).
-    bool ensure_fused(const fusion & f, hipStream_t on_stream, bool at_load, std::string & err) {
+    bool ensure_fused(const fusion & f, hipStream_t on_stream, bool at_load, std::string & err,
+                      const void ** packed = nullptr) {
+        std::lock_guard<std::mutex> lk(weights_mu);
         const wkey key = fused_key(f);
         auto it = weights.find(key);
         if (it != weights.end()) {
@@ -301,6 +311,7 @@ struct context {
                 err = "waiting for a weight conversion failed";
                 return false;
             }
+            if (packed) *packed = it->second.packed;
             return true;
         }
         const ggml_tensor * gw = f.gate_mm->src[0], * uw = f.up_mm ? f.up_mm->src[0] : nullptr;
@@ -346,6 +357,7 @@ struct context {
             built_in_graph++;
         }
         weights.emplace(key, e);
+        if (packed) *packed = e.packed;
         return true;
     }
 };
@@ -378,7 +390,8 @@ context::~context() {
     if (loader) (void) hipStreamDestroy(loader);
 }
 
-// Drops the cache entries `stale` names, after the work that may read them.
+// Drops the cache entries `stale` names, after the work that may read them
+// (weights_mu held).
 void context::drop_where(const std::function<bool(const wkey &)> & stale) {
     bool synced = false;
     for (auto it = weights.begin(); it != weights.end();) {
@@ -399,11 +412,13 @@ void context::drop_where(const std::function<bool(const wkey &)> & stale) {
 
 // every entry of a weight in buffer b, or paired with one there
 void context::evict(const ggml_backend_buffer * b) {
+    std::lock_guard<std::mutex> lk(weights_mu);
     drop_where([b](const wkey & k) { return k.buffer == b || k.partner_buffer == b; });
 }
 
 // every entry converted from the tensor at `data`
 void context::forget(const void * data) {
+    std::lock_guard<std::mutex> lk(weights_mu);
     if (weights.empty()) return;
     drop_where([data](const wkey & k) { return k.uses(data); });
 }
@@ -803,8 +818,7 @@ struct piece {
         float * y[ZEST_GEMM_MAX_GROUP];
         for (size_t i = 0; i < ms.size(); i++) {
             const ggml_tensor * wt = ms[i]->src[0];
-            if (!ctx.ensure_weight(wt, ctx.stream, false, err)) return false;
-            w[i] = ctx.weights.at(key_of(wt)).packed;
+            if (!ctx.ensure_weight(wt, ctx.stream, false, err, &w[i])) return false;
             N[i] = wt->ne[1];
             ldc[i] = (int64_t) (ms[i]->nb[1] / 4);
             y[i] = (float *) out(ms[i]);
@@ -830,8 +844,8 @@ struct piece {
         const int64_t K = wt->ne[0], N = wt->ne[1], M = x->ne[1];
         const void * ap = deferred_input(n);
         if (!ap) return false;
-        if (!ctx.ensure_weight(wt, ctx.stream, false, err)) return false;
-        const void * wp = ctx.weights.at(key_of(wt)).packed;
+        const void * wp = nullptr;
+        if (!ctx.ensure_weight(wt, ctx.stream, false, err, &wp)) return false;
         const float * rd = (const float *) in(r);
         float * y = (float *) out(a);
         if (!rd || !y) return fail("out of device memory for a residual add");
@@ -858,8 +872,8 @@ struct piece {
         const int64_t M = x->ne[1];
         const void * ap = deferred_input(f.gate_mm);
         if (!ap) return false;
-        if (!ctx.ensure_fused(f, ctx.stream, false, err)) return false;
-        const void * wp = ctx.weights.at(fused_key(f)).packed;
+        const void * wp = nullptr;
+        if (!ctx.ensure_fused(f, ctx.stream, false, err, &wp)) return false;
         ggml_tensor * n = f.glu;
         void * pk = packed_for(n, M, f.F);
         float * y = pk && only_matmuls_read(n) ? nullptr : (float *) out(n);

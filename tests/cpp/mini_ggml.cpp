@@ -6,6 +6,7 @@
 
 #include <dlfcn.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -496,7 +497,7 @@ float test_rng::normal(float mean, float sd) {
     return mean + sd * (float) (r * std::cos(th));
 }
 
-static int g_failures = 0;
+static std::atomic<int> g_failures{0};  // programs may check from several threads
 int test_check(bool ok, const char * fmt, ...) {
     char buf[512];
     va_list ap;

@@ -36,6 +36,7 @@
 #include <cstring>
 #include <deque>
 #include <string>
+#include <thread>
 #include <unordered_map>
 #include <vector>
 
@@ -411,28 +412,44 @@ private:
 
 }  // namespace
 
+// test_pieces_random [CASES [SEED [THREADS]]]: with THREADS > 1, each thread
+// runs CASES cases of its own (seeds SEED + 1000 t + c) on a backend of its
+// own, all at once, as llama.cpp contexts on several threads do: they share
+// the library, the gate's reader log and the budget, and every write of a
+// tensor looks through every context's weight cache.
 int main(int argc, char ** argv) {
     const int cases = argc > 1 ? atoi(argv[1]) : 24;
     const uint64_t seed0 = argc > 2 ? strtoull(argv[2], nullptr, 10) : 1000;
+    const int threads = argc > 3 ? std::max(1, atoi(argv[3])) : 1;
     ggml_backend_load_all();
     ggml_backend_dev_t dev = ggml_backend_dev_by_name("XDNA0");
     if (!dev) {
         fprintf(stderr, "XDNA device not registered - is GGML_BACKEND_PATH set?\n");
         return 2;
     }
-    ggml_backend_t be = ggml_backend_dev_init(dev, nullptr);
-    if (!be) {
-        fprintf(stderr, "cannot start the backend\n");
-        return 2;
+    std::vector<ggml_backend_t> backends;
+    for (int t = 0; t < threads; t++) {
+        backends.push_back(ggml_backend_dev_init(dev, nullptr));
+        if (!backends.back()) {
+            fprintf(stderr, "cannot start the backend\n");
+            return 2;
+        }
     }
-    for (int c = 0; c < cases; c++) {
-        random_piece p(seed0 + (uint64_t) c);
-        p.build();
-        printf("case %d (seed %llu): %s\n", c, (unsigned long long) (seed0 + c), p.describe.c_str());
-        fflush(stdout);
-        p.run(be);
-    }
-    ggml_backend_free(be);
+    auto work = [&](int t) {
+        for (int c = 0; c < cases; c++) {
+            const uint64_t seed = seed0 + 1000 * (uint64_t) t + (uint64_t) c;
+            random_piece p(seed);
+            p.build();
+            printf("thread %d case %d (seed %llu): %s\n", t, c, (unsigned long long) seed, p.describe.c_str());
+            fflush(stdout);
+            p.run(backends[t]);
+        }
+    };
+    std::vector<std::thread> pool;
+    for (int t = 1; t < threads; t++) pool.emplace_back(work, t);
+    work(0);
+    for (std::thread & th : pool) th.join();
+    for (ggml_backend_t be : backends) ggml_backend_free(be);
     printf("%s\n", test_failures() ? "FAILED" : "ALL PASS");
     return test_failures() ? 1 : 0;
 }

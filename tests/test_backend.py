@@ -123,6 +123,14 @@ def test_random_pieces_gpu():
 
 
 @pytest.mark.gpu
+def test_random_pieces_on_threads_gpu():
+    # four backends computing on four threads at once, sharing the library,
+    # the gate's reader log and the budget; each thread's tensor writes look
+    # through every context's weight cache
+    run("test_pieces_random", "6", "5000", "4", GGML_XDNA_MIN_BATCH="1")
+
+
+@pytest.mark.gpu
 def test_injected_failure_gpu():
     run("test_failure", GGML_XDNA_FAIL_AFTER="0")
 
