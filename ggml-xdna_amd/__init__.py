@@ -53,6 +53,7 @@ SIGNATURES = {
     "zest_gemm_residual": (_c_i, [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p]),
     "zest_gemm_group": (_c_i, [_c_p, _c_i64, _c_i64, _c_i, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p]),
     "zest_gemm_group_noalloc": (_c_i, [_c_p, _c_i64, _c_i64, _c_i, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p]),
+    "zest_release_stream": (_c_i, [_c_p]),
     "zest_convert_weight_gu": (_c_i, [_c_i, _c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p]),
     "zest_gemm_glu": (_c_i, [_c_i, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_p]),
     "zest_rms_norm": (_c_i, [_c_p, _c_i64, _c_i64, _c_f, _c_p, _c_p, _c_p, _c_p]),

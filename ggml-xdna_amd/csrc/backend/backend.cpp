@@ -386,6 +386,9 @@ context::~context() {
     for (block & b : blocks) (void) hipFree(b.p);
     if (nonfinite) (void) hipFree(nonfinite);
     if (nonfinite_host) (void) hipHostFree(nonfinite_host);
+    // the library's split-K workspaces for these streams go with them
+    if (stream) (void) zest_release_stream(stream);
+    if (loader) (void) zest_release_stream(loader);
     if (stream) (void) hipStreamDestroy(stream);
     if (loader) (void) hipStreamDestroy(loader);
 }

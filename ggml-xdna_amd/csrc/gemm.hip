@@ -1202,13 +1202,15 @@ int cu_count(int dev) {
     return n;
 }
 
+// The split-K workspaces, by device and stream (until zest_release_stream).
+std::mutex g_sk_mu;
+std::map<std::pair<int, hipStream_t>, sk_space> g_sk_spaces;
+
 int sk_reserve(hipStream_t s, size_t partial_bytes, size_t n_counters, sk_space & out, const char * name) {
-    static std::mutex mu;
-    static std::map<std::pair<int, hipStream_t>, sk_space> spaces;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return zest::fail(ZEST_E_HIP, "%s: hipGetDevice failed", name);
-    std::lock_guard<std::mutex> lock(mu);
-    sk_space & sp = spaces[{dev, s}];
+    std::lock_guard<std::mutex> lock(g_sk_mu);
+    sk_space & sp = g_sk_spaces[{dev, s}];
     // a launch still running on the stream may use the buffers being replaced
     if ((sp.partial_bytes < partial_bytes || sp.n_counters < n_counters) && (sp.partial || sp.counters) &&
         hipStreamSynchronize(s) != hipSuccess)
@@ -1648,6 +1650,26 @@ extern "C" int zest_gemm_group_noalloc(const void * a, int64_t M, int64_t K, int
                                        const int64_t * N, float * const * c, const int64_t * ldc,
                                        uint32_t * nonfinite, void * stream) {
     return gemm_group(a, M, K, n, w, N, c, ldc, nonfinite, stream, "zest_gemm_group_noalloc", true);
+}
+
+extern "C" int zest_release_stream(void * stream) {
+    const hipStream_t s = zest::as_stream(stream);
+    std::lock_guard<std::mutex> lock(g_sk_mu);
+    bool synced = false;
+    for (auto it = g_sk_spaces.begin(); it != g_sk_spaces.end();) {
+        if (it->first.second != s) {
+            ++it;
+            continue;
+        }
+        // launches still queued on the stream may use the workspace
+        if (!synced && hipStreamSynchronize(s) != hipSuccess)
+            return zest::fail(ZEST_E_HIP, "zest_release_stream: stream synchronize");
+        synced = true;
+        if (it->second.partial) (void) hipFree(it->second.partial);
+        if (it->second.counters) (void) hipFree(it->second.counters);
+        it = g_sk_spaces.erase(it);
+    }
+    return ZEST_OK;
 }
 
 extern "C" int zest_gemm(const void * a, int64_t M, const void * w, int64_t N, int64_t K, float * c, int64_t ldc,

@@ -148,8 +148,8 @@ ZEST_API int zest_gemm_residual(const void *a, int64_t M, const void *w, int64_t
  * (:509-547). A launch whose whole tiles would leave CUs idle splits each
  * tile's K among workgroups (split-K) and sums the splits in a fixed order,
  * through a workspace the library allocates per device and stream on first
- * use (and grows, synchronizing the stream): calls that share a stream run
- * in order and never share it concurrently. A launch of at most one small
+ * use (and grows, synchronizing the stream; zest_release_stream frees it):
+ * calls that share a stream run in order and never share it concurrently. A launch of at most one small
  * tile a CU may instead split each tile's K between two groups of waves in
  * one workgroup (K-groups), whose sums meet in LDS, also in a fixed order.
  * The same holds for zest_gemm and zest_gemm_glu, which run through the
@@ -157,6 +157,15 @@ ZEST_API int zest_gemm_residual(const void *a, int64_t M, const void *w, int64_t
 #define ZEST_GEMM_MAX_GROUP 4
 ZEST_API int zest_gemm_group(const void *a, int64_t M, int64_t K, int n, const void *const *w, const int64_t *N,
                              float *const *c, const int64_t *ldc, uint32_t *nonfinite, void *stream);
+
+/* Frees the split-K workspace the library holds for `stream` (on every
+ * device), after the launches queued on it finish. Call it before destroying
+ * a stream that GEMMs ran on: the library cannot see a stream go, and a
+ * process that makes and destroys streams would otherwise keep one workspace
+ * per stream it ever used. A later GEMM on the stream allocates a new one;
+ * a stream that holds none is left as it is. It has no counterpart in the
+ * reference, whose NPU buffers live with its context. */
+ZEST_API int zest_release_stream(void *stream);
 
 /* zest_gemm_group for callers that cannot allocate device memory (code under
  * HIP graph capture, serving loops and harnesses that forbid hipMalloc). It

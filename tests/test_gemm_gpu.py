@@ -546,3 +546,31 @@ def test_gemm_output_bands(zest_gpu, oracle):
     assert gemm_check(outs[1][sel].cpu().numpy(), r64, ab, K)[0] <= 1.0
     n64, nab = oracle.mul_mat_f64(oracle.decode_rows(zest_gpu.tiles_to_blocks(wn.cpu().numpy(), 512, K)), ad)
     assert gemm_check(outs[0][sel].cpu().numpy(), n64, nab, K)[0] <= 1.0
+
+
+def test_release_stream_frees_and_regrows_the_split_k_workspace(zest_gpu, oracle):
+    # a few tiles over a long K: the plan splits K among workgroups, which
+    # takes the stream's workspace; released, the next call on the stream
+    # allocates it again and computes the same bits
+    import torch
+    M, N, K = 64, 512, 16384
+    x = wide_blocks(M, K, 5)
+    w = wide_blocks(N, K, 6, 0.02)
+    a = zest_gpu.pack_act_x(_dev(x))
+    wp = zest_gpu.convert_weight(0, _dev(w.view(np.uint8)), N, K)
+    lib = zest_gpu.lib()
+    s = torch.cuda.Stream()
+    outs = []
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            outs.append(zest_gpu.gemm(a, M, wp, N, K))
+            assert lib.zest_release_stream(s.cuda_stream) == 0
+            assert lib.zest_release_stream(s.cuda_stream) == 0      # nothing held any more
+    s.synchronize()
+    assert lib.zest_release_stream(None) == 0                       # the null stream's, if any
+    c0, c1 = (o.cpu().numpy() for o in outs)
+    assert np.array_equal(c0.view(np.uint32), c1.view(np.uint32))
+    rows = np.arange(0, M, 7)
+    r64, ab = oracle.mul_mat_f64(decoded(zest_gpu, oracle, wp, N, K), decoded_act(zest_gpu, oracle, a, M, K)[rows])
+    worst, _ = gemm_check(c0[rows], r64, ab, K)
+    assert worst <= 1.0

@@ -195,7 +195,7 @@ def test_every_entry_point_rejects_bad_arguments_before_the_gpu():
     covered = {name for name, _, _ in cases}
     # every entry point that takes device memory has cases here
     assert declared - covered <= {"zest_init", "zest_self_test", "zest_last_error", "zest_rows_pad", "zest_k_pad",
-                                  "zest_bfp16_bytes", "zest_act_bytes", "zest_raw_row_bytes"}
+                                  "zest_bfp16_bytes", "zest_act_bytes", "zest_raw_row_bytes", "zest_release_stream"}
     for name, args, want in cases:
         got = getattr(lib, name)(*args)
         msg = lib.zest_last_error().decode()
