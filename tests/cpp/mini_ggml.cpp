@@ -155,6 +155,15 @@ ggml_tensor * ggml_reshape_2d(ggml_context * ctx, ggml_tensor * a, int64_t ne0, 
     return t;
 }
 
+ggml_tensor * ggml_reshape_3d(ggml_context * ctx, ggml_tensor * a, int64_t ne0, int64_t ne1, int64_t ne2) {
+    ggml_tensor * t = view_of(ctx, a, GGML_OP_RESHAPE, 0);
+    t->ne[0] = ne0;
+    t->ne[1] = ne1;
+    t->ne[2] = ne2;
+    set_strides(t);
+    return t;
+}
+
 ggml_tensor * ggml_mul_mat(ggml_context * ctx, ggml_tensor * a, ggml_tensor * b) {
     const int64_t ne[4] = {a->ne[1], b->ne[1], b->ne[2], b->ne[3]};
     ggml_tensor * t = op_result(ctx, GGML_OP_MUL_MAT, GGML_TYPE_F32, ne);

@@ -45,6 +45,7 @@ size_t ggml_row_size(ggml_type type, int64_t ne);
 // ops, with ggml's op_params conventions
 ggml_tensor * ggml_view_2d(ggml_context * ctx, ggml_tensor * a, int64_t ne0, int64_t ne1, size_t nb1, size_t offset);
 ggml_tensor * ggml_reshape_2d(ggml_context * ctx, ggml_tensor * a, int64_t ne0, int64_t ne1);
+ggml_tensor * ggml_reshape_3d(ggml_context * ctx, ggml_tensor * a, int64_t ne0, int64_t ne1, int64_t ne2);
 ggml_tensor * ggml_mul_mat(ggml_context * ctx, ggml_tensor * a, ggml_tensor * b);
 ggml_tensor * ggml_mul_mat_id(ggml_context * ctx, ggml_tensor * as, ggml_tensor * b, ggml_tensor * ids);
 ggml_tensor * ggml_add(ggml_context * ctx, ggml_tensor * a, ggml_tensor * b);

@@ -4,8 +4,10 @@
 //   a norm (RMS_NORM with its scale row, RMS_NORM alone, the scale row
 //   multiplied in place, or none) -> one to three matmuls on its result (a
 //   group), sometimes through a reshape, sometimes a residual ADD of the
-//   first with the matmul on either side, sometimes a matmul over a range of
-//   rows, sometimes the norm's result scaled in place and multiplied again ->
+//   first with the matmul on either side, sometimes one of them taken as
+//   heads through ROPE (normal or NeoX, partial, YaRN, frequency factors),
+//   sometimes a matmul over a range of rows, sometimes the norm's result
+//   scaled in place and multiplied again ->
 //   a second norm -> gate/up as two matmuls or as one of 2F rows (either half
 //   first) under a random GLU kind -> the down projection, added to the
 //   block's input on either side or in place -> sometimes a SCALE, in place
@@ -118,6 +120,7 @@ public:
         ggml_backend_buffer_set_usage(wbuf_, GGML_BACKEND_BUFFER_USAGE_WEIGHTS);
         for (weight & w : weights_) ggml_backend_tensor_set(w.t, w.bytes.data(), 0, w.bytes.size());
         for (auto & [t, v] : leaves_) ggml_backend_tensor_set(t, v.data(), 0, ggml_nbytes(t));
+        for (auto & [t, v] : positions_) ggml_backend_tensor_set(t, v.data(), 0, ggml_nbytes(t));
         ggml_cgraph * gf = ggml_new_graph(ctx_);
         for (ggml_tensor * t : outputs_) ggml_build_forward_expand(gf, t);
         ggml_backend_plan_graph(be, gf);
@@ -184,6 +187,7 @@ private:
     std::deque<weight> weights_;
     std::unordered_map<const ggml_tensor *, const weight *> weight_of_;
     std::vector<std::pair<ggml_tensor *, fvec>> leaves_;
+    std::vector<std::pair<ggml_tensor *, std::vector<int32_t>>> positions_;  // ROPE's token positions
     std::vector<ggml_tensor *> outputs_;
     std::unordered_map<const ggml_tensor *, fvec> mem_;  // the CPU chain: root tensor -> its memory
 
@@ -231,6 +235,33 @@ private:
         w.deq = bfp16(w.deq, n, k);
     }
     ggml_type any_type() { return k_types[pick(10)]; }
+
+    ggml_tensor * last_proj_ = nullptr;
+    // p's rows as heads of 64 (or 32) through ROPE with random settings
+    void rope_heads(ggml_tensor * p, int b) {
+        const int64_t hd = p->ne[0] % 64 == 0 ? 64 : 32, heads = p->ne[0] / hd;
+        const int n_dims = (int) (coin(0.5) ? hd : hd / 2), mode = coin(0.5) ? GGML_ROPE_TYPE_NEOX : GGML_ROPE_TYPE_NORMAL;
+        const bool yarn = coin(0.5);
+        ggml_tensor * pos = ggml_new_tensor_1d(ctx_, GGML_TYPE_I32, T_);
+        name(pos, "pos%d", b);
+        std::vector<int32_t> pv((size_t) T_);
+        const int32_t p0 = (int32_t) pick(40000);
+        for (int64_t i = 0; i < T_; i++) pv[(size_t) i] = p0 + (int32_t) i;
+        positions_.emplace_back(pos, std::move(pv));
+        ggml_tensor * ff = nullptr;
+        if (coin(0.4)) {
+            ff = ggml_new_tensor_1d(ctx_, GGML_TYPE_F32, n_dims / 2);
+            name(ff, "freq_factors%d", b);
+            fvec v((size_t) (n_dims / 2));
+            for (float & f : v) f = (float) (1.0 + 3.0 * rng_.uniform());
+            leaves_.emplace_back(ff, std::move(v));
+        }
+        ggml_tensor * q3 = ggml_reshape_3d(ctx_, p, hd, heads, T_);
+        ggml_tensor * r = ggml_rope_ext(ctx_, q3, pos, ff, n_dims, mode, yarn ? 4096 : 0, 10000.0f, yarn ? 0.25f : 1.0f,
+                                        yarn ? 1.0f : 0.0f, 1.0f, 32.0f, 1.0f);
+        name(r, "rope%d", b);
+        output(r);
+    }
     ggml_type type_for(int64_t k) {
         for (;;) {
             const ggml_type t = any_type();
@@ -268,7 +299,9 @@ private:
             name(p, i == 0 ? "proj%d.0" : i == 1 ? "proj%d.1" : "proj%d.2", b);
             if (i == 0) first = p;
             if (i > 0 || !residual || coin(0.2)) output(p);
+            last_proj_ = p;
         }
+        if (coin(0.35)) rope_heads(last_proj_, b);
         if (residual) {
             x = coin(0.5) ? ggml_add(ctx_, first, x) : ggml_add(ctx_, x, first);
             name(x, "attn_out%d", b);
@@ -358,6 +391,8 @@ private:
 
     void cpu_chain(const ggml_cgraph * gf) {
         for (auto & [t, v] : leaves_) mem_[t] = v;
+        std::unordered_map<const ggml_tensor *, const std::vector<int32_t> *> pos_of;
+        for (auto & [t, v] : positions_) pos_of[t] = &v;
         for (int i = 0; i < gf->n_nodes; i++) {
             const ggml_tensor * n = gf->nodes[i];
             if (n->op == GGML_OP_NONE || n->op == GGML_OP_RESHAPE || n->op == GGML_OP_VIEW) continue;
@@ -401,6 +436,15 @@ private:
                         orc_glu(kind, a.data() + (swapped ? w : 0), 2 * w, a.data() + (swapped ? 0 : w), 2 * w, rows, w,
                                 y.data());
                     }
+                    break;
+                }
+                case GGML_OP_ROPE: {
+                    float fp[11];
+                    memcpy(fp, n->op_params, sizeof(fp));
+                    const fvec ff = n->src[2] ? value(n->src[2]) : fvec();
+                    orc_rope(value(n->src[0]).data(), n->ne[2], n->ne[1], n->ne[0], pos_of.at(n->src[1])->data(),
+                             n->src[2] ? ff.data() : nullptr, n->op_params[1], n->op_params[2], n->op_params[4], fp[5],
+                             fp[6], fp[7], fp[8], fp[9], fp[10], y.data());
                     break;
                 }
                 default: test_check(false, "cpu chain: unexpected op %d", (int) n->op); return;
