@@ -3,7 +3,8 @@ against zest_gemm_group: the same plan, so the same bits, on two calls in a
 row (the second smaller, so the static workspace holds the first call's
 partial sums when it starts), both within the GEMM bar of the oracle; no
 device memory is allocated by the calls; a plan that needs more workspace than
-the static array holds is refused before anything runs."""
+the static array holds is refused before anything runs; captured in a HIP
+graph, every replay gives the same bits."""
 from __future__ import annotations
 
 import numpy as np
@@ -105,3 +106,34 @@ def test_noalloc_random_shapes(zest_gpu):
             continue
         torch.cuda.synchronize()
         assert torch.equal(got.view(torch.int32), want.view(torch.int32)), (M, N, K)
+
+
+def test_noalloc_under_graph_capture(zest_gpu):
+    # the callers it is for: the no-alloc GEMM captured in a HIP graph (a
+    # split-K plan, so the graph holds the kernel that clears the static
+    # counters, not a memset), replayed three times with eager work between
+    # the replays (the output poisoned); every replay gives the eager
+    # allocating call's bits
+    import torch
+    z = zest_gpu
+    M, ns, K = 2048, [2432], 9728
+    a, ws = _case(z, M, ns, K, 5)
+    want = z.gemm_group(a, M, ws, ns, K)[0].clone()
+    out = torch.empty((M, ns[0]), device="cuda")
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        z.gemm_group(a, M, ws, ns, K, outs=[out], noalloc=True)   # the device's array looked up before capture
+    s.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        z.gemm_group(a, M, ws, ns, K, outs=[out], noalloc=True)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int32), want.view(torch.int32)), rep
+        # eager work on the same array between replays
+        z.gemm_group(a, 600, ws, ns, K, outs=[torch.empty((600, ns[0]), device="cuda")], noalloc=True)
+        torch.cuda.synchronize()
