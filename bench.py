@@ -18,6 +18,7 @@ a bounded sample.
 
     python bench.py [--steps K] [--warmup W] [--workload qwen3-4b] [--chunk M] [--no-cpu]
     python bench.py --hbm      # converter (every GGUF type) and pack HBM rates
+    python bench.py --kernel-configs   # BASELINE configs 1 and 2, launch by launch
 
 The roofline's `traffic` (HBM bytes per GEMM launch) comes from two
 rocprofv3 counter runs of this script's probe mode, summarised into
@@ -277,6 +278,68 @@ def operand_activity(args) -> int:
         print(json.dumps({"shape": [m, n, k], "cases": res}), flush=True)
     return 0
 
+
+def kernel_configs(args) -> int:
+    """BASELINE configs[0] and [1] on one GPU, inputs and converted weights
+    resident, HIP events around back-to-back repetitions after one warm call:
+    config 1, one MUL_MAT 1024 x 2560 x 2560 with a Q8_0 weight (the
+    activation pack, then the GEMM); config 2, the SwiGLU FFN triple at 2048
+    tokens with 1% of the K-channels scaled x20 and Q4_K weights (the pack, the
+    fused gate/up GEMM that computes the SwiGLU and packs it in its epilogue,
+    the down GEMM). One JSON line per config: each launch alone, the chain back
+    to back, TFLOP/s and % of the bf16 peak, and the weights' one-time
+    conversion."""
+    import torch
+    z = load_pkg()
+    import ggml_xdna_amd.quant as quant
+    torch.cuda.set_device(0)
+    z.init(0)
+    g = torch.Generator(device="cuda").manual_seed(0)
+
+    def tf(flops, us):
+        return {"us": round(us, 2), "TFLOP/s": round(flops / us / 1e6, 1), "pct_peak": round(flops / us / 1e6 / BF16_PEAK * 100, 2)}
+
+    # config 1
+    M, N, K = 1024, 2560, 2560
+    x = torch.randn((M, K), device="cuda", generator=g)
+    raw = quant.quantize(8, torch.randn((N, K), device="cuda", generator=g) * 0.02)
+    w = z.empty_packed(N, K)
+    conv = _timed(lambda i: z.convert_weight(8, raw, N, K, out=w), 20)
+    a = z.empty_act(M, K)
+    c = torch.empty((M, N), device="cuda")
+    fl = 2.0 * M * N * K
+    pack = _timed(lambda i: z.pack_act_x(x, out=a), KCONFIG_REPS)
+    gemm = _timed(lambda i: z.gemm(a, M, w, N, K, out=c), KCONFIG_REPS)
+    both = _timed(lambda i: (z.pack_act_x(x, out=a), z.gemm(a, M, w, N, K, out=c)), KCONFIG_REPS)
+    print(json.dumps({"config": 1, "shape": [M, N, K], "weight": "Q8_0", "gemm": tf(fl, gemm),
+                      "pack_us": round(pack, 2), "pack_and_gemm": tf(fl, both), "convert_us": round(conv, 2)}), flush=True)
+
+    # config 2
+    M, D, F = 2048, 2560, 9728
+    x = torch.randn((M, D), device="cuda", generator=g)
+    ch = torch.randperm(D, generator=g, device="cuda")[: D // 100]
+    x[:, ch] *= 20.0
+    gate, up, down = (quant.quantize(12, torch.randn(shape, device="cuda", generator=g) * 0.02)
+                      for shape in ((F, D), (F, D), (D, F)))
+    wgu, wd = z.empty_packed(2 * F, D), z.empty_packed(D, F)
+    conv_gu = _timed(lambda i: z.convert_weight_gu(12, gate, up, F, D, out=wgu), 10)
+    conv_d = _timed(lambda i: z.convert_weight(12, down, D, F, out=wd), 10)
+    a, h = z.empty_act(M, D), z.empty_act(M, F)
+    y = torch.empty((M, D), device="cuda")
+    fl_gu, fl_d = 4.0 * M * F * D, 2.0 * M * D * F
+    pack = _timed(lambda i: z.pack_act_x(x, out=a), KCONFIG_REPS)
+    glu = _timed(lambda i: z.gemm_glu(z.GLU_SWIGLU, a, M, wgu, F, D, xout=h), KCONFIG_REPS)
+    dn = _timed(lambda i: z.gemm(h, M, wd, D, F, out=y), KCONFIG_REPS)
+    chain = _timed(lambda i: (z.pack_act_x(x, out=a), z.gemm_glu(z.GLU_SWIGLU, a, M, wgu, F, D, xout=h),
+                              z.gemm(h, M, wd, D, F, out=y)), KCONFIG_REPS)
+    print(json.dumps({"config": 2, "tokens": M, "hidden": D, "ffn": F, "weight": "Q4_K", "outliers": "1% of K x20",
+                      "gate_up_glu": tf(fl_gu, glu), "down": tf(fl_d, dn), "pack_us": round(pack, 2),
+                      "triple": tf(fl_gu + fl_d, chain), "convert_gate_up_us": round(conv_gu, 2),
+                      "convert_down_us": round(conv_d, 2)}), flush=True)
+    return 0
+
+
+KCONFIG_REPS = 50
 
 ACTIVITY_SHAPES = ((8192, 8192, 8192), (2048, 19456, 2560), (2048, 2560, 9728))
 ACTIVITY_CASES = ("random bytes", "workload data", "W mantissas zero", "A zero", "workload data again")
@@ -597,6 +660,8 @@ def main() -> int:
     ap.add_argument("--traffic-probe", action="store_true", help="one step and the calibration kernel, for rocprofv3")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
     ap.add_argument("--hbm", action="store_true", help="HBM rates of the converter (every type) and the pack")
+    ap.add_argument("--kernel-configs", action="store_true",
+                    help="BASELINE configs 1 and 2: one Q8_0 MUL_MAT and the SwiGLU FFN triple, launch by launch")
     ap.add_argument("--operand-activity", action="store_true",
                     help="the same GEMM launches on random, workload and all-zero operands (power sensitivity)")
     ap.add_argument("--activity-summary", nargs=2, metavar=("PMC_DIR", "TRACE_DIR"),
@@ -610,6 +675,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.hbm:
         return hbm_kernels(args)
+    if args.kernel_configs:
+        return kernel_configs(args)
     if args.operand_activity:
         return operand_activity(args)
     if args.activity_summary:
