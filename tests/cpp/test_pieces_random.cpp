@@ -3,8 +3,9 @@
 // weight types. Each case draws one or two blocks of
 //   a norm (RMS_NORM with its scale row, RMS_NORM alone, the scale row
 //   multiplied in place, or none) -> one to three matmuls on its result (a
-//   group), sometimes through a reshape, sometimes a residual ADD of the
-//   first with the matmul on either side, sometimes one of them taken as
+//   group), sometimes through a reshape, sometimes a bias row added to one,
+//   sometimes a residual ADD of the first with the matmul on either side,
+//   sometimes one of them taken as
 //   heads through ROPE (normal or NeoX, partial, YaRN, frequency factors),
 //   sometimes a matmul over a range of rows, sometimes the norm's result
 //   scaled in place and multiplied again ->
@@ -297,6 +298,14 @@ private:
             const int64_t n = i == 0 && residual ? D_ : widths[pick(5)];
             ggml_tensor * p = ggml_mul_mat(ctx_, new_weight(D_, n, type_for(D_), b), hin);
             name(p, i == 0 ? "proj%d.0" : i == 1 ? "proj%d.1" : "proj%d.2", b);
+            if (i > 0 && coin(0.3)) {
+                // a bias row added to every row of the projection (q/k/v biases)
+                ggml_tensor * bias = ggml_new_tensor_1d(ctx_, GGML_TYPE_F32, n);
+                name(bias, i == 1 ? "bias%d.1" : "bias%d.2", b);
+                leaf(bias, 0.5f, 0.0f);
+                p = ggml_add(ctx_, p, bias);
+                name(p, i == 1 ? "proj%d.1+bias" : "proj%d.2+bias", b);
+            }
             if (i == 0) first = p;
             if (i > 0 || !residual || coin(0.2)) output(p);
             last_proj_ = p;
@@ -415,7 +424,12 @@ private:
                     break;
                 }
                 case GGML_OP_MUL: orc_mul_row(value(n->src[0]).data(), rows, w, value(n->src[1]).data(), y.data()); break;
-                case GGML_OP_ADD: orc_add(value(n->src[0]).data(), value(n->src[1]).data(), w * rows, y.data()); break;
+                case GGML_OP_ADD:
+                    if (ggml_nelements(n->src[1]) == w)  // a bias row
+                        orc_add_row(value(n->src[0]).data(), rows, w, value(n->src[1]).data(), y.data());
+                    else
+                        orc_add(value(n->src[0]).data(), value(n->src[1]).data(), w * rows, y.data());
+                    break;
                 case GGML_OP_SCALE: {
                     float s, b;
                     memcpy(&s, &n->op_params[0], sizeof(s));
