@@ -392,6 +392,54 @@ SUSTAIN_SHAPE = (2048, 19456, 2560)  # the fused gate/up's GEMM at 2048 tokens, 
 SUSTAIN_CASES = ("workload data", "W mantissas zero", "random bytes")
 
 
+def sustain_kinds(args) -> int:
+    """The qwen3-4b stack's four GEMM launch kinds at 2048 tokens (the q/k/v
+    group, O + residual, the fused gate/up with its SwiGLU, down + residual),
+    each back to back for `args.sustain_kinds` seconds on the workload's kind
+    of data after two idle seconds, for sampling the board's power and clock
+    beside it. One JSON line per phase, as --sustain prints them."""
+    import time
+    import torch
+    z = load_pkg()
+    import ggml_xdna_amd.quant as quant
+    torch.cuda.set_device(0)
+    z.init(0)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    M, H, Q, KV, F = 2048, 2560, 4096, 1024, 9728
+
+    def weight(t, n, k):
+        return z.convert_weight(t, quant.quantize(t, torch.randn((n, k), device="cuda", generator=g) * 0.02), n, k)
+
+    a, ao, ad = (z.pack_act_x(torch.randn((M, k), device="cuda", generator=g)) for k in (H, Q, F))
+    wq, wk, wv, wo, wd = weight(12, Q, H), weight(12, KV, H), weight(12, KV, H), weight(8, H, Q), weight(8, H, F)
+    gate, up = (quant.quantize(12, torch.randn((F, H), device="cuda", generator=g) * 0.02) for _ in range(2))
+    wgu = z.convert_weight_gu(12, gate, up, F, H)
+    qo, ko, vo = torch.empty((M, Q), device="cuda"), torch.empty((M, KV), device="cuda"), torch.empty((M, KV), device="cuda")
+    h = torch.randn((M, H), device="cuda", generator=g)
+    xo = z.empty_act(M, F)
+    kinds = {
+        "qkv": (lambda: z.gemm_group(a, M, [wq, wk, wv], [Q, KV, KV], H, outs=[qo, ko, vo]), 2.0 * M * (Q + 2 * KV) * H),
+        "o": (lambda: z.gemm_residual(ao, M, wo, H, Q, h, out=h), 2.0 * M * H * Q),
+        "gate_up": (lambda: z.gemm_glu(z.GLU_SWIGLU, a, M, wgu, F, H, xout=xo), 4.0 * M * F * H),
+        "down": (lambda: z.gemm_residual(ad, M, wd, H, F, h, out=h), 2.0 * M * H * F),
+    }
+    for name, (fn, flops) in kinds.items():
+        torch.cuda.synchronize()
+        t = time.time()
+        time.sleep(2.0)
+        print(json.dumps({"phase": "idle", "t0": t, "t1": time.time()}), flush=True)
+        t0, launches = time.time(), 0
+        while time.time() - t0 < args.sustain_kinds:
+            for _ in range(20):
+                fn()
+            launches += 20
+            torch.cuda.synchronize()
+        t1 = time.time()
+        print(json.dumps({"phase": name, "t0": t0, "t1": t1, "launches": launches,
+                          "TFLOP/s": round(flops * launches / (t1 - t0) / 1e12, 1)}), flush=True)
+    return 0
+
+
 def sustain(args) -> int:
     """The same GEMM launch, back to back for `args.sustain` seconds per
     operand case (the cases of --operand-activity), each after two idle
@@ -668,6 +716,8 @@ def main() -> int:
                     help="clock and MFMA busy per case from rocprofv3 runs of --operand-activity")
     ap.add_argument("--sustain", type=float, default=None, metavar="SECONDS",
                     help="one GEMM back to back for SECONDS per operand case, for sampling power beside it")
+    ap.add_argument("--sustain-kinds", type=float, default=None, metavar="SECONDS",
+                    help="the stack's four GEMM launch kinds back to back for SECONDS each, for sampling power")
     ap.add_argument("--sustain-summary", nargs=2, metavar=("PHASES_LOG", "SMI_LOG"),
                     help="power, clock and power-cap status per --sustain phase from amd-smi samples")
     ap.add_argument("--counter-summary", nargs=4, metavar=("MFMA_DIR", "FETCH_DIR", "WRITE_DIR", "TRACE_DIR"),
@@ -683,6 +733,8 @@ def main() -> int:
         return activity_summary(*args.activity_summary)
     if args.sustain is not None:
         return sustain(args)
+    if args.sustain_kinds is not None:
+        return sustain_kinds(args)
     if args.sustain_summary:
         return sustain_summary(*args.sustain_summary)
     if args.counter_summary:
