@@ -23,6 +23,12 @@
 // reuses its plan of it): the same bits; and once more after one of its
 // weights is rewritten with new values (its cache entries must go).
 //
+// Every sixth case is model-sized: config 3's shapes (2048 or 1537 tokens,
+// hidden 2560, projections of 4096, 1024 and 2560 rows, an FFN of 9728) in
+// one block. Every op here is row-local, so for those the CPU chain runs on 16
+// sampled token rows (the first, the last and 14 others) and the outputs are
+// compared on those rows.
+//
 // Bars: nrmse <= 5e-3 over each output and <= 5e-2 over each of its rows.
 // Only fp32 rounding differs between the two chains, but every matmul input
 // is packed again to 8-bit mantissas, so a rounding difference that moves a
@@ -78,7 +84,7 @@ bool super_blocks(ggml_type t) {
 // One case: its graph, the values of its leaves, and what it expects.
 class random_piece {
 public:
-    random_piece(uint64_t seed) : rng_(seed) {
+    random_piece(uint64_t seed, bool big = false) : rng_(seed), big_(big) {
         ggml_init_params ip = {ggml_tensor_overhead() * 256 + ggml_graph_overhead(), nullptr, true};
         wctx_ = ggml_init(ip);
         ictx_ = ggml_init(ip);
@@ -97,17 +103,27 @@ public:
 
     void build() {
         static const int64_t tokens[] = {1, 3, 17, 64, 100, 255, 256, 257, 513, 1000, 1024, 1100, 1500};
-        T_ = tokens[pick(13)];
-        D_ = pick(2) ? 512 : 256;
+        T_ = big_ ? (pick(2) ? 2048 : 1537) : tokens[pick(13)];
+        D_ = big_ ? 2560 : pick(2) ? 512 : 256;
         host_input_ = coin(0.3);
+        if (big_) {
+            std::vector<int64_t> rows{0, T_ - 1};
+            while (rows.size() < 16) {
+                const int64_t r = 1 + pick((int) T_ - 2);
+                if (std::find(rows.begin(), rows.end(), r) == rows.end()) rows.push_back(r);
+            }
+            std::sort(rows.begin(), rows.end());
+            sample_ = rows;
+        }
         char buf[96];
-        snprintf(buf, sizeof(buf), "T=%lld D=%lld%s", (long long) T_, (long long) D_, host_input_ ? " x on host" : "");
+        snprintf(buf, sizeof(buf), "T=%lld D=%lld%s%s", (long long) T_, (long long) D_, host_input_ ? " x on host" : "",
+                 big_ ? " (model-sized, 16 rows checked)" : "");
         describe = buf;
         ggml_tensor * cur = ggml_new_tensor_2d(ictx_, GGML_TYPE_F32, D_, T_);
         ggml_set_name(cur, "x");
         ggml_set_input(cur);
         leaf(cur, 1.0f, 0.0f);
-        const int blocks = 1 + pick(2);
+        const int blocks = big_ ? 1 : 1 + pick(2);
         for (int b = 0; b < blocks; b++) cur = block(b, cur);
         output(cur);
     }
@@ -148,6 +164,39 @@ public:
         return check(gf, after, nullptr) && ok;
     }
 
+    // The CPU chain on every row, then on four token rows (cases without a
+    // row-range view, whose offsets the sampled chain does not follow): the
+    // same values on those rows. Tensors in host memory, nothing computed on
+    // a device.
+    bool self_check(ggml_backend_buffer_type_t host, int & checked) {
+        if (T_ < 8) return true;
+        wbuf_ = ggml_backend_alloc_ctx_tensors_from_buft(wctx_, host);
+        ibuf_ = ggml_backend_alloc_ctx_tensors_from_buft(ictx_, host);
+        abuf_ = ggml_backend_alloc_ctx_tensors_from_buft(ctx_, host);
+        ggml_cgraph * gf = ggml_new_graph(ctx_);
+        for (ggml_tensor * t : outputs_) ggml_build_forward_expand(gf, t);
+        for (int i = 0; i < gf->n_nodes; i++)
+            if (gf->nodes[i]->op == GGML_OP_VIEW) return true;
+        mem_.clear();
+        cpu_chain(gf);
+        const std::unordered_map<const ggml_tensor *, fvec> full = mem_;
+        sample_ = {0, 2, 5, T_ - 1};
+        mem_.clear();
+        cpu_chain(gf);
+        for (ggml_tensor * t : outputs_) {
+            const fvec & a = full.at(root(t)), & b = mem_.at(root(t));
+            const int64_t w = t->ne[0], per = ggml_nrows(t) / T_;
+            for (int64_t r = 0; r < rows_of(t); r++) {
+                const int64_t g = sample_[(size_t) (r / per)] * per + r % per;
+                if (memcmp(&a[(size_t) (g * w)], &b[(size_t) (r * w)], (size_t) w * sizeof(float)) != 0)
+                    return test_check(false, "%s: %s row %lld of the sampled chain differs", describe.c_str(), t->name,
+                                      (long long) r);
+            }
+            checked++;
+        }
+        return true;
+    }
+
     // every output against the CPU chain; the GPU's values kept in `got_all`
     bool check(const ggml_cgraph * gf, const char * when, std::vector<fvec> * got_all) {
         mem_.clear();
@@ -159,11 +208,13 @@ public:
             if (got_all) got_all->push_back(got);
             const fvec & want = mem_.at(root(t));
             double se = 0, ss = 0, worst_row = 0;
-            const int64_t w = t->ne[0];
-            for (int64_t r = 0; r < ggml_nrows(t); r++) {
+            const int64_t w = t->ne[0], per_token = ggml_nrows(t) / T_;
+            for (int64_t r = 0; r < rows_of(t); r++) {
+                // row r of the chain's rows: its token's row in the GPU's output
+                const int64_t g = sample_.empty() ? r : sample_[(size_t) (r / per_token)] * per_token + r % per_token;
                 double rse = 0, rss = 0;
                 for (int64_t c = 0; c < w; c++) {
-                    const double d = (double) got[r * w + c] - want[r * w + c];
+                    const double d = (double) got[g * w + c] - want[r * w + c];
                     rse += d * d;
                     rss += (double) want[r * w + c] * want[r * w + c];
                 }
@@ -184,6 +235,22 @@ private:
     ggml_backend_buffer_t wbuf_ = nullptr, ibuf_ = nullptr, abuf_ = nullptr;
     int64_t T_ = 0, D_ = 0;
     bool host_input_ = false;
+    bool big_ = false;
+    std::vector<int64_t> sample_;  // model-sized cases: the token rows the CPU chain computes
+
+    // rows of t the CPU chain holds: all, or its rows of the sampled tokens
+    int64_t rows_of(const ggml_tensor * t) const {
+        return sample_.empty() ? ggml_nrows(t) : ggml_nrows(t) / T_ * (int64_t) sample_.size();
+    }
+    // a leaf's values on the sampled tokens: per = values per token (the
+    // width of [w x T] rows, 1 for ROPE's positions); parameters stay whole
+    template <class V>
+    V sampled(const V & v, int64_t per) const {
+        if (sample_.empty() || per == 0) return v;
+        V out;
+        for (int64_t tok : sample_) out.insert(out.end(), v.begin() + tok * per, v.begin() + (tok + 1) * per);
+        return out;
+    }
     int n_weights_ = 0;
     std::deque<weight> weights_;
     std::unordered_map<const ggml_tensor *, const weight *> weight_of_;
@@ -290,12 +357,12 @@ private:
         ggml_tensor * h = norm(x, b);
         const bool h_is_leaf = root(h)->op == GGML_OP_NONE;  // the graph's input: never written
         ggml_tensor * hin = coin(0.3) ? ggml_reshape_2d(ctx_, h, D_, T_) : h;
-        static const int64_t widths[] = {32, 64, 96, 160, 256};
+        static const int64_t widths[] = {32, 64, 96, 160, 256}, big_widths[] = {4096, 1024, 1024, 2560, 64};
         const int nproj = 1 + pick(3);
         const bool residual = coin(0.5);
         ggml_tensor * first = nullptr;
         for (int i = 0; i < nproj; i++) {
-            const int64_t n = i == 0 && residual ? D_ : widths[pick(5)];
+            const int64_t n = i == 0 && residual ? D_ : big_ ? big_widths[pick(5)] : widths[pick(5)];
             ggml_tensor * p = ggml_mul_mat(ctx_, new_weight(D_, n, type_for(D_), b), hin);
             name(p, i == 0 ? "proj%d.0" : i == 1 ? "proj%d.1" : "proj%d.2", b);
             if (i > 0 && coin(0.3)) {
@@ -323,7 +390,7 @@ private:
             name(e, "after_inplace%d", b);
             output(e);
         }
-        if (T_ > 4 && coin(0.25)) {
+        if (!big_ && T_ > 4 && coin(0.25)) {
             // a matmul over a range of the norm's rows
             const int64_t r0 = 1 + pick((int) (T_ / 2)), r1 = r0 + 1 + pick((int) (T_ - r0 - 1));
             ggml_tensor * v = ggml_view_2d(ctx_, h, D_, r1 - r0, h->nb[1], (size_t) r0 * h->nb[1]);
@@ -335,7 +402,7 @@ private:
         // the FFN: gate/up, a GLU, the down projection, the residual
         ggml_tensor * h2 = norm(x, b + 10);
         const ggml_type gt = type_for(D_), dt = any_type();
-        const int64_t F = super_blocks(dt) ? 256 * (1 + pick(3)) : 32 * (1 + pick(24));
+        const int64_t F = big_ ? 9728 : super_blocks(dt) ? 256 * (1 + pick(3)) : 32 * (1 + pick(24));
         static const ggml_glu_op kinds[] = {GGML_GLU_OP_SWIGLU, GGML_GLU_OP_GEGLU, GGML_GLU_OP_REGLU,
                                             GGML_GLU_OP_GEGLU_ERF, GGML_GLU_OP_GEGLU_QUICK};
         const ggml_glu_op kind = kinds[pick(5)];
@@ -399,13 +466,13 @@ private:
     }
 
     void cpu_chain(const ggml_cgraph * gf) {
-        for (auto & [t, v] : leaves_) mem_[t] = v;
-        std::unordered_map<const ggml_tensor *, const std::vector<int32_t> *> pos_of;
-        for (auto & [t, v] : positions_) pos_of[t] = &v;
+        for (auto & [t, v] : leaves_) mem_[t] = sampled(v, t->ne[1] == T_ && ggml_nrows(t) == T_ ? t->ne[0] : 0);
+        std::unordered_map<const ggml_tensor *, std::vector<int32_t>> pos_of;
+        for (auto & [t, v] : positions_) pos_of[t] = sampled(v, 1);
         for (int i = 0; i < gf->n_nodes; i++) {
             const ggml_tensor * n = gf->nodes[i];
             if (n->op == GGML_OP_NONE || n->op == GGML_OP_RESHAPE || n->op == GGML_OP_VIEW) continue;
-            const int64_t w = n->ne[0], rows = ggml_nrows(n);
+            const int64_t w = n->ne[0], rows = rows_of(n);
             fvec y((size_t) (w * rows));
             switch (n->op) {
                 case GGML_OP_MUL_MAT: {
@@ -456,7 +523,7 @@ private:
                     float fp[11];
                     memcpy(fp, n->op_params, sizeof(fp));
                     const fvec ff = n->src[2] ? value(n->src[2]) : fvec();
-                    orc_rope(value(n->src[0]).data(), n->ne[2], n->ne[1], n->ne[0], pos_of.at(n->src[1])->data(),
+                    orc_rope(value(n->src[0]).data(), rows / n->ne[1], n->ne[1], n->ne[0], pos_of.at(n->src[1]).data(),
                              n->src[2] ? ff.data() : nullptr, n->op_params[1], n->op_params[2], n->op_params[4], fp[5],
                              fp[6], fp[7], fp[8], fp[9], fp[10], y.data());
                     break;
@@ -470,12 +537,32 @@ private:
 
 }  // namespace
 
+// The checker's own check, with no GPU: on ordinary cases (tensors in host
+// memory), the CPU chain restricted to a few token rows gives exactly the
+// full chain's values on those rows, as the model-sized cases assume.
+static int self_check(int cases, uint64_t seed0) {
+    int checked = 0;
+    ggml_backend_buffer_type_t host = ggml_backend_dev_buffer_type(ggml_backend_dev_by_type(GGML_BACKEND_DEVICE_TYPE_CPU));
+    for (int c = 0; c < cases; c++) {
+        random_piece p(seed0 + (uint64_t) c);
+        p.build();
+        if (!p.self_check(host, checked)) return 1;
+    }
+    printf("self-check: %d outputs, sampled rows equal to the full chain's\n", checked);
+    printf("%s\n", checked > 0 && !test_failures() ? "ALL PASS" : "FAILED");
+    return checked > 0 && !test_failures() ? 0 : 1;
+}
+
 // test_pieces_random [CASES [SEED [THREADS]]]: with THREADS > 1, each thread
 // runs CASES cases of its own (seeds SEED + 1000 t + c) on a backend of its
 // own, all at once, as llama.cpp contexts on several threads do: they share
 // the library, the gate's reader log and the budget, and every write of a
 // tensor looks through every context's weight cache.
 int main(int argc, char ** argv) {
+    if (argc > 1 && strcmp(argv[1], "--self-check") == 0) {
+        ggml_backend_load_all();
+        return self_check(60, 1000);
+    }
     const int cases = argc > 1 ? atoi(argv[1]) : 24;
     const uint64_t seed0 = argc > 2 ? strtoull(argv[2], nullptr, 10) : 1000;
     const int threads = argc > 3 ? std::max(1, atoi(argv[3])) : 1;
@@ -496,7 +583,7 @@ int main(int argc, char ** argv) {
     auto work = [&](int t) {
         for (int c = 0; c < cases; c++) {
             const uint64_t seed = seed0 + 1000 * (uint64_t) t + (uint64_t) c;
-            random_piece p(seed);
+            random_piece p(seed, c % 6 == 5);
             p.build();
             printf("thread %d case %d (seed %llu): %s\n", t, c, (unsigned long long) seed, p.describe.c_str());
             fflush(stdout);

@@ -61,6 +61,13 @@ def test_two_contexts_on_threads_planning():
     run("test_contexts", GGML_XDNA_PLAN_ONLY="1", GGML_XDNA_MAX_COPY_GB="0.05")
 
 
+def test_random_pieces_checker_self_check():
+    # the random-piece test's CPU chain on sampled token rows (how it checks
+    # its model-sized cases) equals the full chain on those rows; no GPU
+    out = run("test_pieces_random", "--self-check", GGML_XDNA_PLAN_ONLY="1")
+    assert "sampled rows equal" in out
+
+
 def test_host_code_under_sanitizers():
     # the host side rebuilt with ThreadSanitizer and with AddressSanitizer +
     # UBSan (tests/cpp/Makefile, `sanitize`), the gate, budget, safe-start and
